@@ -1,0 +1,250 @@
+"""Benchmark of the INT8 quantized-inference path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+
+Headline (`value`): configs[1] of BASELINE.json -- the fused W8A8 linear at M=N=K=4096
+(FP16 activations with 8 outlier channels x20, per-token quantize, INT8 MFMA GEMM with
+INT32 accumulation, dequant + bias to FP16). One step = one forge_int8_linear call
+(quantize kernel + GEMM kernel) on inputs already resident in HBM. value = 2*M*N*K / t.
+
+roofline: the dominant kernel (the GEMM) timed alone with HIP events on the launch stream,
+algorithmic ops 2*M*N*K per launch against MI355X's dense INT8 peak (5.0 POP/s).
+cpu_baseline: the oracle's single-threaded INT32 loop + dequant epilogue (oracle/) on a
+bounded slice of rows of the same workload, timed on this host.
+extra: configs[2] (2:4 sparse vs dense at 4096x11008x4096) and configs[3] (decode
+M = 1/4/16, N = K = 8192, dense and 2:4, HBM GB/s with >= 5 rotating weight copies so
+the 256 MB MALL cannot hold them).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "INT8 dense/2:4-sparse GEMM TOPS @4096^3 (% MFMA peak); M=16 HBM GB/s"
+PEAK_INT8_TOPS = 5000.0      # MI355X dense INT8 MFMA, 5.0 POP/s
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
+
+
+def events_time_ms(fn, reps: int) -> float:
+    """Average duration of fn() over reps launches, HIP events on torch's current stream
+    (the stream the library launches on)."""
+    import torch
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def make_c2(dev, seed=2):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    M = N = K = 4096
+    x = torch.randn((M, K), generator=g, device=dev, dtype=torch.float32)
+    cols = torch.randperm(K, generator=g, device=dev)[:8]
+    x[:, cols] *= 20
+    x = x.half()
+    W = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+    ws = (torch.rand((N,), generator=g, device=dev) * 9e-3 + 1e-3).half()
+    b = (torch.randn((N,), generator=g, device=dev) * 0.1).half()
+    return x, W, ws, b
+
+
+def cpu_baseline(target_s: float = 10.0):
+    """Single-threaded oracle INT32 GEMM + dequant on a slice of configs[1] rows."""
+    from oracle import oracle
+    oracle.build()
+    rng = np.random.default_rng(2)
+    K = N = 4096
+    W = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    x = rng.standard_normal((256, K), dtype=np.float32)
+    x[:, rng.choice(K, 8, replace=False)] *= 20
+    q, s = oracle.quantize_rows(x.astype(np.float16))
+    ws = rng.uniform(1e-3, 1e-2, N).astype(np.float16)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float16)
+    rows = 4
+    t, _ = oracle.time_gemm_dequant_rows(q, W, s, ws, b, rows)
+    rows = int(max(4, min(256, target_s / max(t, 1e-6) * rows)))
+    t, _ = oracle.time_gemm_dequant_rows(q, W, s, ws, b, rows)
+    tops = 2.0 * rows * N * K / t / 1e12
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": tops, "unit": "TOPS", "cores": 1, "kind": "port",
+            "sample": f"oracle INT32 loop + dequant epilogue, rows 0..{rows - 1} of configs[1] "
+                      f"(N=K=4096), {t:.2f} s, g++ -O3 single thread, host CPU '{model}'"}
+
+
+def bench_extra(dev):
+    import torch
+    from forge_amd import ops
+    out = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    # 2:4 sparse 4096 x 11008 x 4096 INT32 out, and the same shape dense
+    M, K, N = 4096, 4096, 11008
+    W = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+    x = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+    comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+    raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+    meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+    ops.prune_compress_24(W, comp, raw, N, K)
+    ops.pack_metadata(raw, meta, N, K)
+    C = torch.empty((M, N), dtype=torch.int32, device=dev)
+    for _ in range(3):
+        ops.sparse_int8_gemm_s32(comp, x, meta, out=C)
+        ops.int8_gemm_s32(x, W, out=C)
+    t_sp = events_time_ms(lambda: ops.sparse_int8_gemm_s32(comp, x, meta, out=C), 10)
+    t_de = events_time_ms(lambda: ops.int8_gemm_s32(x, W, out=C), 10)
+    ops_ = 2.0 * M * N * K
+    out["c3_sparse_tops"] = ops_ / t_sp / 1e9
+    out["c3_dense_tops"] = ops_ / t_de / 1e9
+    out["c3_sparse_over_dense"] = t_de / t_sp
+    del W, x, comp, raw, meta, C
+    torch.cuda.empty_cache()
+
+    # decode, N = K = 8192, 6 rotating weight copies (384 MB dense)
+    N = K = 8192
+    copies = 6
+    Ws = [torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8) for _ in range(copies)]
+    comps, metas = [], []
+    for Wc in Ws:
+        cp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+        rw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+        mt = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+        ops.prune_compress_24(Wc, cp, rw, N, K)
+        ops.pack_metadata(rw, mt, N, K)
+        comps.append(cp)
+        metas.append(mt)
+    ws = (torch.rand((N,), generator=g, device=dev) * 9e-3 + 1e-3).half()
+    b = (torch.randn((N,), generator=g, device=dev) * 0.1).half()
+    for M in (1, 4, 16):
+        xh = torch.randn((M, K), generator=g, device=dev).half()
+        sq = torch.empty((M, K), dtype=torch.int8, device=dev)
+        ss = torch.empty((M,), dtype=torch.float32, device=dev)
+        i = [0]
+
+        def dense():
+            ops.int8_linear(xh, Ws[i[0] % copies], ws, b, sq, ss)
+            i[0] += 1
+
+        def sparse():
+            ops.sparse_int8_linear(xh, comps[i[0] % copies], metas[i[0] % copies], ws, b, sq, ss)
+            i[0] += 1
+        for _ in range(copies):
+            dense()
+            sparse()
+        td = events_time_ms(dense, 6 * copies)
+        ts = events_time_ms(sparse, 6 * copies)
+        bytes_d = N * K + M * K * 2 + M * N * 2 + N * 2 + N * 2
+        bytes_s = N * K // 2 + N * K // 8 + M * K * 2 + M * N * 2 + N * 2 + N * 2
+        out[f"c4_M{M}_dense_GBs"] = bytes_d / td / 1e6
+        out[f"c4_M{M}_sparse_GBs"] = bytes_s / ts / 1e6
+        out[f"c4_M{M}_dense_us"] = td * 1e3
+        out[f"c4_M{M}_sparse_us"] = ts * 1e3
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the W8A8 kernels shard by rows or columns with no communication; see DESIGN.md).",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    import forge_amd
+    from forge_amd import ops
+    forge_amd.load()
+    dev = torch.device("cuda:0")
+    x, W, ws, b = make_c2(dev)
+    M, K = x.shape
+    N = W.shape[0]
+    sq = torch.empty((M, K), dtype=torch.int8, device=dev)
+    ss = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = torch.empty((M, N), dtype=torch.float16, device=dev)
+
+    def step():
+        ops.int8_linear(x, W, ws, b, sq, ss)
+
+    # spin to clocks, then warm up
+    t_end = time.time() + 1.0
+    while time.time() < t_end:
+        for _ in range(20):
+            step()
+        torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / args.steps
+    tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+
+    # dominant kernel alone: the dequantizing GEMM on the quantized activations
+    gemm = lambda: ops.int8_gemm_dequant(sq, W, ss, ws, b, out=y)
+    for _ in range(5):
+        gemm()
+    t_gemm = events_time_ms(gemm, 50)
+    achieved = 2.0 * M * N * K / (t_gemm * 1e-3) / 1e12
+    quant = lambda: ops.fused_quantize_activation(x, M, K)
+    t_q = events_time_ms(quant, 50)
+
+    line = {
+        "metric": METRIC,
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (configs[1]: N(0,1) fp16 activations with 8 outlier channels x20, "
+                "uniform int8 weights, random fp16 scales and bias)",
+        "config": {"workload": "configs[1] fused W8A8 linear, M=N=K=4096, fp16 in/out",
+                   "M": M, "N": N, "K": K, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
+                     "kernel": "gemm_tile_kernel<256,256,2,2,dequant>", "kernel_ms": round(t_gemm, 5),
+                     "quantize_ms": round(t_q, 5)},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    if not args.no_extra:
+        line["extra"] = {k: round(v, 3) for k, v in bench_extra(dev).items()}
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,17 @@
+"""forge_amd: the reference's INT8 quantized-inference path (forge::quant, forge::gemm,
+forge::sparsity, forge::nn int8 conv) as a gfx950-native HIP library.
+
+The product is libforge_amd.so (C-ABI in include/forge_amd.h, C++ API in
+include/forge/). This package builds it (forge_amd.build), binds it with ctypes
+(forge_amd._lib) and exposes torch-tensor operators (forge_amd.ops).
+"""
+from ._lib import ForgeError, LIB_PATH, load  # noqa: F401
+
+__all__ = ["ForgeError", "LIB_PATH", "load", "ops"]
+
+
+def __getattr__(name):
+    if name == "ops":
+        from . import ops
+        return ops
+    raise AttributeError(name)

@@ -1,0 +1,457 @@
+// 2:4 structured-sparse INT8 GEMM for gfx950 on v_smfmac_i32_16x16x128_i8.
+//
+// Reference: src/gemm/int8_sparse.cu (persistent-CTA mma.sp.m16n8k64, 3-stage cp.async
+// pipeline, FP32-atomic split-K, RTX-4090 cost model). Computes
+//     Y[m,n] = half(fma(sum_k x[m,k] * Wp[n,k], act_scale[m] * w_scale[n], bias[n]))
+// (int8_sparse.cu:659-661), Wp = the 2:4 weights given by W_comp (N,K/2) and w_meta.
+//
+// Operand roles: the SMFMAC sparse operand A is the compressed weight (16 weight rows x
+// 128 dense K per instruction), operand B the activations (128 K x 16 tokens). The
+// accumulator block is C[n][m]; lane l holds rows n = 4*(l/16)+e (e = 0..3) of token
+// column m = l%16, i.e. 4 consecutive outputs of one row of Y -> one 8-byte FP16 (or
+// 16-byte INT32) store.
+// Lane operand ownership per 128-deep K step (lane l, g = l/16 selects a 32-deep K slice):
+//   A: 16 compressed bytes of weight row l%16 covering dense K [32g, 32g+32)
+//   B: 32 bytes of token row l%16, K [32g, 32g+32)
+//   index: the reference metadata word (row l%16, 32-K chunk 4s+g): nibble j (bits 4j..4j+3)
+//          holds the two kept positions of the j-th group of 4.
+// pack_metadata stores exactly these words so that a wave's 64 index words are one
+// contiguous 256-byte run (sparsity.hip).
+//
+// Split-K: each split adds its exact INT32 partial sum into the caller's (M,N)
+// workspace with integer atomics (order-independent), then a finalize kernel applies
+// the epilogue -- every split yields the same bits as split_k = 1 (the reference's
+// FP32-atomic split-K is not deterministic, int8_sparse.cu:610-632).
+#include "common.h"
+#include "gemm_dense.h"
+#include "mfma_tile.h"
+#include "forge/gemm/int8_sparse.h"
+
+#include <algorithm>
+#include <mutex>
+
+namespace forge_amd {
+
+constexpr int kSpStep = 128;        // dense K per stage
+constexpr int kSpARow = 64;         // compressed bytes per weight row per stage
+constexpr int kSpBRow = 128;        // activation bytes per token row per stage
+
+// A rows: 64 B (4 chunks), same swizzle as the dense engine. B rows: 128 B (8 chunks),
+// chunk position c ^ ((r ^ (r >> 3)) & 7): conflict free for the 16-row, same-chunk reads.
+__device__ __forceinline__ int sp_a_off(int r, int c) { return r * kSpARow + ((c ^ (((r >> 1) ^ (r >> 3)) & 3)) << 4); }
+__device__ __forceinline__ int sp_b_off(int r, int c) { return r * kSpBRow + ((c ^ ((r ^ (r >> 3)) & 7)) << 4); }
+
+struct SparseArgs {
+    const int8_t* W_comp;     // (N, K/2)
+    const int8_t* x;          // (M, K)
+    const uint32_t* meta;     // gfx950 layout
+    const float* act_scale;
+    const uint16_t* w_scale;
+    const uint16_t* bias;
+    uint16_t* out16;          // direct FP16 output (split == 1)
+    int32_t* out32;           // direct INT32 output, or the split-K workspace
+    int M, K, N;
+    int split_k, steps_per_split;
+    int tiles_n, tiles_m;
+    int atomic;               // accumulate into out32 with atomics (split-K)
+};
+
+template <int BNW, int BMT, int WN, int WM>
+struct SparseCfg {
+    static constexpr int kThreads = WN * WM * kWave;
+    static constexpr int kTN = BNW / WN / 16;   // 16-row weight blocks per wave
+    static constexpr int kTM = BMT / WM / 16;   // 16-token blocks per wave
+    static constexpr int kAChunks = BNW * 4 / kThreads;
+    static constexpr int kBChunks = BMT * 8 / kThreads;
+    static constexpr int kMetaInt4 = BNW;               // BNW/16 blocks x 16 int4 (64 words)
+    static constexpr int kMChunks = (kMetaInt4 + kThreads - 1) / kThreads;
+    static constexpr int kStageBytes = BNW * kSpARow + BMT * kSpBRow + BNW * 16;
+    static constexpr int kLdsBytes = 2 * kStageBytes;
+    static_assert(BNW * 4 % kThreads == 0 && BMT * 8 % kThreads == 0, "stage split");
+};
+
+template <int BNW, int BMT, int WN, int WM>
+__global__ __launch_bounds__(WN * WM * kWave) void sparse_gemm_kernel(SparseArgs p)
+{
+    using Cfg = SparseCfg<BNW, BMT, WN, WM>;
+    extern __shared__ __align__(16) int8_t lds[];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+
+    const int spatial = p.tiles_n * p.tiles_m;
+    const int split = blockIdx.x / spatial;
+    int tn, tm;
+    tile_coords(blockIdx.x - split * spatial, p.tiles_n, p.tiles_m, tn, tm);
+    const int n0 = tn * BNW, m0 = tm * BMT;
+    const int steps_total = (p.K + kSpStep - 1) / kSpStep;
+    const int s_begin = split * p.steps_per_split;
+    const int s_end = min(s_begin + p.steps_per_split, steps_total);
+    const int wn = (wave / WM) * (BNW / WN);
+    const int wm = (wave % WM) * (BMT / WM);
+    const int K = p.K, N = p.N, M = p.M;
+    const int Kc = K >> 1, cpr = K >> 5;
+
+    v4i acc[Cfg::kTN][Cfg::kTM];
+#pragma unroll
+    for (int i = 0; i < Cfg::kTN; i++)
+#pragma unroll
+        for (int j = 0; j < Cfg::kTM; j++) acc[i][j] = v4i{0, 0, 0, 0};
+
+    if (s_begin < s_end) {
+        int4 ra[Cfg::kAChunks], rb[Cfg::kBChunks], rm[Cfg::kMChunks];
+        auto gload = [&](int s) {
+            const int kd = s * kSpStep;          // dense K of this stage
+            const int kc = kd >> 1;              // compressed K
+#pragma unroll
+            for (int i = 0; i < Cfg::kAChunks; i++) {
+                const int id = tid + i * Cfg::kThreads;
+                const int r = id >> 2, c = id & 3;
+                const int n = n0 + r, k = kc + (c << 4);
+                ra[i] = (n < N && k < Kc) ? *reinterpret_cast<const int4*>(p.W_comp + static_cast<size_t>(n) * Kc + k)
+                                          : make_int4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < Cfg::kBChunks; i++) {
+                const int id = tid + i * Cfg::kThreads;
+                const int r = id >> 3, c = id & 7;
+                const int m = m0 + r, k = kd + (c << 4);
+                rb[i] = (m < M && k < K) ? *reinterpret_cast<const int4*>(p.x + static_cast<size_t>(m) * K + k)
+                                         : make_int4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < Cfg::kMChunks; i++) {
+                const int id = tid + i * Cfg::kThreads;     // int4 index within the stage
+                const int blk = id >> 4, q = id & 15;       // 16 int4 = 64 words per 16-row block
+                const int c = (kd >> 5) + (q >> 2);         // 32-K chunk of these 4 words
+                const int n = n0 + blk * 16;
+                rm[i] = (id < Cfg::kMetaInt4 && n < N && c < cpr)
+                            ? *reinterpret_cast<const int4*>(p.meta + static_cast<size_t>(n >> 4) * cpr * 16 +
+                                                             static_cast<size_t>(kd >> 5) * 16 + q * 4)
+                            : make_int4(0, 0, 0, 0);
+            }
+        };
+        auto lstore = [&](int buf) {
+            int8_t* base = lds + buf * Cfg::kStageBytes;
+            int8_t* As = base;
+            int8_t* Bs = base + BNW * kSpARow;
+            int8_t* Ms = Bs + BMT * kSpBRow;
+#pragma unroll
+            for (int i = 0; i < Cfg::kAChunks; i++) {
+                const int id = tid + i * Cfg::kThreads;
+                *reinterpret_cast<int4*>(As + sp_a_off(id >> 2, id & 3)) = ra[i];
+            }
+#pragma unroll
+            for (int i = 0; i < Cfg::kBChunks; i++) {
+                const int id = tid + i * Cfg::kThreads;
+                *reinterpret_cast<int4*>(Bs + sp_b_off(id >> 3, id & 7)) = rb[i];
+            }
+#pragma unroll
+            for (int i = 0; i < Cfg::kMChunks; i++) {
+                const int id = tid + i * Cfg::kThreads;
+                if (id < Cfg::kMetaInt4) *reinterpret_cast<int4*>(Ms + id * 16) = rm[i];
+            }
+        };
+
+        gload(s_begin);
+        lstore(0);
+        __syncthreads();
+        const int g = lane >> 4;
+        const int r16 = lane & 15;
+        for (int s = s_begin; s < s_end; s++) {
+            const int cur = (s - s_begin) & 1;
+            const bool more = (s + 1) < s_end;
+            if (more) gload(s + 1);
+            const int8_t* base = lds + cur * Cfg::kStageBytes;
+            const int8_t* As = base;
+            const int8_t* Bs = base + BNW * kSpARow;
+            const uint32_t* Ms = reinterpret_cast<const uint32_t*>(Bs + BMT * kSpBRow);
+            v4i fa[Cfg::kTN];
+            int fi[Cfg::kTN];
+#pragma unroll
+            for (int i = 0; i < Cfg::kTN; i++) {
+                const int r = wn + 16 * i + r16;
+                fa[i] = *reinterpret_cast<const v4i*>(As + sp_a_off(r, g));
+                fi[i] = static_cast<int>(Ms[((wn >> 4) + i) * 64 + lane]);
+            }
+#pragma unroll
+            for (int j = 0; j < Cfg::kTM; j++) {
+                const int r = wm + 16 * j + r16;
+                const v4i b0 = *reinterpret_cast<const v4i*>(Bs + sp_b_off(r, 2 * g));
+                const v4i b1 = *reinterpret_cast<const v4i*>(Bs + sp_b_off(r, 2 * g + 1));
+                const v8i fb = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+#pragma unroll
+                for (int i = 0; i < Cfg::kTN; i++)
+                    acc[i][j] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(fa[i], fb, acc[i][j], fi[i], 0, 0);
+            }
+            if (more) lstore(cur ^ 1);
+            __syncthreads();
+        }
+    }
+
+    // Epilogue: lane holds C[n0+wn+16i+4*(l/16)+e][m0+wm+16j+l%16], e = 0..3.
+    const int nq = 4 * (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < Cfg::kTM; j++) {
+        const int m = m0 + wm + 16 * j + (lane & 15);
+        if (m >= M) continue;
+        const float as = p.out16 ? p.act_scale[m] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < Cfg::kTN; i++) {
+            const int n = n0 + wn + 16 * i + nq;
+            if (n >= N) continue;                      // N % 16 == 0: 4 rows in or out together
+            const size_t o = static_cast<size_t>(m) * N + n;
+            if (p.atomic) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) atomicAdd(p.out32 + o + e, acc[i][j][e]);
+            } else if (p.out16) {
+                uint16_t h[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float b = p.bias ? h2f(p.bias[n + e]) : 0.0f;
+                    h[e] = dequant_gemm(acc[i][j][e], as, h2f(p.w_scale[n + e]), b, p.bias != nullptr);
+                }
+                *reinterpret_cast<uint2*>(p.out16 + o) =
+                    make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+            } else {
+                *reinterpret_cast<int4*>(p.out32 + o) = make_int4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+            }
+        }
+    }
+}
+
+// Zero fill (graph-capture safe: a kernel, not a memset node).
+__global__ __launch_bounds__(256) void zero_i32_kernel(int4* __restrict__ p, long long n4, int32_t* tail, int ntail)
+{
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n4; i += stride)
+        p[i] = make_int4(0, 0, 0, 0);
+    if (blockIdx.x == 0 && threadIdx.x < ntail) tail[threadIdx.x] = 0;
+}
+
+// Split-K finalize: INT32 sums -> FP16 with the GEMM epilogue.
+__global__ __launch_bounds__(256) void splitk_finalize_kernel(
+    const int32_t* __restrict__ ws, const float* __restrict__ act_scale, const uint16_t* __restrict__ w_scale,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int N, long long total)
+{
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < total; i += stride) {
+        const int m = static_cast<int>(i / N), n = static_cast<int>(i % N);
+        out[i] = dequant_gemm(ws[i], act_scale[m], h2f(w_scale[n]), bias ? h2f(bias[n]) : 0.0f, bias != nullptr);
+    }
+}
+
+// Reference splitk_reduce (int8_sparse.cu:99-111): fp32 workspace + bias -> fp16.
+__global__ __launch_bounds__(256) void splitk_reduce_f32_kernel(
+    const float* __restrict__ ws, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int N, long long total)
+{
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < total; i += stride) {
+        float v = ws[i];
+        if (bias) v += h2f(bias[i % N]);
+        out[i] = f2h(v);
+    }
+}
+
+// ---- tile configurations ----------------------------------------------------------
+
+constexpr int kSpTileBW[FORGE_SPARSE_NUM_TILES] = {256, 128, 128};
+constexpr int kSpTileBC[FORGE_SPARSE_NUM_TILES] = {128, 128, 64};
+
+template <int BNW, int BMT, int WN, int WM>
+static void sparse_set_attr() {
+    using Cfg = SparseCfg<BNW, BMT, WN, WM>;
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&sparse_gemm_kernel<BNW, BMT, WN, WM>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::kLdsBytes);
+}
+
+static void sparse_init_attrs() {
+    static std::once_flag once;
+    std::call_once(once, [] {
+        sparse_set_attr<256, 128, 2, 2>();
+        sparse_set_attr<128, 128, 2, 2>();
+        sparse_set_attr<128, 64, 2, 2>();
+        (void)hipGetLastError();
+    });
+}
+
+template <int BNW, int BMT, int WN, int WM>
+static int sparse_launch_cfg(SparseArgs p, hipStream_t s)
+{
+    using Cfg = SparseCfg<BNW, BMT, WN, WM>;
+    p.tiles_n = divup(p.N, BNW);
+    p.tiles_m = divup(p.M, BMT);
+    const long long grid = static_cast<long long>(p.tiles_n) * p.tiles_m * p.split_k;
+    if (grid > 0x7FFFFFFFLL) return FORGE_EINVAL;
+    sparse_gemm_kernel<BNW, BMT, WN, WM><<<static_cast<unsigned>(grid), Cfg::kThreads, Cfg::kLdsBytes, s>>>(p);
+    return launch_status();
+}
+
+static int sparse_launch(int tile, const SparseArgs& p, hipStream_t s)
+{
+    sparse_init_attrs();
+    switch (tile) {
+    case 0: return sparse_launch_cfg<256, 128, 2, 2>(p, s);
+    case 1: return sparse_launch_cfg<128, 128, 2, 2>(p, s);
+    default: return sparse_launch_cfg<128, 64, 2, 2>(p, s);
+    }
+}
+
+// ---- planner ------------------------------------------------------------------------
+// Wave-aware cost model with the reference's form (int8_sparse.cu:875-920):
+//   t(tile, s) = waves * (a_tile * ceil(steps / s) + b_tile) + [s > 1] (c0 + (c1 + c2 s) MN/1e6)
+//   waves      = ceil(tiles(tile) * s / CUs)
+// a_tile: time of one 128-deep K step of a tile at the SMFMAC rate (dense-equivalent
+// 2*BW*BC*128 ops at 2 x 5.0 POPS / 256 CUs per CU), inflated for LDS/issue overhead;
+// b_tile: per-tile fixed cost (fill + epilogue). Times in microseconds.
+double sparse_plan_cost(int M, int K, int N, int split_k, bool have_ws, int tile, int cu, int* out_tile,
+                        int* out_split)
+{
+    static const double kA[FORGE_SPARSE_NUM_TILES] = {0.110, 0.058, 0.032};   // us per K step per tile
+    static const double kB[FORGE_SPARSE_NUM_TILES] = {1.60, 1.10, 0.80};      // us per tile
+    const double kC0 = 2.0, kC1 = 0.60, kC2 = 0.25;                     // split-K launch / zero+finalize / atomics
+    static const int kAutoSplits[] = {1, 2, 3, 4, 6};
+    if (tile >= FORGE_SPARSE_NUM_TILES) tile = -1;
+    if (split_k > 1 && !have_ws) split_k = 1;
+    const int steps = divup(K, kSpStep);
+    const bool auto_split = split_k <= 0;
+    int best_t = 1, best_s = 1;
+    double best = 1e300;
+    for (int t = 0; t < FORGE_SPARSE_NUM_TILES; t++) {
+        if (tile >= 0 && t != tile) continue;
+        const long long tiles = static_cast<long long>(divup(N, kSpTileBW[t])) * divup(M, kSpTileBC[t]);
+        const int ncand = auto_split ? (have_ws ? 5 : 1) : 1;
+        for (int c = 0; c < ncand; c++) {
+            const int sp = auto_split ? kAutoSplits[c] : split_k;
+            if (auto_split && sp > 1 && sp > steps / 2) continue;
+            const long long waves = divupll(tiles * sp, cu);
+            const int ks = divup(steps, sp);
+            double cost = static_cast<double>(waves) * (kA[t] * ks + kB[t]);
+            if (sp > 1) cost += kC0 + (kC1 + kC2 * sp) * (static_cast<double>(M) * N * 1e-6);
+            if (cost < best) { best = cost; best_t = t; best_s = sp; }
+        }
+    }
+    *out_tile = best_t;
+    *out_split = best_s;
+    return best;
+}
+
+static int cu_count_or_default() {
+    int st = FORGE_OK;
+    const DeviceInfo& d = device_info(&st);
+    return (st == FORGE_OK && d.cu_count > 0) ? d.cu_count : default_cu_count();
+}
+
+int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, const float* act_scale,
+                const uint16_t* w_scale, const uint16_t* bias, uint16_t* out16, int32_t* out32, int M,
+                int K, int N, int32_t* ws, int split_k, int tile, hipStream_t s)
+{
+    if (K % 64 != 0 || N % 16 != 0) return FORGE_EINVAL;
+    if (!aligned(W_comp, 16) || !aligned(x, 16) || !aligned(meta, 16)) return FORGE_EINVAL;
+    if (out16 && !aligned(out16, 8)) return FORGE_EINVAL;
+    if (out32 && !aligned(out32, 16)) return FORGE_EINVAL;
+    int st = FORGE_OK;
+    device_info(&st);
+    if (st != FORGE_OK) return st;
+
+    int pt = 1, ps = 1;
+    sparse_plan_cost(M, K, N, out32 ? 1 : split_k, out32 ? false : ws != nullptr, tile,
+                     cu_count_or_default(), &pt, &ps);
+    const int steps = divup(K, kSpStep);
+    SparseArgs p{};
+    p.W_comp = W_comp; p.x = x; p.meta = meta; p.act_scale = act_scale; p.w_scale = w_scale;
+    p.bias = bias; p.M = M; p.K = K; p.N = N;
+    if (ps > 1 && ws) {
+        p.split_k = ps;
+        p.steps_per_split = divup(steps, ps);
+        p.out16 = nullptr;
+        p.out32 = ws;
+        p.atomic = 1;
+        const long long total = static_cast<long long>(M) * N;
+        const int blocks = static_cast<int>(std::min<long long>(divupll(total / 4, 256) + 1, 8192));
+        zero_i32_kernel<<<blocks, 256, 0, s>>>(reinterpret_cast<int4*>(ws), total / 4, ws + (total / 4) * 4,
+                                               static_cast<int>(total % 4));
+        if ((st = launch_status()) != FORGE_OK) return st;
+        if ((st = sparse_launch(pt, p, s)) != FORGE_OK) return st;
+        const int fblocks = static_cast<int>(std::min<long long>(divupll(total, 256), 8192));
+        splitk_finalize_kernel<<<fblocks, 256, 0, s>>>(ws, act_scale, w_scale, bias, out16, N, total);
+        return launch_status();
+    }
+    p.split_k = 1;
+    p.steps_per_split = steps;
+    p.out16 = out16;
+    p.out32 = out32;
+    p.atomic = 0;
+    return sparse_launch(pt, p, s);
+}
+
+}  // namespace forge_amd
+
+using namespace forge_amd;
+
+extern "C" int forge_sparse_int8_gemm_plan(int M, int K, int N_out, int split_k, int have_workspace,
+                                           int tile, int* out_tile, int* out_split_k)
+{
+    if (!out_tile || !out_split_k) return FORGE_EINVAL;
+    sparse_plan_cost(std::max(M, 1), std::max(K, 1), std::max(N_out, 1), split_k, have_workspace != 0, tile,
+                     cu_count_or_default(), out_tile, out_split_k);
+    return FORGE_OK;
+}
+
+extern "C" int forge_sparse_int8_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* w_meta,
+                                      const float* act_scale, const uint16_t* w_scale,
+                                      const uint16_t* bias, uint16_t* out, int M, int K, int N_out,
+                                      float* splitk_workspace, int split_k, void* stream, int tile)
+{
+    if (M <= 0 || K <= 0 || N_out <= 0) return FORGE_OK;
+    if (!W_comp || !x || !w_meta || !act_scale || !w_scale || !out) return FORGE_EINVAL;
+    if (splitk_workspace && !aligned(splitk_workspace, 16)) return FORGE_EINVAL;
+    return sparse_gemm(W_comp, x, w_meta, act_scale, w_scale, bias, out, nullptr, M, K, N_out,
+                       reinterpret_cast<int32_t*>(splitk_workspace), split_k, tile, as_stream(stream));
+}
+
+extern "C" int forge_sparse_int8_gemm_s32(const int8_t* W_comp, const int8_t* x, const uint32_t* w_meta,
+                                          int32_t* C, int M, int K, int N_out, void* stream)
+{
+    if (M <= 0 || K <= 0 || N_out <= 0) return FORGE_OK;
+    if (!W_comp || !x || !w_meta || !C) return FORGE_EINVAL;
+    return sparse_gemm(W_comp, x, w_meta, nullptr, nullptr, nullptr, nullptr, C, M, K, N_out, nullptr, 1,
+                       -1, as_stream(stream));
+}
+
+// The fused quantize + GEMM path (reference int8_sparse.cu:258-335, K <= 1280) is not
+// built yet; the automatic choice therefore never selects it.
+extern "C" int forge_sparse_int8_linear_fused(int M, int K, int N_out, int* out_flag)
+{
+    (void)M; (void)K; (void)N_out;
+    if (!out_flag) return FORGE_EINVAL;
+    *out_flag = 0;
+    return FORGE_OK;
+}
+
+extern "C" int forge_sparse_int8_linear(const uint16_t* x, const int8_t* W_comp, const uint32_t* w_meta,
+                                        const uint16_t* w_scale, const uint16_t* bias, uint16_t* out,
+                                        int M, int K, int N_out, int8_t* scratch_q, float* scratch_scale,
+                                        float* splitk_workspace, int split_k, void* stream, int path)
+{
+    (void)path;   // every path computes the same bits; the two-pass path serves them all
+    if (M <= 0 || K <= 0 || N_out <= 0) return FORGE_OK;
+    if (!x || !W_comp || !w_meta || !w_scale || !out || !scratch_q || !scratch_scale) return FORGE_EINVAL;
+    if (K % 64 != 0 || N_out % 16 != 0) return FORGE_EINVAL;
+    hipStream_t s = as_stream(stream);
+    int st = launch_quantize(x, scratch_q, scratch_scale, M, K, s);
+    if (st != FORGE_OK) return st;
+    return sparse_gemm(W_comp, scratch_q, w_meta, scratch_scale, w_scale, bias, out, nullptr, M, K, N_out,
+                       reinterpret_cast<int32_t*>(splitk_workspace), split_k, -1, s);
+}
+
+extern "C" int forge_splitk_reduce(const float* workspace, const uint16_t* bias, uint16_t* out, int M,
+                                   int N_out, void* stream)
+{
+    if (M <= 0 || N_out <= 0) return FORGE_OK;
+    if (!workspace || !out) return FORGE_EINVAL;
+    const long long total = static_cast<long long>(M) * N_out;
+    const int blocks = static_cast<int>(std::min<long long>(divupll(total, 256), 8192));
+    splitk_reduce_f32_kernel<<<blocks, 256, 0, as_stream(stream)>>>(workspace, bias, out, N_out, total);
+    return launch_status();
+}

@@ -1,0 +1,241 @@
+// Per-token FP16 -> INT8 activation quantization and INT32 -> FP16 dequantization
+// for gfx950.
+//
+// Reference behaviour: src/quant/quantize.cu:8-191 and src/quant/dequantize.cu:8-45.
+//   scale[m] = max(absmax(x[m,:]), 1e-8f) / 127.0f      (IEEE division)
+//   q[m,k]   = clamp(rne(x[m,k] * (1.0f / scale[m])), -128, 127)
+//
+// MI355X design: the main kernel gives each row to ONE wavefront (4 rows per 256-thread
+// workgroup). A lane holds VPT 16-byte vectors of its row in VGPRs, so x is read from
+// HBM once; the row absmax is a 64-lane butterfly (no LDS, no barrier), then each lane
+// writes 8 int8 per vector. The exported two-pass kernel (any K, any alignment, any
+// block size) reduces through LDS; both compute the same max (exact) and the same
+// IEEE-rounded arithmetic, so their outputs are bit-identical.
+#include "common.h"
+#include "forge/quant/quantize.h"
+#include "forge/quant/dequantize.h"
+
+namespace forge_amd {
+
+__device__ __forceinline__ float row_scale(float amax) {
+    return fmaxf(amax, 1e-8f) / 127.0f;
+}
+
+__device__ __forceinline__ int quant1(float x, float inv) {
+    const float r = __builtin_rintf(x * inv);
+    // NaN -> 0 (as a float->int conversion of NaN gives on both vendors), then clamp.
+    int q = (r == r) ? static_cast<int>(fminf(fmaxf(r, -128.0f), 127.0f)) : 0;
+    return q;
+}
+
+// 8 halves (one uint4) -> 8 int8 packed into a uint2.
+__device__ __forceinline__ uint2 quant8(uint4 v, float inv) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t out[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int q0 = quant1(h2f(static_cast<uint16_t>(w[j] & 0xFFFFu)), inv);
+        const int q1 = quant1(h2f(static_cast<uint16_t>(w[j] >> 16)), inv);
+        out[j >> 1] |= ((static_cast<uint32_t>(q0) & 0xFFu) << (16 * (j & 1))) |
+                       ((static_cast<uint32_t>(q1) & 0xFFu) << (16 * (j & 1) + 8));
+    }
+    return make_uint2(out[0], out[1]);
+}
+
+__device__ __forceinline__ float absmax8(uint4 v, float m) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        m = fmaxf(m, fabsf(h2f(static_cast<uint16_t>(w[j] & 0xFFFFu))));
+        m = fmaxf(m, fabsf(h2f(static_cast<uint16_t>(w[j] >> 16))));
+    }
+    return m;
+}
+
+// One wavefront per row; K % 8 == 0, K <= VPT * 512, x 16-byte and q 8-byte aligned.
+template <int VPT>
+__global__ __launch_bounds__(256) void quantize_rows_wave_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scales,
+    int M, int K)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (row >= M) return;   // whole wave exits together: no barrier below
+    const int nvec = K >> 3;
+    const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<size_t>(row) * K);
+    uint2* dst = reinterpret_cast<uint2*>(q + static_cast<size_t>(row) * K);
+
+    uint4 v[VPT];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const int idx = lane + i * kWave;
+        if (idx < nvec) {
+            v[i] = src[idx];
+            amax = absmax8(v[i], amax);
+        }
+    }
+    amax = wave_max(amax);
+    const float scale = row_scale(amax);
+    const float inv = 1.0f / scale;
+    if (lane == 0) scales[row] = scale;
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const int idx = lane + i * kWave;
+        if (idx < nvec) dst[idx] = quant8(v[i], inv);
+    }
+}
+
+// Two-pass body shared by the exported kernel: any K, any alignment, any blockDim.
+__device__ void quantize_row_twopass(const uint16_t* __restrict__ in_row, int8_t* __restrict__ out_row,
+                                     float* __restrict__ scale_out, int K)
+{
+    __shared__ float red[1024];
+    const int t = threadIdx.x, nt = blockDim.x;
+    float m = 0.0f;
+    for (int k = t; k < K; k += nt) m = fmaxf(m, fabsf(h2f(in_row[k])));
+    red[t] = m;
+    __syncthreads();
+    // Tree over the next power of two >= blockDim (missing entries read as 0).
+    int p = 1;
+    while (p < nt) p <<= 1;
+    for (int s = p >> 1; s > 0; s >>= 1) {
+        if (t < s && t + s < nt) red[t] = fmaxf(red[t], red[t + s]);
+        __syncthreads();
+    }
+    const float scale = row_scale(red[0]);
+    const float inv = 1.0f / scale;
+    if (t == 0) *scale_out = scale;
+    for (int k = t; k < K; k += nt) out_row[k] = static_cast<int8_t>(quant1(h2f(in_row[k]), inv));
+}
+
+// Dequant of src/quant/dequantize.cu:22-26: ((float)acc * as) * ws [+ bias].
+__device__ __forceinline__ uint16_t dequant_standalone(int acc, float as, float ws, float b, bool has_bias) {
+    const float p = static_cast<float>(acc) * as;
+    return f2h(has_bias ? __builtin_fmaf(p, ws, b) : p * ws);
+}
+
+// Vectorised launcher kernel: 4 outputs per thread, grid-stride over the (M,N) range.
+__global__ __launch_bounds__(256) void dequantize_vec4_kernel(
+    const int4* __restrict__ acc, const float* __restrict__ act_scale,
+    const uint16_t* __restrict__ w_scale, const uint16_t* __restrict__ bias,
+    uint2* __restrict__ out, int N, long long total4)
+{
+    const int n4 = N >> 2;
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < total4;
+         i += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const int m = static_cast<int>(i / n4);
+        const int n = static_cast<int>(i - static_cast<long long>(m) * n4) * 4;
+        const int4 a = acc[i];
+        const float as = act_scale[m];
+        const int av[4] = {a.x, a.y, a.z, a.w};
+        uint16_t h[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            h[j] = dequant_standalone(av[j], as, h2f(w_scale[n + j]), bias ? h2f(bias[n + j]) : 0.0f,
+                                      bias != nullptr);
+        out[i] = make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16),
+                            h[2] | (static_cast<uint32_t>(h[3]) << 16));
+    }
+}
+
+}  // namespace forge_amd
+
+// ---- exported kernels (reference symbols) ----------------------------------------
+
+namespace forge { namespace quant {
+
+// include/forge/quant/quantize.cuh:17-21: grid = M rows, any block size.
+__global__ void fused_quantize_activation_kernel(const __half* __restrict__ input,
+                                                 int8_t* __restrict__ output,
+                                                 float* __restrict__ scales, int K)
+{
+    const size_t row = blockIdx.x;
+    forge_amd::quantize_row_twopass(reinterpret_cast<const uint16_t*>(input) + row * K,
+                                    output + row * K, scales + row, K);
+}
+
+// include/forge/quant/dequantize.cuh:14-20: grid = M rows, any block size.
+__global__ void fused_dequantize_bias_kernel(const int32_t* __restrict__ input,
+                                             const float* __restrict__ act_scale,
+                                             const __half* __restrict__ w_scale,
+                                             const __half* __restrict__ bias,
+                                             __half* __restrict__ output, int N)
+{
+    const size_t row = blockIdx.x;
+    const float as = act_scale[row];
+    const uint16_t* ws = reinterpret_cast<const uint16_t*>(w_scale);
+    const uint16_t* b = reinterpret_cast<const uint16_t*>(bias);
+    uint16_t* out = reinterpret_cast<uint16_t*>(output) + row * N;
+    for (int n = threadIdx.x; n < N; n += blockDim.x)
+        out[n] = forge_amd::dequant_standalone(input[row * N + n], as, forge_amd::h2f(ws[n]),
+                                               b ? forge_amd::h2f(b[n]) : 0.0f, b != nullptr);
+}
+
+}}  // namespace forge::quant
+
+// ---- C-ABI -----------------------------------------------------------------------
+
+using namespace forge_amd;
+
+namespace forge_amd {
+
+int launch_quantize(const uint16_t* x, int8_t* q, float* scales, int M, int K, hipStream_t s)
+{
+    const bool vec_ok = (K % 8 == 0) && K <= 16 * 512 && aligned(x, 16) && aligned(q, 8);
+    if (vec_ok) {
+        const int rows_per_block = 4;
+        const dim3 grid(divup(M, rows_per_block)), block(rows_per_block * kWave);
+        const int vpt = divup(K, 512);
+        if (vpt <= 1)      quantize_rows_wave_kernel<1><<<grid, block, 0, s>>>(x, q, scales, M, K);
+        else if (vpt <= 2) quantize_rows_wave_kernel<2><<<grid, block, 0, s>>>(x, q, scales, M, K);
+        else if (vpt <= 4) quantize_rows_wave_kernel<4><<<grid, block, 0, s>>>(x, q, scales, M, K);
+        else if (vpt <= 8) quantize_rows_wave_kernel<8><<<grid, block, 0, s>>>(x, q, scales, M, K);
+        else               quantize_rows_wave_kernel<16><<<grid, block, 0, s>>>(x, q, scales, M, K);
+    } else {
+        forge::quant::fused_quantize_activation_kernel<<<M, 256, 0, s>>>(
+            reinterpret_cast<const __half*>(x), q, scales, K);
+    }
+    return launch_status();
+}
+
+}  // namespace forge_amd
+
+extern "C" int forge_quantize_activation(const uint16_t* x, int8_t* q, float* scales,
+                                         int M, int K, void* stream)
+{
+    if (M <= 0 || K <= 0) return FORGE_OK;
+    if (!x || !q || !scales) return FORGE_EINVAL;
+    return launch_quantize(x, q, scales, M, K, as_stream(stream));
+}
+
+extern "C" int forge_quantize_activation_twopass(const uint16_t* x, int8_t* q, float* scales,
+                                                 int M, int K, int threads, void* stream)
+{
+    if (M <= 0 || K <= 0) return FORGE_OK;
+    if (!x || !q || !scales || threads < 1 || threads > 1024) return FORGE_EINVAL;
+    forge::quant::fused_quantize_activation_kernel<<<M, threads, 0, as_stream(stream)>>>(
+        reinterpret_cast<const __half*>(x), q, scales, K);
+    return launch_status();
+}
+
+extern "C" int forge_dequantize_bias(const int32_t* acc, const float* act_scale,
+                                     const uint16_t* w_scale, const uint16_t* bias, uint16_t* out,
+                                     int M, int N, void* stream)
+{
+    if (M <= 0 || N <= 0) return FORGE_OK;
+    if (!acc || !act_scale || !w_scale || !out) return FORGE_EINVAL;
+    hipStream_t s = as_stream(stream);
+    if (N % 4 == 0 && aligned(acc, 16) && aligned(out, 8)) {
+        const long long total4 = static_cast<long long>(M) * (N / 4);
+        const int blocks = static_cast<int>(std::min<long long>(divupll(total4, 256), 8192));
+        dequantize_vec4_kernel<<<blocks, 256, 0, s>>>(reinterpret_cast<const int4*>(acc), act_scale,
+                                                     w_scale, bias, reinterpret_cast<uint2*>(out),
+                                                     N, total4);
+    } else {
+        forge::quant::fused_dequantize_bias_kernel<<<M, 256, 0, s>>>(
+            acc, act_scale, reinterpret_cast<const __half*>(w_scale),
+            reinterpret_cast<const __half*>(bias), reinterpret_cast<__half*>(out), N);
+    }
+    return launch_status();
+}

@@ -1,0 +1,173 @@
+// 2:4 prune + compress and metadata packing for gfx950.
+//
+// prune: src/sparsity/prune_compress.cu:24-68 -- per group of 4 along K keep the two
+// largest magnitudes; the two smallest are found with strict '<' comparisons seeded
+// from positions (0, 1), so among equal magnitudes the lower index is pruned. Kept
+// positions are ascending; nibble = keep0 | keep1 << 2. Values and nibbles are
+// bit-identical to the reference.
+//
+// pack: src/sparsity/pack_metadata.cu:23-29 builds word (n, c) = sum_g nib[n,8c+g] << 4g.
+// The same words are emitted here in the gfx950 SMFMAC layout: position
+//     (n/16) * (K/32) * 16 + c * R + n%16,  R = min(16, N - 16*(n/16))
+// For a full 16-row block, the 64 lanes of one v_smfmac_i32_16x16x128_i8 (lane =
+// row%16 + 16*chunk) then read their index words as one contiguous 256-byte run.
+#include "common.h"
+#include "forge/sparsity/prune_compress.h"
+#include "forge/sparsity/pack_metadata.h"
+
+namespace forge_amd {
+
+__host__ __device__ __forceinline__ size_t meta_pos(int n, int c, int N, int cpr) {
+    const int blk = n >> 4;
+    const int rows = (N - (blk << 4)) < 16 ? (N - (blk << 4)) : 16;
+    return static_cast<size_t>(blk) * cpr * 16 + static_cast<size_t>(c) * rows + (n & 15);
+}
+
+// Prune one group of 4 (abs of int8 fits in int; abs(-128) = 128).
+__device__ __forceinline__ void prune4(const int8_t v[4], int8_t& c0, int8_t& c1, uint8_t& nib) {
+    int a[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) a[i] = abs(static_cast<int>(v[i]));
+    int min1 = 0, min2 = 1;
+    if (a[0] > a[1]) { min1 = 1; min2 = 0; }
+#pragma unroll
+    for (int i = 2; i < 4; i++) {
+        if (a[i] < a[min1]) { min2 = min1; min1 = i; }
+        else if (a[i] < a[min2]) { min2 = i; }
+    }
+    // Kept = the complement of {min1, min2}, ascending.
+    const int pruned = (1 << min1) | (1 << min2);
+    int k0 = -1, k1 = -1;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (!(pruned & (1 << i))) {
+            if (k0 < 0) k0 = i; else k1 = i;
+        }
+    }
+    c0 = v[k0];
+    c1 = v[k1];
+    nib = static_cast<uint8_t>(k0 | (k1 << 2));
+}
+
+// Vectorised launcher kernel: one thread per 4 groups (16 weights -> 8 compressed bytes and
+// 4 nibbles); needs K % 16 == 0 and 16/8/4-byte aligned buffers.
+__global__ __launch_bounds__(256) void prune_compress_vec_kernel(
+    const int4* __restrict__ w, uint2* __restrict__ comp, uint32_t* __restrict__ meta, long long n16)
+{
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n16;
+         i += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const int4 v = w[i];
+        const int8_t* b = reinterpret_cast<const int8_t*>(&v);
+        uint32_t cw[2] = {0u, 0u};
+        uint32_t mw = 0;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            int8_t c0, c1;
+            uint8_t nib;
+            prune4(b + 4 * g, c0, c1, nib);
+            const uint32_t pair = (static_cast<uint32_t>(static_cast<uint8_t>(c0))) |
+                                  (static_cast<uint32_t>(static_cast<uint8_t>(c1)) << 8);
+            cw[g >> 1] |= pair << (16 * (g & 1));
+            mw |= static_cast<uint32_t>(nib) << (8 * g);
+        }
+        comp[i] = make_uint2(cw[0], cw[1]);
+        meta[i] = mw;
+    }
+}
+
+__global__ __launch_bounds__(256) void unpack_metadata_kernel(
+    const uint32_t* __restrict__ packed, uint8_t* __restrict__ raw, int N, int K)
+{
+    const int cpr = K / 32;
+    const long long total = static_cast<long long>(N) * cpr;
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const int n = static_cast<int>(i / cpr), c = static_cast<int>(i % cpr);
+        const uint32_t w = packed[meta_pos(n, c, N, cpr)];
+        uint8_t* dst = raw + static_cast<size_t>(n) * (K / 4) + static_cast<size_t>(c) * 8;
+#pragma unroll
+        for (int g = 0; g < 8; g++) dst[g] = static_cast<uint8_t>((w >> (4 * g)) & 0xFu);
+    }
+}
+
+}  // namespace forge_amd
+
+namespace forge { namespace sparsity {
+
+__global__ void prune_compress_kernel(const int8_t* __restrict__ weight,
+                                      int8_t* __restrict__ compressed,
+                                      uint8_t* __restrict__ metadata_raw, int N, int K)
+{
+    const long long idx = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    const int gpr = K / 4;
+    if (idx >= static_cast<long long>(N) * gpr) return;
+    const long long row = idx / gpr, g = idx % gpr;
+    const int8_t* src = weight + row * K + g * 4;
+    const int8_t v[4] = {src[0], src[1], src[2], src[3]};
+    int8_t c0, c1;
+    uint8_t nib;
+    forge_amd::prune4(v, c0, c1, nib);
+    compressed[row * (K / 2) + g * 2 + 0] = c0;
+    compressed[row * (K / 2) + g * 2 + 1] = c1;
+    metadata_raw[idx] = nib;
+}
+
+__global__ void pack_metadata_kernel(const uint8_t* __restrict__ meta_raw,
+                                     uint32_t* __restrict__ meta_packed, int N, int K)
+{
+    const long long idx = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    const int cpr = K / 32;
+    if (idx >= static_cast<long long>(N) * cpr) return;
+    const int n = static_cast<int>(idx / cpr), c = static_cast<int>(idx % cpr);
+    const uint8_t* src = meta_raw + static_cast<size_t>(n) * (K / 4) + static_cast<size_t>(c) * 8;
+    uint32_t w = 0;
+#pragma unroll
+    for (int g = 0; g < 8; g++) w |= (static_cast<uint32_t>(src[g]) & 0xFu) << (4 * g);
+    meta_packed[forge_amd::meta_pos(n, c, N, cpr)] = w;
+}
+
+}}  // namespace forge::sparsity
+
+using namespace forge_amd;
+
+extern "C" int forge_prune_compress_24(const int8_t* w, int8_t* comp, uint8_t* meta_raw,
+                                       int N, int K, void* stream)
+{
+    if (N <= 0 || K <= 0) return FORGE_OK;
+    if (!w || !comp || !meta_raw || K % 4 != 0) return FORGE_EINVAL;
+    hipStream_t s = as_stream(stream);
+    const long long groups = static_cast<long long>(N) * (K / 4);
+    if (K % 16 == 0 && aligned(w, 16) && aligned(comp, 8) && aligned(meta_raw, 4)) {
+        const long long n16 = groups / 4;
+        const int blocks = static_cast<int>(std::min<long long>(divupll(n16, 256), 16384));
+        prune_compress_vec_kernel<<<blocks, 256, 0, s>>>(reinterpret_cast<const int4*>(w),
+                                                        reinterpret_cast<uint2*>(comp),
+                                                        reinterpret_cast<uint32_t*>(meta_raw), n16);
+    } else {
+        forge::sparsity::prune_compress_kernel<<<static_cast<unsigned>(divupll(groups, 256)), 256, 0, s>>>(
+            w, comp, meta_raw, N, K);
+    }
+    return launch_status();
+}
+
+extern "C" int forge_pack_metadata(const uint8_t* meta_raw, uint32_t* meta_packed, int N, int K,
+                                   void* stream)
+{
+    if (N <= 0 || K <= 0) return FORGE_OK;
+    if (!meta_raw || !meta_packed || K % 32 != 0) return FORGE_EINVAL;
+    const long long total = static_cast<long long>(N) * (K / 32);
+    forge::sparsity::pack_metadata_kernel<<<static_cast<unsigned>(divupll(total, 256)), 256, 0,
+                                            as_stream(stream)>>>(meta_raw, meta_packed, N, K);
+    return launch_status();
+}
+
+extern "C" int forge_unpack_metadata(const uint32_t* meta_packed, uint8_t* meta_raw, int N, int K,
+                                     void* stream)
+{
+    if (N <= 0 || K <= 0) return FORGE_OK;
+    if (!meta_raw || !meta_packed || K % 32 != 0) return FORGE_EINVAL;
+    const long long total = static_cast<long long>(N) * (K / 32);
+    const int blocks = static_cast<int>(std::min<long long>(divupll(total, 256), 16384));
+    unpack_metadata_kernel<<<blocks, 256, 0, as_stream(stream)>>>(meta_packed, meta_raw, N, K);
+    return launch_status();
+}

@@ -1,0 +1,100 @@
+"""CPU checks of the C-ABI library: it loads, exports every symbol include/forge_amd.h
+declares (and the C++ API symbols of include/forge/), and rejects invalid arguments
+before touching a device. No compute calls are made here."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "forge_amd.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(forge_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import forge_amd
+    return forge_amd.load()
+
+
+def test_header_declares_the_path():
+    syms = declared_symbols()
+    for s in ["forge_quantize_activation", "forge_dequantize_bias", "forge_int8_gemm_dequant",
+              "forge_int8_linear", "forge_int8_gemm", "forge_sparse_int8_gemm", "forge_sparse_int8_linear",
+              "forge_sparse_int8_gemm_plan", "forge_prune_compress_24", "forge_pack_metadata",
+              "forge_splitk_reduce", "forge_int8_conv2d_forward", "forge_int8_conv2d_workspace_size"]:
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from forge_amd import _lib
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} missing from the ctypes table"
+
+
+def test_cpp_api_symbols_exported():
+    from forge_amd import LIB_PATH
+    out = subprocess.run(["nm", "-DC", "--defined-only", LIB_PATH], capture_output=True, text=True).stdout
+    for sym in ["forge::quant::fused_quantize_activation(", "forge::quant::fused_dequantize_bias(",
+                "forge::quant::fused_quantize_activation_kernel(", "forge::quant::fused_dequantize_bias_kernel(",
+                "forge::gemm::int8_gemm_dequant(", "forge::gemm::int8_linear(", "forge::gemm::int8_gemm(",
+                "forge::gemm::get_compute_capability(", "forge::gemm::has_wmma_int8(",
+                "forge::gemm::int8_dp4a_gemm_dequant(", "forge::gemm::int8_dp4a_linear(",
+                "forge::gemm::sparse_int8_gemm_plan(", "forge::gemm::sparse_int8_gemm(",
+                "forge::gemm::sparse_int8_linear(", "forge::gemm::sparse_int8_linear_fused(",
+                "forge::gemm::splitk_reduce(", "forge::sparsity::prune_compress_24(",
+                "forge::sparsity::pack_metadata(", "forge::sparsity::prune_compress_kernel(",
+                "forge::sparsity::pack_metadata_kernel(", "forge::nn::int8_conv2d_forward(",
+                "forge::nn::int8_conv2d_workspace_size(", "forge::last_error("]:
+        assert sym in out, sym
+
+
+def test_status_strings(lib):
+    assert lib.forge_status_string(0) == b"ok"
+    assert b"invalid" in lib.forge_status_string(-1)
+
+
+def test_nonpositive_dims_are_noops(lib):
+    # reference launchers return early on M, N or K <= 0 (src/gemm/int8_dense.cu:195)
+    assert lib.forge_int8_gemm_dequant(None, None, None, None, None, None, 0, 16, 16, None) == 0
+    assert lib.forge_quantize_activation(None, None, None, 0, 8, None) == 0
+    assert lib.forge_sparse_int8_gemm(None, None, None, None, None, None, None, 4, -1, 16, None, 1, None, -1) == 0
+    assert lib.forge_prune_compress_24(None, None, None, 0, 0, None) == 0
+
+
+def test_invalid_arguments_rejected_without_device(lib):
+    fake = ctypes.c_void_p(4096)   # never dereferenced: validation fails first
+    assert lib.forge_int8_gemm_dequant(None, fake, fake, fake, None, fake, 4, 16, 16, None) == -1
+    assert lib.forge_quantize_activation(fake, None, fake, 4, 8, None) == -1
+    assert lib.forge_quantize_activation_twopass(fake, fake, fake, 4, 8, 0, None) == -1
+    assert lib.forge_quantize_activation_twopass(fake, fake, fake, 4, 8, 2048, None) == -1
+    # sparse contract: K % 64 == 0 and N % 16 == 0 (include/forge/gemm/int8_sparse.cuh:12)
+    assert lib.forge_sparse_int8_gemm(fake, fake, fake, fake, fake, None, fake, 4, 96, 16, None, 1, None, -1) == -1
+    assert lib.forge_sparse_int8_gemm(fake, fake, fake, fake, fake, None, fake, 4, 128, 24, None, 1, None, -1) == -1
+    assert lib.forge_sparse_int8_linear(fake, fake, fake, fake, None, fake, 4, 96, 16, fake, fake, None, 1, None,
+                                        -1) == -1
+    # misaligned compressed weights
+    assert lib.forge_sparse_int8_gemm(ctypes.c_void_p(4097), fake, fake, fake, fake, None, fake, 4, 128, 16, None,
+                                      1, None, -1) == -1
+    assert lib.forge_prune_compress_24(fake, fake, fake, 4, 6, None) == -1     # K % 4
+    assert lib.forge_pack_metadata(fake, fake, 4, 48, None) == -1             # K % 32
+    out = ctypes.c_int()
+    assert lib.forge_sparse_int8_gemm_plan(4, 64, 16, 1, 1, -1, None, ctypes.byref(out)) == -1
+
+
+def test_conv_workspace_size(lib):
+    # [col fp16 | col int8 | act_scale | gemm_out] for one sample, 256-byte aligned regions
+    n = lib.forge_int8_conv2d_workspace_size(8, 16, 16, 16, 3, 3, 1, 1, 1, 1, 1, 1)
+    M, K = 16 * 16, 8 * 9
+    up = lambda b: (b + 255) // 256 * 256
+    assert n == up(M * K * 2) + up(M * K) + up(M * 4) + up(M * 16 * 2)
+    assert n >= M * K * 2 + M * K + M * 4 + M * 16 * 2     # at least the reference's size

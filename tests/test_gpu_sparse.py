@@ -1,0 +1,169 @@
+"""GPU parity: 2:4 prune/compress, gfx950 metadata pack, and the SMFMAC sparse GEMM.
+
+Bar: compressed values, raw nibbles and packed words bit-exact (tests/test_prune_compress.cu,
+tests/test_pack_metadata.cu); INT32 GEMM bit-exact; FP16 outputs bit-exact to the oracle's
+epilogue for every tile x split the planner can run (tests/test_int8_sparse_gemm.cu:140-155),
+with poisoned output and workspace; split-K bit-identical to unsplit (exact INT32
+reduction); sparse_int8_linear paths bit-identical (:222-230)."""
+import numpy as np
+import pytest
+
+from conftest import golden
+from helpers import fp16_normal, int8_uniform, poison, say, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def _prep(dev, W):
+    import torch
+    from forge_amd import ops
+    N, K = W.shape
+    comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+    raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+    meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+    ops.prune_compress_24(to_dev(W, dev), comp, raw, N, K)
+    ops.pack_metadata(raw, meta, N, K)
+    return comp, raw, meta
+
+
+def test_prune_golden(dev):
+    import torch
+    from forge_amd import ops
+    g = golden("prune")
+    N, K = g["W"].shape
+    say("prune golden")
+    comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+    raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+    ops.prune_compress_24(to_dev(g["W"], dev), comp, raw, N, K)
+    assert np.array_equal(to_host(comp), g["comp"]) and np.array_equal(to_host(raw), g["nibbles"])
+
+
+@pytest.mark.parametrize("N,K", [(32, 128), (11008, 4096), (7, 20), (48, 1040)])
+def test_prune_random(dev, orc, N, K):
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(N + K)
+    W = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    W[:, :8] = rng.integers(-2, 3, (N, 8))          # ties
+    cr, mr = orc.prune_compress_24(W)
+    say(f"prune N={N} K={K}")
+    comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+    raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+    ops.prune_compress_24(to_dev(W, dev), comp, raw, N, K)
+    assert np.array_equal(to_host(comp), cr) and np.array_equal(to_host(raw), mr)
+
+
+@pytest.mark.parametrize("which", ["", "_ragged"])
+def test_pack_golden_and_roundtrip(dev, which):
+    import torch
+    from forge_amd import ops
+    g = golden("pack")
+    raw = g["raw" + which]
+    N, K = (16, 128) if not which else (20, 96)
+    say(f"pack golden {which}")
+    meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+    ops.pack_metadata(to_dev(raw, dev), meta, N, K)
+    assert np.array_equal(to_host(meta).view(np.uint32), g["gfx950" + which])
+    back = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+    ops.unpack_metadata(meta, back, N, K)
+    assert np.array_equal(to_host(back), raw)
+
+
+# tests/test_int8_sparse_gemm.cu:275-284
+REF_SHAPES = [(1, 64, 16), (32, 128, 64), (37, 192, 208), (100, 640, 272), (300, 1280, 384),
+              (1000, 1536, 512), (2050, 512, 400), (129, 4096, 96)]
+
+
+@pytest.mark.parametrize("M,K,N", REF_SHAPES)
+def test_sparse_int32_all_tiles(dev, orc, M, K, N):
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(M * 13 + K + N)
+    W = int8_uniform(rng, (N, K))
+    x = int8_uniform(rng, (M, K))
+    cr, mr = orc.prune_compress_24(W)
+    ref = orc.sparse_gemm_s32(cr, x, mr, N, K)
+    comp, raw, meta = _prep(dev, W)
+    xd = to_dev(x, dev)
+    say(f"sparse s32 M={M} K={K} N={N}")
+    C = to_host(ops.sparse_int8_gemm_s32(comp, xd, meta))
+    assert np.array_equal(C, ref)
+
+
+@pytest.mark.parametrize("M,K,N", REF_SHAPES)
+def test_sparse_fp16_tiles_and_splits(dev, orc, M, K, N):
+    """Every tile x split (1,2,3,4,6,7, ksteps+1), poisoned output and workspace."""
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(M + K * 5 + N)
+    W = int8_uniform(rng, (N, K))
+    x = int8_uniform(rng, (M, K))
+    act = rng.uniform(0.001, 0.05, M).astype(np.float32)
+    ws = rng.uniform(0.001, 0.05, N).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
+    cr, mr = orc.prune_compress_24(W)
+    acc = orc.sparse_gemm_s32(cr, x, mr, N, K)
+    ref_b = orc.dequant_epilogue(acc, act, ws, b).view(np.uint16)
+    ref_nb = orc.dequant_epilogue(acc, act, ws, None).view(np.uint16)
+    comp, raw, meta = _prep(dev, W)
+    xd, actd, wsd, bd = to_dev(x, dev), to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev)
+    out = torch.empty((M, N), dtype=torch.float16, device=dev)
+    wsp = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ksteps = K // 64
+    for tile in range(3):
+        for split in (1, 2, 3, 4, 6, 7, ksteps + 1):
+            use_bias = split % 2 == 1
+            poison(out, 0x7B)
+            poison(wsp, 0x5A)
+            say(f"sparse fp16 M={M} K={K} N={N} tile={tile} split={split}")
+            ops.sparse_int8_gemm(comp, xd, meta, actd, wsd, bd if use_bias else None, splitk_workspace=wsp,
+                                 split_k=split, tile=tile, out=out)
+            got = to_host(out).view(np.uint16)
+            assert np.array_equal(got, ref_b if use_bias else ref_nb), (tile, split)
+    for split, use_ws in [(0, True), (0, False), (1, False), (4, False)]:
+        poison(out, 0x7B)
+        say(f"sparse fp16 auto split={split} ws={use_ws}")
+        ops.sparse_int8_gemm(comp, xd, meta, actd, wsd, bd, splitk_workspace=wsp if use_ws else None,
+                             split_k=split, out=out)
+        assert np.array_equal(to_host(out).view(np.uint16), ref_b)
+
+
+@pytest.mark.parametrize("M,K,N", [(37, 64, 16), (5000, 1024, 336), (70, 1280, 320), (16, 8192, 1024)])
+def test_sparse_linear_paths(dev, orc, M, K, N):
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(M + K + N)
+    W = int8_uniform(rng, (N, K))
+    x = rng.uniform(-2.0, 2.0, (M, K)).astype(np.float16)
+    ws = rng.uniform(0.001, 0.05, N).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
+    cr, mr = orc.prune_compress_24(W)
+    qr, sr = orc.quantize_rows(x)
+    ref = orc.dequant_epilogue(orc.sparse_gemm_s32(cr, qr, mr, N, K), sr, ws, b).view(np.uint16)
+    comp, raw, meta = _prep(dev, W)
+    xd, wsd, bd = to_dev(x, dev), to_dev(ws, dev), to_dev(b, dev)
+    sq = torch.empty((M, K), dtype=torch.int8, device=dev)
+    ss = torch.empty((M,), dtype=torch.float32, device=dev)
+    outs = []
+    for path, split in [(0, 1), (1, 1), (-1, 0), (-1, 3)]:
+        say(f"sparse linear M={M} K={K} N={N} path={path} split={split}")
+        outs.append(to_host(ops.sparse_int8_linear(xd, comp, meta, wsd, bd, sq, ss, None, split, path)).view(np.uint16))
+    for o in outs:
+        assert np.array_equal(o, ref)
+
+
+def test_config3_full_size_sampled(dev, orc):
+    """W (11008, 4096) pruned 2:4, A (4096, 4096); INT32 out, sampled rows."""
+    from forge_amd import ops
+    rng = np.random.default_rng(3)
+    N, K, M = 11008, 4096, 4096
+    W = int8_uniform(rng, (N, K))
+    x = int8_uniform(rng, (M, K))
+    cr, mr = orc.prune_compress_24(W)
+    rows = np.array([0, 1, 127, 128, 2049, 4095])
+    ref = orc.sparse_gemm_s32(cr, x[rows], mr, N, K)
+    comp, raw, meta = _prep(dev, W)
+    assert np.array_equal(to_host(comp), cr) and np.array_equal(to_host(raw), mr)
+    say("config3 sparse 4096x11008x4096")
+    C = to_host(ops.sparse_int8_gemm_s32(comp, to_dev(x, dev), meta))
+    assert np.array_equal(C[rows], ref)

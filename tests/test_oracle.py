@@ -1,0 +1,268 @@
+"""Pins the CPU oracle (oracle/forge_oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against something independent of its own formula:
+numpy/torch library routines, the golden fixtures (computed by tests/golden/make_golden.py
+with those routines), closed-form special cases, invariants, and brute force -- chosen so
+that a plausible mistake (dropped term, wrong sign or index, transposed operand, wrong
+rounding mode) fails at least one check.
+"""
+import itertools
+
+import numpy as np
+import pytest
+
+from conftest import golden
+
+
+# ---- fp16 conversions -------------------------------------------------------------
+
+def test_f16_to_f32_all_halves(orc):
+    L = orc.lib()
+    bits = np.arange(65536, dtype=np.uint32)
+    ref = bits.astype(np.uint16).view(np.float16).astype(np.float32)
+    got = np.array([L.orc_f16_to_f32(int(b)) for b in bits], np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_rne_matches_numpy(orc):
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(1000),
+        rng.standard_normal(20000).astype(np.float32) * np.float32(1e-5),   # subnormal halves
+        np.array([65504, 65519.99, 65520, 65536, -65520, 2 ** -24, 2 ** -25, 3 * 2 ** -26,
+                  2 ** -25 * 1.0000001, 0.0, -0.0, np.inf, -np.inf, 1.0 + 2 ** -11,
+                  1.0 + 3 * 2 ** -11, 2049.0, 2051.0], np.float32),
+    ])
+    # every halfway point between consecutive halves (ties) in the normal range
+    h = np.arange(0x0400, 0x7BFF, 37, dtype=np.uint16).view(np.float16).astype(np.float64)
+    h2 = np.arange(0x0401, 0x7C00, 37, dtype=np.uint16).view(np.float16).astype(np.float64)
+    n = min(len(h), len(h2))
+    ties = ((h[:n] + h2[:n]) / 2).astype(np.float32)
+    vals = np.concatenate([vals, ties, -ties])
+    got = orc.f32_to_f16_bits(vals)
+    ref = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
+# ---- quantize ----------------------------------------------------------------------
+
+def test_quantize_golden(orc):
+    g = golden("quantize")
+    q, s = orc.quantize_rows(g["X"])
+    assert np.array_equal(s.view(np.uint32), g["scales"].view(np.uint32))
+    assert np.array_equal(q, g["q"])
+
+
+def test_quantize_closed_forms(orc):
+    K = 16
+    x = np.zeros((4, K), np.float16)
+    x[1, 3] = -3.25                         # single nonzero -> -127
+    x[2, :6] = [127, 2.5, 3.5, -2.5, 0.5, 1.5]   # scale exactly 1.0: RNE ties
+    x[3, :4] = [254, 5, 7, -3]              # scale exactly 2.0: 2.5 -> 2, 3.5 -> 4, -1.5 -> -2
+    q, s = orc.quantize_rows(x)
+    assert s[0] == np.float32(1e-8) / np.float32(127.0) and not q[0].any()
+    assert q[1, 3] == -127 and np.count_nonzero(q[1]) == 1
+    assert s[2] == 1.0 and list(q[2, :6]) == [127, 2, 4, -2, 0, 2]
+    assert s[3] == 2.0 and list(q[3, :4]) == [127, 2, 4, -2]
+
+
+def test_quantize_invariants(orc):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((64, 300)) * rng.uniform(0.01, 100, (64, 1))).astype(np.float16)
+    q, s = orc.quantize_rows(x)
+    xf = x.astype(np.float32)
+    amax = np.abs(xf).max(axis=1)
+    assert np.all(np.abs(q.astype(np.int32)) <= 127)
+    # the absmax element maps to +-127 with its sign
+    idx = np.abs(xf).argmax(axis=1)
+    assert np.all(q[np.arange(64), idx] == np.sign(xf[np.arange(64), idx]) * 127)
+    # reconstruction error at most half a step (plus float slack)
+    err = np.abs(xf - q.astype(np.float32) * s[:, None])
+    assert np.all(err <= s[:, None] * 0.5 * (1 + 1e-5))
+    # scale = amax / 127 up to one rounding
+    assert np.allclose(s, amax / 127.0, rtol=2e-7)
+    # sign preserved and monotone within a row
+    assert np.all(np.sign(q) * np.sign(xf) >= 0)
+
+
+def test_quantize_matches_numpy_float32(orc):
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((40, 1000)).astype(np.float16)
+    x[:, rng.choice(1000, 8, replace=False)] *= 20
+    q, s = orc.quantize_rows(x)
+    xf = x.astype(np.float32)
+    sc = (np.maximum(np.abs(xf).max(axis=1), np.float32(1e-8)) / np.float32(127)).astype(np.float32)
+    inv = (np.float32(1) / sc).astype(np.float32)
+    qr = np.clip(np.rint((xf * inv[:, None]).astype(np.float32)), -128, 127).astype(np.int8)
+    assert np.array_equal(s, sc) and np.array_equal(q, qr)
+
+
+# ---- dequant ----------------------------------------------------------------------
+
+def _ulp_diff(a16, b16):
+    a = a16.view(np.uint16).astype(np.int32)
+    b = b16.view(np.uint16).astype(np.int32)
+    # map sign-magnitude to a monotone integer line
+    a = np.where(a & 0x8000, 0x8000 - (a & 0x7FFF), 0x8000 + a)
+    b = np.where(b & 0x8000, 0x8000 - (b & 0x7FFF), 0x8000 + b)
+    return np.abs(a - b)
+
+
+def test_dequant_golden(orc):
+    g = golden("dequant")
+    out = orc.dequantize_bias(g["acc"], g["act_scale"], g["w_scale"], g["bias"])
+    assert _ulp_diff(out, g["out_standalone"]).max() <= 1
+    epi = orc.dequant_epilogue(g["acc"], g["act_scale"], g["w_scale"], g["bias"])
+    assert _ulp_diff(epi, g["out_epilogue"]).max() <= 1
+    # the two associations really are different functions (and both are exercised)
+    nob = orc.dequant_epilogue(g["acc"], g["act_scale"], g["w_scale"], None)
+    ref = (g["acc"].astype(np.float64) * (g["act_scale"][:, None] * g["w_scale"].astype(np.float32)[None, :])
+           .astype(np.float64)).astype(np.float16)
+    assert _ulp_diff(nob, ref).max() <= 1
+
+
+def test_dequant_bias_and_sign(orc):
+    acc = np.array([[0, 1, -1, 1000]], np.int32)
+    out = orc.dequant_epilogue(acc, np.array([0.5], np.float32), np.array([2.0] * 4, np.float16),
+                               np.array([0.25, 0.25, 0.25, -1.0], np.float16))
+    assert list(out.astype(np.float32)[0]) == [0.25, 1.25, -0.75, 999.0]
+
+
+# ---- GEMM ---------------------------------------------------------------------------
+
+def test_gemm_c1_golden(orc):
+    g = golden("c1_gemm")
+    assert np.array_equal(orc.gemm_s32(g["A"], g["B"]), g["C"])
+
+
+def test_gemm_numpy_and_closed_forms(orc):
+    rng = np.random.default_rng(5)
+    for M, K, N in [(1, 1, 1), (7, 7, 5), (33, 28, 17), (16, 8192, 4)]:
+        A = rng.integers(-128, 128, (M, K)).astype(np.int8)
+        B = rng.integers(-128, 128, (N, K)).astype(np.int8)
+        assert np.array_equal(orc.gemm_s32(A, B), (A.astype(np.int64) @ B.astype(np.int64).T).astype(np.int32))
+    K = 8192
+    ones = np.ones((2, K), np.int8)
+    assert np.all(orc.gemm_s32(ones, -ones) == -K)
+    ext = np.full((1, K), -128, np.int8)
+    assert orc.gemm_s32(ext, ext)[0, 0] == 128 * 128 * K          # 2^27, no overflow
+    # transposition check: C = A B^T, not A^T B or B A^T
+    A = np.array([[1, 2], [3, 4], [5, 6]], np.int8)
+    B = np.array([[1, 0], [0, 1]], np.int8)
+    assert np.array_equal(orc.gemm_s32(A, B), A.astype(np.int32))
+
+
+# ---- prune / pack ---------------------------------------------------------------------
+
+def test_prune_golden(orc):
+    g = golden("prune")
+    comp, meta = orc.prune_compress_24(g["W"])
+    assert np.array_equal(comp, g["comp"]) and np.array_equal(meta, g["nibbles"])
+
+
+def test_prune_known_answers(orc):
+    cases = {
+        (5, 5, 5, 5): ((5, 5), 2 | 3 << 2),         # all equal: lower indices pruned -> keep {2,3}
+        (0, 0, 0, 0): ((0, 0), 2 | 3 << 2),
+        (1, -5, 3, 0): ((-5, 3), 1 | 2 << 2),
+        (-128, 127, -127, 1): ((-128, -127), 0 | 2 << 2),   # |127| tie: index 1 pruned
+        (2, 1, 1, 0): ((2, 1), 0 | 2 << 2),          # tie between 1 and 2: index 1 pruned
+        (0, 0, 0, 9): ((0, 9), 2 | 3 << 2),
+        (7, 0, 0, 0): ((7, 0), 0 | 3 << 2),
+    }
+    for vals, (kept, nib) in cases.items():
+        comp, meta = orc.prune_compress_24(np.array([vals], np.int8))
+        assert tuple(comp[0]) == kept and meta[0] == nib, vals
+
+
+def test_prune_brute_force(orc):
+    values = [-128, -3, -1, 0, 1, 3, 127]
+    groups = np.array(list(itertools.product(values, repeat=4)), np.int8)      # 2401 groups
+    comp, meta = orc.prune_compress_24(groups.reshape(1, -1))
+    comp = comp.reshape(-1, 2)
+    for g, c, m in zip(groups, comp, meta):
+        order = sorted(range(4), key=lambda i: (abs(int(g[i])), i))
+        keep = sorted(order[2:])
+        assert m == (keep[0] | keep[1] << 2)
+        assert c[0] == g[keep[0]] and c[1] == g[keep[1]]
+    # decompress round trip
+    dense = orc.decompress_24(comp.reshape(1, -1), meta, 1, groups.size)
+    for g, d in zip(groups, dense.reshape(-1, 4)):
+        order = sorted(range(4), key=lambda i: (abs(int(g[i])), i))
+        exp = g.copy()
+        exp[order[0]] = 0
+        exp[order[1]] = 0
+        assert np.array_equal(d, exp)
+
+
+def test_mt19937_standard_answer(orc):
+    # C++ [rand.predef]: the 10000th invocation of a default-constructed mt19937 is 4123659995
+    assert orc.mt19937(5489, 10000)[-1] == 4123659995
+    assert orc.mt19937(5489, 10000)[-1] == golden("pack")["mt19937_5489_10000"][0]
+
+
+def test_pack_reference_vectors(orc):
+    g = golden("pack")
+    raw = g["raw"]
+    # the reference test's input: std::mt19937(42) & 0xF (tests/test_pack_metadata.cu:124-126)
+    assert np.array_equal((orc.mt19937(42, raw.size) & 0xF).astype(np.uint8), raw)
+    words = orc.pack_metadata_ref(raw, 16, 128)
+    assert np.array_equal(words, g["words"])
+    gfx = orc.pack_metadata_gfx950(raw, 16, 128)
+    assert np.array_equal(gfx, g["gfx950"])
+    assert np.array_equal(orc.unpack_metadata_gfx950(gfx, 16, 128), raw)
+    # the gfx950 buffer is a permutation of the reference words
+    assert np.array_equal(np.sort(gfx), np.sort(words.ravel()))
+
+
+def test_pack_ragged_rows(orc):
+    g = golden("pack")
+    raw = g["raw_ragged"]
+    gfx = orc.pack_metadata_gfx950(raw, 20, 96)
+    assert np.array_equal(gfx, g["gfx950_ragged"])
+    assert np.array_equal(orc.unpack_metadata_gfx950(gfx, 20, 96), raw)
+
+
+def test_sparse_gemm_golden_and_dense_equivalence(orc):
+    g = golden("sparse")
+    comp, meta = orc.prune_compress_24(g["W"])
+    assert np.array_equal(comp, g["comp"]) and np.array_equal(meta, g["nibbles"])
+    C = orc.sparse_gemm_s32(comp, g["x"], meta, 32, 128)
+    assert np.array_equal(C, g["C"])
+    # sparse == dense GEMM of the decompressed weights, computed by numpy
+    rng = np.random.default_rng(9)
+    W = rng.integers(-127, 128, (48, 256)).astype(np.int8)
+    x = rng.integers(-127, 128, (5, 256)).astype(np.int8)
+    comp, meta = orc.prune_compress_24(W)
+    dense = orc.decompress_24(comp, meta, 48, 256)
+    assert np.array_equal(orc.sparse_gemm_s32(comp, x, meta, 48, 256),
+                          (x.astype(np.int64) @ dense.astype(np.int64).T).astype(np.int32))
+    # exactly two nonzeros survive per group of 4 when the weights have no zeros
+    Wn = np.where(W == 0, 1, W).astype(np.int8)
+    comp, meta = orc.prune_compress_24(Wn)
+    d = orc.decompress_24(comp, meta, 48, 256).reshape(48, 64, 4)
+    assert np.all((d != 0).sum(axis=2) == 2)
+
+
+# ---- conv -----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["3x3_p1", "2x2_s2", "3x3_d2"])
+def test_conv_golden(orc, name):
+    g = golden("conv")
+    pad, stride, dil = (int(v) for v in g[name + "_cfg"])
+    out = orc.conv2d_nhwc_s32(g[name + "_x"], g[name + "_w"], (pad, pad), (stride, stride), (dil, dil))
+    assert np.array_equal(out, g[name + "_out"])
+
+
+def test_conv_matches_torch_asymmetric(orc):
+    import torch
+    rng = np.random.default_rng(11)
+    x = rng.integers(-127, 128, (2, 9, 6, 16)).astype(np.int8)
+    w = rng.integers(-127, 128, (5, 3, 2, 16)).astype(np.int8)
+    out = orc.conv2d_nhwc_s32(x, w, (1, 0), (2, 1), (1, 2))
+    ref = torch.nn.functional.conv2d(torch.from_numpy(x).permute(0, 3, 1, 2).double(),
+                                     torch.from_numpy(w).permute(0, 3, 1, 2).double(),
+                                     stride=(2, 1), padding=(1, 0), dilation=(1, 2))
+    assert np.array_equal(out, ref.permute(0, 2, 3, 1).numpy().astype(np.int32))
