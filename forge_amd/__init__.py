@@ -11,7 +11,9 @@ __all__ = ["ForgeError", "LIB_PATH", "load", "ops"]
 
 
 def __getattr__(name):
+    # importlib (not `from . import ops`): the from-import would probe this hook again
+    # through hasattr() before the submodule is bound, and recurse.
     if name == "ops":
-        from . import ops
-        return ops
+        import importlib
+        return importlib.import_module(".ops", __name__)
     raise AttributeError(name)

@@ -19,8 +19,9 @@ constexpr int kSkWaves = 4;
 constexpr int kSkUnroll = 4;
 constexpr int kSkStep = 128;   // K bytes per wave step
 
-__device__ __forceinline__ int4 ld16_guard(const int8_t* p, int k, int K) {
-    return (k < K) ? *reinterpret_cast<const int4*>(p + k) : make_int4(0, 0, 0, 0);
+// 16 bytes at row[k], or zeros when k >= K (K % 16 == 0, so a chunk is all in or all out).
+__device__ __forceinline__ int4 ld16_guard(const int8_t* row, int k, int K) {
+    return (k < K) ? *reinterpret_cast<const int4*>(row + k) : make_int4(0, 0, 0, 0);
 }
 
 __device__ __forceinline__ v4i as_v4i(int4 v) {
@@ -42,8 +43,8 @@ __global__ __launch_bounds__(kSkWaves * kWave) void gemm_skinny_kernel(
     const int M = ep.M, N = ep.N;
     const bool arow = r < M;
     const bool brow = (n0 + r) < N;
-    const int8_t* pa = A + static_cast<size_t>(arow ? r : 0) * K + kq;
-    const int8_t* pb = B + static_cast<size_t>(brow ? n0 + r : n0) * K + kq;
+    const int8_t* pa = A + static_cast<size_t>(arow ? r : 0) * K;
+    const int8_t* pb = B + static_cast<size_t>(brow ? n0 + r : n0) * K;
 
     v4i acc = {0, 0, 0, 0};
     const int steps = (K + kSkStep - 1) / kSkStep;
@@ -51,12 +52,11 @@ __global__ __launch_bounds__(kSkWaves * kWave) void gemm_skinny_kernel(
         int4 wb[kSkUnroll][2], xa[kSkUnroll][2];
 #pragma unroll
         for (int u = 0; u < kSkUnroll; u++) {
-            const int k = (s0 + u) * kSkStep;
-            const int kl = k + kq;
-            wb[u][0] = brow ? ld16_guard(pb + k, kl, K) : make_int4(0, 0, 0, 0);
-            wb[u][1] = brow ? ld16_guard(pb + k + 16, kl + 16, K) : make_int4(0, 0, 0, 0);
-            xa[u][0] = arow ? ld16_guard(pa + k, kl, K) : make_int4(0, 0, 0, 0);
-            xa[u][1] = arow ? ld16_guard(pa + k + 16, kl + 16, K) : make_int4(0, 0, 0, 0);
+            const int kl = (s0 + u) * kSkStep + kq;
+            wb[u][0] = brow ? ld16_guard(pb, kl, K) : make_int4(0, 0, 0, 0);
+            wb[u][1] = brow ? ld16_guard(pb, kl + 16, K) : make_int4(0, 0, 0, 0);
+            xa[u][0] = arow ? ld16_guard(pa, kl, K) : make_int4(0, 0, 0, 0);
+            xa[u][1] = arow ? ld16_guard(pa, kl + 16, K) : make_int4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int u = 0; u < kSkUnroll; u++) {

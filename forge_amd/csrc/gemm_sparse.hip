@@ -10,11 +10,14 @@
 // accumulator block is C[n][m]; lane l holds rows n = 4*(l/16)+e (e = 0..3) of token
 // column m = l%16, i.e. 4 consecutive outputs of one row of Y -> one 8-byte FP16 (or
 // 16-byte INT32) store.
-// Lane operand ownership per 128-deep K step (lane l, g = l/16 selects a 32-deep K slice):
-//   A: 16 compressed bytes of weight row l%16 covering dense K [32g, 32g+32)
-//   B: 32 bytes of token row l%16, K [32g, 32g+32)
-//   index: the reference metadata word (row l%16, 32-K chunk 4s+g): nibble j (bits 4j..4j+3)
-//          holds the two kept positions of the j-th group of 4.
+// Lane operand ownership per 128-deep K step (lane l, g = l/16), as measured on gfx950 with
+// one-hot operands:
+//   A: 16 compressed bytes of weight row l%16 covering dense K [32g, 32g+32); compressed
+//      byte pair q is the q-th group of 4 of that range
+//   index: the lane's own VGPR, the reference metadata word (row l%16, 32-K chunk 4s+g):
+//          nibble q (bits 4q..4q+3) holds the two kept positions of the q-th group
+//   B: 32 bytes of token row l%16: bytes 0-15 = K [16g, 16g+16), bytes 16-31 =
+//      K [64+16g, 64+16g+16) (two 64-deep halves, each in the dense 16x16x64 layout)
 // pack_metadata stores exactly these words so that a wave's 64 index words are one
 // contiguous 256-byte run (sparsity.hip).
 //
@@ -177,8 +180,8 @@ __global__ __launch_bounds__(WN * WM * kWave) void sparse_gemm_kernel(SparseArgs
 #pragma unroll
             for (int j = 0; j < Cfg::kTM; j++) {
                 const int r = wm + 16 * j + r16;
-                const v4i b0 = *reinterpret_cast<const v4i*>(Bs + sp_b_off(r, 2 * g));
-                const v4i b1 = *reinterpret_cast<const v4i*>(Bs + sp_b_off(r, 2 * g + 1));
+                const v4i b0 = *reinterpret_cast<const v4i*>(Bs + sp_b_off(r, g));
+                const v4i b1 = *reinterpret_cast<const v4i*>(Bs + sp_b_off(r, g + 4));
                 const v8i fb = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
 #pragma unroll
                 for (int i = 0; i < Cfg::kTN; i++)

@@ -98,3 +98,11 @@ def test_conv_workspace_size(lib):
     up = lambda b: (b + 255) // 256 * 256
     assert n == up(M * K * 2) + up(M * K) + up(M * 4) + up(M * 16 * 2)
     assert n >= M * K * 2 + M * K + M * 4 + M * 16 * 2     # at least the reference's size
+
+
+def test_ops_module_imports_like_the_gpu_tests():
+    """`from forge_amd import ops` (the form every GPU test uses) resolves on the CPU."""
+    import forge_amd
+    from forge_amd import ops
+    assert ops is forge_amd.ops
+    assert callable(ops.int8_linear) and callable(ops.sparse_int8_gemm)
