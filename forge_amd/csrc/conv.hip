@@ -3,7 +3,7 @@
 // NHWC implicit GEMM (the MI355X form of config-5 shapes): output pixels are GEMM rows
 // (M = N*Ho*Wo), output channels GEMM columns, K = kH*kW*C in (kh, kw, c) order so
 // OHWI weights are already the (Co, K) row-major B operand. The A tile is gathered
-// straight from the NHWC image by ConvLoader (16 contiguous channels per chunk, zero
+// straight from the NHWC image by ConvOperand (16 contiguous channels per chunk, zero
 // outside the padded image) into the same LDS-staged MFMA tile as the dense GEMM; no
 // im2col buffer is written. Integer sums do not depend on K order, so the INT32 stage
 // equals the reference's im2col GEMM (src/nn/int8_conv2d.cu:151-223, K order
@@ -42,12 +42,11 @@ static int conv_nhwc(const int8_t* x, const int8_t* w, const float* act_scale, c
     const long long K = static_cast<long long>(kH) * kW * C;
     if (rows > 0x7FFFFFFFLL || K > 0x7FFFFFFFLL) return FORGE_EINVAL;
     const bool vec = (C % 16 == 0) && aligned(x, 16) && aligned(w, 16);
-    ConvLoader la{x, static_cast<int>(rows), static_cast<int>(K), H, W, C, Ho, Wo, kW,
-                  padH, padW, strideH, strideW, dilH, dilW};
-    RowMajorLoader lb{w, Co, static_cast<int>(K)};
-    GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, static_cast<int>(rows), Co};
-    if (out16) return launch_gemm_tiles<true>(la, lb, ep, static_cast<int>(rows), Co, static_cast<int>(K), vec, s);
-    return launch_gemm_tiles<false>(la, lb, ep, static_cast<int>(rows), Co, static_cast<int>(K), vec, s);
+    ConvGeom g{x, static_cast<int>(rows), static_cast<int>(K), H, W, C, Ho, Wo, kW,
+               padH, padW, strideH, strideW, dilH, dilW};
+    const int vec_out = out16 ? (aligned(out16, 16) && Co % 8 == 0) : (aligned(out32, 16) && Co % 4 == 0);
+    GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, static_cast<int>(rows), Co, vec_out ? 1 : 0};
+    return launch_conv_gemm(g, w, ep, Co, vec, s);
 }
 
 // Patch gather for the NCHW API: col[p][k], p = ho*Wo + wo, k = ci*kH*kW + kh*kW + kw

@@ -2,18 +2,9 @@
 #pragma once
 
 #include "common.h"
+#include "mfma_tile.h"
 
 namespace forge_amd {
-
-// Output of a GEMM: exactly one of c32 (INT32) or c16 (dequantized FP16) is non-null.
-struct GemmEpilogue {
-    int32_t* c32;
-    uint16_t* c16;
-    const float* act_scale;     // (M,)  FP16 mode only
-    const uint16_t* w_scale;    // (N,)
-    const uint16_t* bias;       // (N,) or nullptr
-    int M, N;
-};
 
 // Rows at or below which the weight-streaming skinny kernel serves the dense GEMM.
 constexpr int kSkinnyMaxM = 16;
@@ -29,8 +20,8 @@ int gemm_dense(const int8_t* A, const int8_t* B, const float* act_scale, const u
 int launch_gemm_skinny(const int8_t* A, const int8_t* B, const GemmEpilogue& ep, int M, int K, int N,
                        hipStream_t s);
 
-template <bool DEQUANT, class ALoader>
-int launch_gemm_tiles(const ALoader& la, const struct RowMajorLoader& lb, const GemmEpilogue& ep,
-                      int M, int N, int K, bool vec, hipStream_t s);
+// Implicit-GEMM NHWC conv through the dense tile engine (conv.hip supplies the geometry).
+int launch_conv_gemm(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep, int Co, bool vec,
+                     hipStream_t s);
 
 }  // namespace forge_amd

@@ -5,8 +5,10 @@
 // unpipelined global->smem loads) and src/gemm/int8_gemm.cu:12-46 (dispatch). The
 // epilogue arithmetic follows int8_dense.cu:171-174:
 //     Y[m,n] = half(fma((float)acc, act_scale[m] * w_scale[n], bias[n]))
-// The tile engine (mfma_tile.h) stages 64-byte K slices through swizzled LDS with one
-// barrier per stage; tiles are mapped XCD-aware. Skinny M (decode) goes to gemm_skinny.
+// Row-major operands with K % 128 == 0 run on the DMA engine (global_load_lds into a
+// 2-slot LDS ring); other shapes and the conv gather on the register-staged engine
+// (mfma_tile.h).
+// Tiles are mapped XCD-aware. Skinny M (decode) goes to gemm_skinny.
 #include "common.h"
 #include "mfma_tile.h"
 #include "gemm_dense.h"
@@ -18,94 +20,176 @@
 
 namespace forge_amd {
 
-template <int BM, int BN, int WM, int WN, bool DEQUANT, class ALoader>
-__global__ __launch_bounds__(WM * WN * kWave) void gemm_tile_kernel(
-    ALoader la, RowMajorLoader lb, GemmEpilogue ep, int tiles_m, int tiles_n, int K, int vec)
+// LDS bytes a tile needs: its K loop or the epilogue staging, whichever is larger.
+template <class Tile, int BM, int BN, bool DEQUANT>
+constexpr int tile_lds_bytes() {
+    constexpr int epi = epilogue_lds_bytes<BM, BN, DEQUANT>();
+    return Tile::kLdsBytes > epi ? Tile::kLdsBytes : epi;
+}
+
+// Register-staged engine: any operand type (row-major, conv gather, byte gathers).
+template <int BM, int BN, bool EVEN_K, bool DEQUANT, class OpA, class OpB>
+__global__ __launch_bounds__(kGemmThreads) void gemm_nt_kernel(
+    OpA opa, OpB opb, GemmEpilogue ep, int tiles_m, int tiles_n, int K)
 {
     extern __shared__ __align__(16) int8_t lds[];
-    using Tile = MfmaTile<BM, BN, WM, WN>;
     int tm, tn;
     tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    Tile t;
-    t.run(la, lb, m0, n0, K, vec != 0, lds);
-
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const int wm = m0 + (wave / WN) * (BM / WM);
-    const int wn = n0 + (wave % WN) * (BN / WN);
-#pragma unroll
-    for (int j = 0; j < Tile::kTN; j++) {
-        const int col = wn + 32 * j + acc_col(lane);
-        if (col >= ep.N) continue;
-        float ws = 0.0f, b = 0.0f;
-        if constexpr (DEQUANT) {
-            ws = h2f(ep.w_scale[col]);
-            if (ep.bias) b = h2f(ep.bias[col]);
-        }
-#pragma unroll
-        for (int i = 0; i < Tile::kTM; i++) {
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const int row = wm + 32 * i + acc_row(e, lane);
-                if (row >= ep.M) continue;
-                const size_t o = static_cast<size_t>(row) * ep.N + col;
-                if constexpr (DEQUANT)
-                    ep.c16[o] = dequant_gemm(t.acc[i][j][e], ep.act_scale[row], ws, b, ep.bias != nullptr);
-                else
-                    ep.c32[o] = t.acc[i][j][e];
-            }
-        }
-    }
+    NtTile<BM, BN> t;
+    t.template run<EVEN_K>(opa, opb, m0, n0, K, lds);
+    store_tile<BM, BN, DEQUANT>(t.acc, ep, m0, n0, lds);
 }
 
-template <int BM, int BN, int WM, int WN, bool DEQUANT, class ALoader>
-static int launch_tile(const ALoader& la, const RowMajorLoader& lb, const GemmEpilogue& ep,
-                       int M, int N, int K, bool vec, hipStream_t s)
+// DMA engine: row-major operands, K % 128 == 0, 16-byte aligned.
+template <int BM, int BN, bool DEQUANT>
+__global__ __launch_bounds__(kGemmThreads) void gemm_dma_kernel(
+    const int8_t* __restrict__ A, const int8_t* __restrict__ B, GemmEpilogue ep, int tiles_m, int tiles_n, int K)
 {
-    using Tile = MfmaTile<BM, BN, WM, WN>;
+    extern __shared__ __align__(16) int8_t lds[];
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    DmaTile<BM, BN> t;
+    t.run(A, B, ep.M, ep.N, K, m0, n0, lds);
+    store_tile<BM, BN, DEQUANT>(t.acc, ep, m0, n0, lds);
+}
+
+// Raises a kernel's dynamic-LDS limit once (host-side attribute; safe under graph capture).
+template <class Kern>
+static int allow_lds(Kern kern, int bytes) {
+    if (bytes <= 65536) return FORGE_OK;
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    return e == hipSuccess ? FORGE_OK : static_cast<int>(e);
+}
+
+template <int BM, int BN, bool EVEN_K, bool DEQUANT, class OpA, class OpB>
+static int launch_tile(const OpA& opa, const OpB& opb, const GemmEpilogue& ep, int M, int N, int K,
+                       hipStream_t s)
+{
+    constexpr int lds = tile_lds_bytes<NtTile<BM, BN>, BM, BN, DEQUANT>();
     const int tiles_m = divup(M, BM), tiles_n = divup(N, BN);
     const long long total = static_cast<long long>(tiles_m) * tiles_n;
     if (total > 0x7FFFFFFFLL) return FORGE_EINVAL;
-    gemm_tile_kernel<BM, BN, WM, WN, DEQUANT, ALoader>
-        <<<static_cast<unsigned>(total), Tile::kThreads, Tile::kLdsBytes, s>>>(
-            la, lb, ep, tiles_m, tiles_n, K, vec ? 1 : 0);
+    auto kern = gemm_nt_kernel<BM, BN, EVEN_K, DEQUANT, OpA, OpB>;
+    static const int attr = allow_lds(kern, lds);
+    if (attr != FORGE_OK) return attr;
+    gemm_nt_kernel<BM, BN, EVEN_K, DEQUANT, OpA, OpB>
+        <<<static_cast<unsigned>(total), kGemmThreads, lds, s>>>(opa, opb, ep, tiles_m, tiles_n, K);
     return launch_status();
 }
 
-// Picks the largest tile that still gives every CU a workgroup.
-template <bool DEQUANT, class ALoader>
-int launch_gemm_tiles(const ALoader& la, const RowMajorLoader& lb, const GemmEpilogue& ep,
-                      int M, int N, int K, bool vec, hipStream_t s)
+template <int BM, int BN, bool DEQUANT>
+static int launch_dma(const int8_t* A, const int8_t* B, const GemmEpilogue& ep, int M, int N, int K,
+                      hipStream_t s)
 {
-    int st = FORGE_OK;
-    const DeviceInfo& d = device_info(&st);
-    if (st != FORGE_OK) return st;
-    const long long t256 = static_cast<long long>(divup(M, 256)) * divup(N, 256);
-    const long long t128 = static_cast<long long>(divup(M, 128)) * divup(N, 128);
-    if (t256 >= d.cu_count)
-        return launch_tile<256, 256, 2, 2, DEQUANT>(la, lb, ep, M, N, K, vec, s);
-    if (t128 >= d.cu_count / 2)
-        return launch_tile<128, 128, 2, 2, DEQUANT>(la, lb, ep, M, N, K, vec, s);
-    return launch_tile<64, 64, 2, 2, DEQUANT>(la, lb, ep, M, N, K, vec, s);
+    constexpr int lds = tile_lds_bytes<DmaTile<BM, BN>, BM, BN, DEQUANT>();
+    const int tiles_m = divup(M, BM), tiles_n = divup(N, BN);
+    const long long total = static_cast<long long>(tiles_m) * tiles_n;
+    if (total > 0x7FFFFFFFLL) return FORGE_EINVAL;
+    auto kern = gemm_dma_kernel<BM, BN, DEQUANT>;
+    static const int attr = allow_lds(kern, lds);
+    if (attr != FORGE_OK) return attr;
+    gemm_dma_kernel<BM, BN, DEQUANT><<<static_cast<unsigned>(total), kGemmThreads, lds, s>>>(A, B, ep, tiles_m, tiles_n, K);
+    return launch_status();
 }
 
-template int launch_gemm_tiles<true, ConvLoader>(const ConvLoader&, const RowMajorLoader&,
-                                                 const GemmEpilogue&, int, int, int, bool, hipStream_t);
-template int launch_gemm_tiles<false, ConvLoader>(const ConvLoader&, const RowMajorLoader&,
-                                                  const GemmEpilogue&, int, int, int, bool, hipStream_t);
+// Tile choice: the largest tile whose grid still covers the chip's CUs; smaller tiles
+// trade MFMA efficiency (operand reuse) for parallelism.
+enum class TileCfg { k256, k128, k64 };
+
+static TileCfg pick_tile(int M, int N, int cu) {
+    const long long t256 = static_cast<long long>(divup(M, 256)) * divup(N, 256);
+    const long long t128 = static_cast<long long>(divup(M, 128)) * divup(N, 128);
+    if (t256 * 2 >= cu) return TileCfg::k256;
+    if (t128 * 2 >= cu) return TileCfg::k128;
+    return TileCfg::k64;
+}
+
+static int cu_count(int* st) {
+    const DeviceInfo& d = device_info(st);
+    return d.cu_count;
+}
+
+// MAX256: whether the 256 x 256 tile may be used (the byte-gather operands of odd shapes
+// would spill registers at that size).
+template <bool EVEN_K, bool DEQUANT, bool MAX256 = true, class OpA, class OpB>
+static int dispatch_tiles(const OpA& opa, const OpB& opb, const GemmEpilogue& ep, int M, int N, int K,
+                          hipStream_t s)
+{
+    int st = FORGE_OK;
+    const int cu = cu_count(&st);
+    if (st != FORGE_OK) return st;
+    TileCfg t = pick_tile(M, N, cu);
+    if constexpr (MAX256) {
+        if (t == TileCfg::k256) return launch_tile<256, 256, EVEN_K, DEQUANT>(opa, opb, ep, M, N, K, s);
+    } else {
+        if (t == TileCfg::k256) t = TileCfg::k128;
+    }
+    if (t == TileCfg::k128) return launch_tile<128, 128, EVEN_K, DEQUANT>(opa, opb, ep, M, N, K, s);
+    return launch_tile<64, 64, EVEN_K, DEQUANT>(opa, opb, ep, M, N, K, s);
+}
+
+template <bool DEQUANT, class OpA, class OpB>
+static int dispatch_k(const OpA& opa, const OpB& opb, const GemmEpilogue& ep, int M, int N, int K,
+                      bool even_k, hipStream_t s)
+{
+    if (even_k) return dispatch_tiles<true, DEQUANT>(opa, opb, ep, M, N, K, s);
+    return dispatch_tiles<false, DEQUANT>(opa, opb, ep, M, N, K, s);
+}
+
+int launch_conv_gemm(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep, int Co, bool vec,
+                     hipStream_t s)
+{
+    const int M = g.rows, K = g.K;
+    if (vec) {
+        ConvOperand a;
+        static_cast<ConvGeom&>(a) = g;
+        RowMajorOperand b{w, Co, K};
+        const bool even = K % kBK == 0;
+        return ep.c16 ? dispatch_k<true>(a, b, ep, M, Co, K, even, s)
+                      : dispatch_k<false>(a, b, ep, M, Co, K, even, s);
+    }
+    ConvBytes a;
+    static_cast<ConvGeom&>(a) = g;
+    RowMajorBytes b{w, Co, K};
+    return ep.c16 ? dispatch_tiles<false, true, false>(a, b, ep, M, Co, K, s)
+                  : dispatch_tiles<false, false, false>(a, b, ep, M, Co, K, s);
+}
+
+// Whether 16-byte row stores of the output are possible.
+static int out_vec(const void* out, int N, int esz) {
+    return aligned(out, 16) && (static_cast<long long>(N) * esz) % 16 == 0 ? 1 : 0;
+}
 
 int gemm_dense(const int8_t* A, const int8_t* B, const float* act_scale, const uint16_t* w_scale,
                const uint16_t* bias, uint16_t* out16, int32_t* out32, int M, int K, int N,
                hipStream_t s)
 {
     const bool vec = (K % 16 == 0) && aligned(A, 16) && aligned(B, 16);
-    GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N};
+    GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N,
+                    out16 ? out_vec(out16, N, 2) : out_vec(out32, N, 4)};
     if (M <= kSkinnyMaxM && vec)
         return launch_gemm_skinny(A, B, ep, M, K, N, s);
-    RowMajorLoader la{A, M, K}, lb{B, N, K};
-    if (out16) return launch_gemm_tiles<true>(la, lb, ep, M, N, K, vec, s);
-    return launch_gemm_tiles<false>(la, lb, ep, M, N, K, vec, s);
+    if (vec && K % kBK == 0) {
+        int st = FORGE_OK;
+        const int cu = cu_count(&st);
+        if (st != FORGE_OK) return st;
+        const TileCfg t = pick_tile(M, N, cu);
+        if (t == TileCfg::k256)
+            return out16 ? launch_dma<256, 256, true>(A, B, ep, M, N, K, s) : launch_dma<256, 256, false>(A, B, ep, M, N, K, s);
+        if (t == TileCfg::k128)
+            return out16 ? launch_dma<128, 128, true>(A, B, ep, M, N, K, s) : launch_dma<128, 128, false>(A, B, ep, M, N, K, s);
+    }
+    if (vec) {
+        RowMajorOperand a{A, M, K}, b{B, N, K};
+        const bool even = K % kBK == 0;
+        return out16 ? dispatch_k<true>(a, b, ep, M, N, K, even, s) : dispatch_k<false>(a, b, ep, M, N, K, even, s);
+    }
+    RowMajorBytes a{A, M, K}, b{B, N, K};
+    return out16 ? dispatch_tiles<false, true, false>(a, b, ep, M, N, K, s)
+                 : dispatch_tiles<false, false, false>(a, b, ep, M, N, K, s);
 }
 
 }  // namespace forge_amd

@@ -1,194 +1,537 @@
-// LDS-staged INT8 MFMA tile engine for gfx950 (v_mfma_i32_32x32x32_i8).
+// LDS-staged INT8 MFMA GEMM engines for gfx950 (v_mfma_i32_32x32x32_i8).
 //
-// One workgroup computes a BM x BN INT32 tile of C = A (rows, K) x B (cols, K)^T with
-// both operands K-contiguous ("NT", the layout of the reference's int8 GEMMs:
-// include/forge/gemm/int8_dense.cuh:9-11). WM x WN wavefronts each own a
-// (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks held in accumulator registers.
+// One 256-thread workgroup (4 wavefronts in a 2 x 2 grid) computes a BM x BN INT32 tile of
+// C = A (rows, K) x B (cols, K)^T with both operands K-contiguous ("NT", the layout of the
+// reference's int8 GEMMs: include/forge/gemm/int8_dense.cuh:9-11). Each wavefront owns a
+// (BM/2) x (BN/2) sub-tile of 32x32 MFMA blocks whose accumulators stay in registers for
+// the whole K loop.
 //
-// K advances in 64-byte stages. A and B stages live in LDS as rows of 64 bytes (four
-// 16-byte chunks); chunk c of row r is stored at chunk position c ^ swz(r), with
-// swz(r) = ((r >> 1) ^ (r >> 3)) & 3. An MFMA operand read (lane l -> row l%32,
-// chunk 2*ks + l/32, one ds_read_b128) then touches 8 (or 16) distinct 16-byte bank
-// groups per 8-lane (16-lane) phase: bank-conflict free for 32 or 64 banks, and the
-// 16-byte ds_write_b128 stores of a stage are conflict free as well.
+// Operand roles: the MFMA computes D[n][m] = sum_k B[n][k] A[m][k] (B rows are the MFMA's
+// A operand). Its accumulator layout (lane l, register e = 0..15: row 8*(e/4) + 4*(l/32) +
+// e%4, col l%32) then gives every lane FOUR CONSECUTIVE OUTPUT COLUMNS n of one output row
+// m per register quad: 8 contiguous bytes of FP16 or 16 of INT32 per store.
 //
-// Two LDS buffers and register prefetch: the global loads of stage k+1 are issued
-// before the MFMAs of stage k and written to the other buffer after them, so one
-// barrier per stage orders everything.
+// Operand K mapping: for each 32-K sub-step, lane l supplies 16 bytes of row l%32 at K
+// offset 16*(l/32); both operands use the same (lane, byte) -> k assignment, so every
+// INT32 dot product is exact.
 //
-// Operand K mapping: for MFMA operands A (32 rows x 32 K) and B (32 cols x 32 K) each
-// lane supplies 16 bytes; lanes l and l+32 cover the two 16-byte halves of the 32-K
-// sub-step. A and B use the same (lane, byte) -> k assignment, and an integer dot
-// product is invariant under a common permutation of k, so results are exact whatever
-// order the hardware uses inside a lane.
-// Accumulator layout of a 32x32 block (lane l, register e = 0..15):
-//     row = 8*(e/4) + 4*(l/32) + (e%4),  col = l%32.
+// Two K-loop engines share that layout and the epilogue:
+//
+// DmaTile (K % 128 == 0, 16-byte aligned row-major operands; the hot path): 128-byte K
+// stages in two LDS slots, filled by gfx950's global_load_lds_dwordx4 (each lane's 16
+// bytes land at M0 + 16*lane, no VGPR staging). Every row of a stage is one full 128-byte
+// cache line read by 8 consecutive lanes; on gfx950 this sustains ~30 B/clk per CU into
+// LDS, against ~26 B/clk for 64-byte half-line rows, whatever the number of stages in
+// flight. Stage kt+1 streams in while stage kt is multiplied; MFMA fragments are
+// double-buffered in registers (sub-step ks+1 loads during sub-step ks), and the last
+// sub-step of stage kt runs after the barrier that publishes stage kt+1, hiding that
+// stage's first LDS reads. Synchronisation is explicit: one s_waitcnt vmcnt(0) lgkmcnt(0)
+// (this wave's DMAs landed, its reads of the old slot done) and one s_barrier per stage.
+// LDS rows are 8 chunks with the (r ^ (r >> 3)) & 7 swizzle below; the DMA lanes are
+// assigned (row, chunk) pairs so that each 1 KB DMA write lands exactly in that layout.
+//
+// NtTile (any K % 16 == 0 operand, including the implicit-im2col conv gather with zero
+// padding, and the byte-gather operands of odd shapes): 128-byte K stages through two LDS
+// buffers with one stage of register staging; rows of 8 chunks, swizzle (r ^ (r >> 3)) & 7.
+//
+// Edges: operand rows beyond the matrix are clamped to its last row (their products land in
+// accumulator entries that are never stored); the epilogue masks rows and columns.
 #pragma once
 
 #include "common.h"
 
 namespace forge_amd {
 
-constexpr int kBK = 64;   // K bytes per pipeline stage
+constexpr int kGemmThreads = 256;
 
-__device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
-__device__ __forceinline__ int lds_off(int r, int c) { return r * kBK + ((c ^ lds_swz(r)) << 4); }
+__device__ __forceinline__ int4 zero4() { return make_int4(0, 0, 0, 0); }
 
-__device__ __forceinline__ int acc_row(int e, int lane) { return 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3); }
-__device__ __forceinline__ int acc_col(int lane) { return lane & 31; }
+// Compiler-only memory fence: keeps LDS accesses on their side of a barrier, emits nothing.
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
-// ---- operand loaders: fetch one 16-byte chunk (row r of the tile, chunk c of stage k0) ----
+// s_waitcnt vmcnt(N) only (expcnt and lgkmcnt left unconstrained). gfx9 encodes the 6-bit
+// vmcnt as bits [3:0] and [15:14] of the immediate.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
 
-// Row-major (rows, K) int8 matrix; vector path needs K % 16 == 0 and a 16-byte base.
-struct RowMajorLoader {
+// 16-byte global -> LDS DMA (global_load_lds_dwordx4): this lane's 16 bytes at `src` land at
+// lds_base + 16 * lane; lds_base must be wave-uniform (it goes to M0). A plain __device__
+// function, so the host pass never sees the device-only builtin inside kernel templates.
+__device__ __forceinline__ void dma16(const int8_t* src, int8_t* lds_base) {
+    __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
+}
+
+// Workgroup barrier without the memory fence of __syncthreads (which would also drain the
+// LDS DMAs still in flight for later stages).
+__device__ __forceinline__ void lds_barrier() {
+    compiler_fence();
+    __builtin_amdgcn_s_barrier();
+    compiler_fence();
+}
+
+// ---- operands of the register-staged engine: per-thread row state + 16-byte chunk loads ----
+
+// Row-major (rows, K) int8 matrix; needs K % 16 == 0 and a 16-byte aligned base.
+struct RowMajorOperand {
     const int8_t* p;
-    int rows;   // valid rows
+    int rows;
     int K;
-    __device__ __forceinline__ int4 load(int row, int k, bool vec) const {
-        if (row >= rows || k >= K) return make_int4(0, 0, 0, 0);
-        const int8_t* src = p + static_cast<size_t>(row) * K + k;
-        if (vec) return *reinterpret_cast<const int4*>(src);
-        int4 v = make_int4(0, 0, 0, 0);
-        int8_t* b = reinterpret_cast<int8_t*>(&v);
-        const int n = (K - k) < 16 ? (K - k) : 16;
-        for (int i = 0; i < n; i++) b[i] = src[i];
-        return v;
+    struct Row { const int8_t* base; };
+    __device__ __forceinline__ Row row(int r) const {
+        r = r < rows ? r : rows - 1;
+        return Row{p + static_cast<size_t>(r) * K};
+    }
+    // Chunk [k, k+16) of the row; zeros when k >= K (only possible when K % 128 != 0).
+    template <bool EVEN_K>
+    __device__ __forceinline__ int4 load(const Row& rw, int k) const {
+        if constexpr (EVEN_K) {
+            return *reinterpret_cast<const int4*>(rw.base + k);
+        } else {
+            const int4 v = *reinterpret_cast<const int4*>(rw.base + (k < K ? k : K - 16));
+            return k < K ? v : zero4();
+        }
     }
 };
 
-// Implicit im2col of an NHWC int8 image: row = output pixel (n, ho, wo), k = (kh*kW+kw)*C + c.
-// Vector path needs C % 16 == 0 (a chunk never straddles two taps) and a 16-byte base.
-struct ConvLoader {
+// Row-major (rows, K) int8 matrix of any K and alignment (byte gathers; odd shapes only).
+struct RowMajorBytes {
+    const int8_t* p;
+    int rows;
+    int K;
+    struct Row { const int8_t* base; };
+    __device__ __forceinline__ Row row(int r) const {
+        r = r < rows ? r : rows - 1;
+        return Row{p + static_cast<size_t>(r) * K};
+    }
+    template <bool EVEN_K>
+    __device__ __forceinline__ int4 load(const Row& rw, int k) const {
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t b = (k + i < K) ? static_cast<uint8_t>(rw.base[k + i]) : 0u;
+            w[i >> 2] |= b << (8 * (i & 3));
+        }
+        return make_int4(static_cast<int>(w[0]), static_cast<int>(w[1]), static_cast<int>(w[2]),
+                         static_cast<int>(w[3]));
+    }
+};
+
+// Implicit im2col of an NHWC int8 image: operand row = output pixel (n, ho, wo), k =
+// (kh*kW + kw)*C + c.
+struct ConvGeom {
     const int8_t* x;
     int rows;   // N * Ho * Wo
     int K;      // kH * kW * C
     int H, W, C, Ho, Wo, kW;
     int padH, padW, strideH, strideW, dilH, dilW;
-    __device__ __forceinline__ int4 load(int row, int k, bool vec) const {
-        int4 v = make_int4(0, 0, 0, 0);
-        if (row >= rows || k >= K) return v;
-        const int wo = row % Wo;
-        const int t0 = row / Wo;
-        const int ho = t0 % Ho;
-        const int n = t0 / Ho;
-        if (vec) {
-            const int tap = k / C, c = k - tap * C;
-            const int kh = tap / kW, kw = tap - kh * kW;
-            const int hi = ho * strideH + kh * dilH - padH;
-            const int wi = wo * strideW + kw * dilW - padW;
-            if (hi < 0 || hi >= H || wi < 0 || wi >= W) return v;
-            return *reinterpret_cast<const int4*>(x + ((static_cast<size_t>(n) * H + hi) * W + wi) * C + c);
-        }
-        int8_t* b = reinterpret_cast<int8_t*>(&v);
-        for (int i = 0; i < 16 && k + i < K; i++) {
+};
+
+// Needs C % 16 == 0 (a chunk never straddles two taps) and a 16-byte aligned image.
+struct ConvOperand : ConvGeom {
+    struct Row { const int8_t* img; int hb, wb; };
+    __device__ __forceinline__ Row row(int r) const {
+        r = r < rows ? r : rows - 1;
+        const int wo = r % Wo;
+        const int t = r / Wo;
+        const int ho = t % Ho;
+        const int n = t / Ho;
+        return Row{x + static_cast<size_t>(n) * H * W * C, ho * strideH - padH, wo * strideW - padW};
+    }
+    template <bool EVEN_K>
+    __device__ __forceinline__ int4 load(const Row& rw, int k) const {
+        const int tap = k / C, c = k - tap * C;
+        const int kh = tap / kW, kw = tap - kh * kW;
+        const int hi = rw.hb + kh * dilH, wi = rw.wb + kw * dilW;
+        const bool ok = (EVEN_K || k < K) && hi >= 0 && hi < H && wi >= 0 && wi < W;
+        const size_t off = ok ? (static_cast<size_t>(hi) * W + wi) * C + c : 0;
+        const int4 v = *reinterpret_cast<const int4*>(rw.img + off);
+        return ok ? v : zero4();
+    }
+};
+
+// Same geometry, any C and alignment (byte gathers; odd shapes only).
+struct ConvBytes : ConvGeom {
+    struct Row { const int8_t* img; int hb, wb; };
+    __device__ __forceinline__ Row row(int r) const {
+        r = r < rows ? r : rows - 1;
+        const int wo = r % Wo;
+        const int t = r / Wo;
+        const int ho = t % Ho;
+        const int n = t / Ho;
+        return Row{x + static_cast<size_t>(n) * H * W * C, ho * strideH - padH, wo * strideW - padW};
+    }
+    template <bool EVEN_K>
+    __device__ __forceinline__ int4 load(const Row& rw, int k) const {
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
             const int kk = k + i;
             const int tap = kk / C, c = kk - tap * C;
             const int kh = tap / kW, kw = tap - kh * kW;
-            const int hi = ho * strideH + kh * dilH - padH;
-            const int wi = wo * strideW + kw * dilW - padW;
-            if (hi >= 0 && hi < H && wi >= 0 && wi < W)
-                b[i] = x[((static_cast<size_t>(n) * H + hi) * W + wi) * C + c];
+            const int hi = rw.hb + kh * dilH, wi = rw.wb + kw * dilW;
+            const bool ok = kk < K && hi >= 0 && hi < H && wi >= 0 && wi < W;
+            const uint32_t b = ok ? static_cast<uint8_t>(rw.img[(static_cast<size_t>(hi) * W + wi) * C + c]) : 0u;
+            w[i >> 2] |= b << (8 * (i & 3));
         }
-        return v;
+        return make_int4(static_cast<int>(w[0]), static_cast<int>(w[1]), static_cast<int>(w[2]),
+                         static_cast<int>(w[3]));
     }
 };
 
-// ---- the tile engine -------------------------------------------------------------
+// ---- register-staged engine (128-byte stages, two LDS buffers) -------------------------
 
-template <int BM, int BN, int WM, int WN>
-struct MfmaTile {
-    static constexpr int kThreads = WM * WN * kWave;
-    static constexpr int kTM = BM / WM / 32;       // 32x32 blocks per wave along rows
-    static constexpr int kTN = BN / WN / 32;       // ... along cols
-    static constexpr int kAChunks = BM * 4 / kThreads;   // 16-byte chunks per thread per stage
-    static constexpr int kBChunks = BN * 4 / kThreads;
-    static constexpr int kLdsBytes = 2 * (BM + BN) * kBK;
+constexpr int kBK = 128;
+
+__device__ __forceinline__ int lds_swz8(int r) { return (r ^ (r >> 3)) & 7; }
+__device__ __forceinline__ int lds_off128(int r, int c) { return r * kBK + ((c ^ lds_swz8(r)) << 4); }
+
+template <int BM, int BN>
+struct NtTile {
+    static constexpr int kTM = BM / 2 / 32;            // 32x32 blocks per wave along rows (m)
+    static constexpr int kTN = BN / 2 / 32;            // ... along cols (n)
+    static constexpr int kAPass = BM * (kBK / 16) / kGemmThreads;   // A chunks per thread per stage
+    static constexpr int kBPass = BN * (kBK / 16) / kGemmThreads;
+    static constexpr int kRowsPerPass = kGemmThreads / (kBK / 16); // 32
+    static constexpr int kStageBytes = (BM + BN) * kBK;
+    static constexpr int kLdsBytes = 2 * kStageBytes;
     static_assert(kTM >= 1 && kTN >= 1, "wave tile must hold a 32x32 block");
-    static_assert(BM * 4 % kThreads == 0 && BN * 4 % kThreads == 0, "stage must split evenly");
+    static_assert(kAPass >= 1 && kBPass >= 1, "stage must split evenly");
 
-    v16i acc[kTM][kTN];
+    v16i acc[kTN][kTM];   // acc[j][i]: D[n][m] of block (n: 32j.., m: 32i..)
 
-    // Runs the K loop for the tile whose first row/col are (m0, n0); ALoader/BLoader are
-    // addressed with tile-relative rows offset by m0/n0.
-    template <class ALoader, class BLoader>
-    __device__ __forceinline__ void run(const ALoader& la, const BLoader& lb, int m0, int n0,
-                                        int K, bool vec, int8_t* lds) {
+    template <bool EVEN_K, class OpA, class OpB>
+    __device__ __forceinline__ void run(const OpA& opa, const OpB& opb, int m0, int n0, int K,
+                                        int8_t* lds) {
         const int tid = threadIdx.x;
         const int lane = tid & (kWave - 1);
         const int wave = tid / kWave;
-        const int wm = (wave / WN) * (BM / WM);
-        const int wn = (wave % WN) * (BN / WN);
-        int8_t* As = lds;
-        int8_t* Bs = lds + 2 * BM * kBK;
+        const int wm = (wave >> 1) * (BM / 2);
+        const int wn = (wave & 1) * (BN / 2);
+        const int cc = tid & 7;        // chunk column this thread stages
+        const int rr = tid >> 3;       // first row this thread stages
 
 #pragma unroll
-        for (int i = 0; i < kTM; i++)
+        for (int j = 0; j < kTN; j++)
 #pragma unroll
-            for (int j = 0; j < kTN; j++)
+            for (int i = 0; i < kTM; i++)
 #pragma unroll
-                for (int e = 0; e < 16; e++) acc[i][j][e] = 0;
+                for (int e = 0; e < 16; e++) acc[j][i][e] = 0;
 
-        int4 ra[kAChunks], rb[kBChunks];
-        auto gload = [&](int k0) {
+        typename OpA::Row ra[kAPass];
+        typename OpB::Row rb[kBPass];
 #pragma unroll
-            for (int i = 0; i < kAChunks; i++) {
-                const int id = tid + i * kThreads;
-                ra[i] = la.load(m0 + (id >> 2), k0 + ((id & 3) << 4), vec);
-            }
+        for (int i = 0; i < kAPass; i++) ra[i] = opa.row(m0 + rr + kRowsPerPass * i);
 #pragma unroll
-            for (int i = 0; i < kBChunks; i++) {
-                const int id = tid + i * kThreads;
-                rb[i] = lb.load(n0 + (id >> 2), k0 + ((id & 3) << 4), vec);
-            }
+        for (int i = 0; i < kBPass; i++) rb[i] = opb.row(n0 + rr + kRowsPerPass * i);
+
+        int4 sa[kAPass], sb[kBPass];
+        auto gload = [&](int kt) {
+            const int k = kt * kBK + 16 * cc;
+#pragma unroll
+            for (int i = 0; i < kAPass; i++) sa[i] = opa.template load<EVEN_K>(ra[i], k);
+#pragma unroll
+            for (int i = 0; i < kBPass; i++) sb[i] = opb.template load<EVEN_K>(rb[i], k);
         };
         auto lstore = [&](int buf) {
-            int8_t* a = As + buf * BM * kBK;
-            int8_t* b = Bs + buf * BN * kBK;
+            int8_t* As = lds + buf * kStageBytes;
+            int8_t* Bs = As + BM * kBK;
 #pragma unroll
-            for (int i = 0; i < kAChunks; i++) {
-                const int id = tid + i * kThreads;
-                *reinterpret_cast<int4*>(a + lds_off(id >> 2, id & 3)) = ra[i];
-            }
+            for (int i = 0; i < kAPass; i++)
+                *reinterpret_cast<int4*>(As + lds_off128(rr + kRowsPerPass * i, cc)) = sa[i];
 #pragma unroll
-            for (int i = 0; i < kBChunks; i++) {
-                const int id = tid + i * kThreads;
-                *reinterpret_cast<int4*>(b + lds_off(id >> 2, id & 3)) = rb[i];
-            }
+            for (int i = 0; i < kBPass; i++)
+                *reinterpret_cast<int4*>(Bs + lds_off128(rr + kRowsPerPass * i, cc)) = sb[i];
         };
 
-        const int kt_total = divup_dev(K, kBK);
+        const int kt_total = (K + kBK - 1) / kBK;
         gload(0);
         lstore(0);
+        if (kt_total > 1) gload(1);
         __syncthreads();
+        const int l31 = lane & 31;
+        const int hi = lane >> 5;
         for (int kt = 0; kt < kt_total; kt++) {
             const int cur = kt & 1;
-            const bool more = (kt + 1) < kt_total;
-            if (more) gload((kt + 1) * kBK);
-            const int8_t* a = As + cur * BM * kBK;
-            const int8_t* b = Bs + cur * BN * kBK;
+            const int8_t* As = lds + cur * kStageBytes;
+            const int8_t* Bs = As + BM * kBK;
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                const int c = 2 * ks + (lane >> 5);
+            for (int ks = 0; ks < kBK / 32; ks++) {
+                const int c = 2 * ks + hi;
                 v4i fa[kTM], fb[kTN];
 #pragma unroll
                 for (int i = 0; i < kTM; i++)
-                    fa[i] = *reinterpret_cast<const v4i*>(a + lds_off(wm + 32 * i + (lane & 31), c));
+                    fa[i] = *reinterpret_cast<const v4i*>(As + lds_off128(wm + 32 * i + l31, c));
 #pragma unroll
                 for (int j = 0; j < kTN; j++)
-                    fb[j] = *reinterpret_cast<const v4i*>(b + lds_off(wn + 32 * j + (lane & 31), c));
+                    fb[j] = *reinterpret_cast<const v4i*>(Bs + lds_off128(wn + 32 * j + l31, c));
 #pragma unroll
-                for (int i = 0; i < kTM; i++)
+                for (int j = 0; j < kTN; j++)
 #pragma unroll
-                    for (int j = 0; j < kTN; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                    for (int i = 0; i < kTM; i++)
+                        acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j], fa[i], acc[j][i], 0, 0, 0);
             }
-            if (more) lstore(cur ^ 1);
+            if (kt + 1 < kt_total) {
+                lstore(cur ^ 1);
+                if (kt + 2 < kt_total) gload(kt + 2);
+            }
             __syncthreads();
         }
     }
-
-    __device__ static __forceinline__ int divup_dev(int a, int b) { return (a + b - 1) / b; }
 };
+
+// ---- DMA engine (128-byte stages, 2-slot LDS ring, global_load_lds) ---------------------
+
+// s_waitcnt vmcnt(0) lgkmcnt(0) (expcnt unconstrained).
+__device__ __forceinline__ void wait_vm_lgkm0() { __builtin_amdgcn_s_waitcnt(0x7 << 4); }
+
+template <int BM, int BN>
+struct DmaTile {
+    static constexpr int kTM = BM / 2 / 32;
+    static constexpr int kTN = BN / 2 / 32;
+    static constexpr int kAIns = BM * (kBK / 16) / kWave / 4;   // 1 KB DMA instructions per wave per stage
+    static constexpr int kBIns = BN * (kBK / 16) / kWave / 4;
+    static constexpr int kSlotBytes = (BM + BN) * kBK;
+    static constexpr int kLdsBytes = 2 * kSlotBytes;
+    static_assert(kTM >= 1 && kTN >= 1 && kAIns >= 1 && kBIns >= 1, "tile too small");
+
+    // MFMA operand fragments of one 32-deep sub-step.
+    struct Frags {
+        v4i a[kTM];
+        v4i b[kTN];
+    };
+
+    v16i acc[kTN][kTM];
+
+    __device__ __forceinline__ void run(const int8_t* A, const int8_t* B, int M, int N, int K, int m0, int n0,
+                                        int8_t* lds) {
+        const int lane = threadIdx.x & (kWave - 1);
+        const int wave = threadIdx.x / kWave;
+        const int wm = (wave >> 1) * (BM / 2);
+        const int wn = (wave & 1) * (BN / 2);
+        const int l31 = lane & 31;
+        const int hi = lane >> 5;
+
+#pragma unroll
+        for (int j = 0; j < kTN; j++)
+#pragma unroll
+            for (int i = 0; i < kTM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[j][i][e] = 0;
+
+        // DMA instruction q of this wave fills slot chunks s = (wave*kIns + q)*64 + lane:
+        // row s/8 (8 lanes read one 128-byte line), physical chunk s%8 = logical chunk
+        // (s%8) ^ swz(row) of that row.
+        const int8_t* pa[kAIns];
+        const int8_t* pb[kBIns];
+#pragma unroll
+        for (int q = 0; q < kAIns; q++) {
+            const int s = (wave * kAIns + q) * kWave + lane;
+            const int r = s >> 3, c = (s & 7) ^ lds_swz8(r);
+            const int gr = (m0 + r) < M ? (m0 + r) : M - 1;
+            pa[q] = A + static_cast<size_t>(gr) * K + 16 * c;
+        }
+#pragma unroll
+        for (int q = 0; q < kBIns; q++) {
+            const int s = (wave * kBIns + q) * kWave + lane;
+            const int r = s >> 3, c = (s & 7) ^ lds_swz8(r);
+            const int gr = (n0 + r) < N ? (n0 + r) : N - 1;
+            pb[q] = B + static_cast<size_t>(gr) * K + 16 * c;
+        }
+        const int nst = K / kBK;
+        // Stage st into slot st % 2; stages past the end re-read the last one (their slot is
+        // never read again), so the issue needs no branch.
+        auto issue = [&](int st) {
+            int8_t* slot = lds + (st & 1) * kSlotBytes;
+            const int k0 = (st < nst ? st : nst - 1) * kBK;
+#pragma unroll
+            for (int q = 0; q < kAIns; q++) dma16(pa[q] + k0, slot + (wave * kAIns + q) * 1024);
+#pragma unroll
+            for (int q = 0; q < kBIns; q++) dma16(pb[q] + k0, slot + BM * kBK + (wave * kBIns + q) * 1024);
+        };
+        auto load_frags = [&](int st, int ks, Frags& F) {
+            const int8_t* As = lds + (st & 1) * kSlotBytes;
+            const int8_t* Bs = As + BM * kBK;
+            const int c = 2 * ks + hi;
+#pragma unroll
+            for (int i = 0; i < kTM; i++)
+                F.a[i] = *reinterpret_cast<const v4i*>(As + lds_off128(wm + 32 * i + l31, c));
+#pragma unroll
+            for (int j = 0; j < kTN; j++)
+                F.b[j] = *reinterpret_cast<const v4i*>(Bs + lds_off128(wn + 32 * j + l31, c));
+        };
+        auto mfmas = [&](const Frags& F) {
+#pragma unroll
+            for (int j = 0; j < kTN; j++)
+#pragma unroll
+                for (int i = 0; i < kTM; i++)
+                    acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(F.b[j], F.a[i], acc[j][i], 0, 0, 0);
+        };
+        // Sub-steps 0..2 of a stage: MFMAs of sub-step ks while sub-step ks+1's fragments load.
+        auto first3 = [&](int st, Frags& F0, Frags& F1) {
+            load_frags(st, 1, F1);
+            mfmas(F0);
+            load_frags(st, 2, F0);
+            mfmas(F1);
+            load_frags(st, 3, F1);
+            mfmas(F0);
+        };
+
+        issue(0);
+        wait_vm_lgkm0();
+        lds_barrier();
+        issue(1);
+        Frags F0, F1;
+        load_frags(0, 0, F0);
+        for (int kt = 0; kt + 1 < nst; kt++) {
+            first3(kt, F0, F1);                    // F1 = sub-step 3 of stage kt
+            // Stage kt+1 landed (own DMAs) and every wave holds stage kt's last fragments.
+            wait_vm_lgkm0();
+            lds_barrier();
+            issue(kt + 2);                         // into stage kt's slot
+            load_frags(kt + 1, 0, F0);
+            mfmas(F1);                             // sub-step 3 of stage kt
+        }
+        first3(nst - 1, F0, F1);
+        mfmas(F1);
+        // Every wave is done with the ring (and no DMA is in flight) before the epilogue.
+        wait_vm_lgkm0();
+        lds_barrier();
+    }
+};
+
+// ---- shared epilogue -------------------------------------------------------------------
+
+// Output of a GEMM: exactly one of c32 (INT32) or c16 (dequantized FP16) is non-null.
+struct GemmEpilogue {
+    int32_t* c32;
+    uint16_t* c16;
+    const float* act_scale;     // (M,)  FP16 mode only
+    const uint16_t* w_scale;    // (N,)
+    const uint16_t* bias;       // (N,) or nullptr
+    int M, N;
+    int vec_out;                // 16-byte row stores allowed (N * elem % 16 == 0, base aligned)
+};
+
+// Copies `rows` x kU 16-byte units of a wave-private staging area (rows of kRowBytes, unit u
+// of row r at slot u ^ (r % kU)) to the output with coalesced 16-byte row stores.
+template <int kU, int kEsz, bool DEQUANT>
+__device__ __forceinline__ void flush_rows(const int8_t* stage, int rows, const GemmEpilogue& ep, int row0,
+                                           int col0) {
+    constexpr int kPer = 16 / kEsz;
+    constexpr int kRowBytes = kU * 16;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int M = ep.M, N = ep.N;
+    for (int idx = lane; idx < rows * kU; idx += kWave) {
+        const int r = idx / kU, u = idx % kU;
+        const int4 v = *reinterpret_cast<const int4*>(stage + r * kRowBytes + ((u ^ (r & (kU - 1))) << 4));
+        const int row = row0 + r;
+        const int col = col0 + u * kPer;
+        if (row >= M || col >= N) continue;
+        const size_t o = static_cast<size_t>(row) * N + col;
+        if (ep.vec_out && col + kPer <= N) {
+            if constexpr (DEQUANT) *reinterpret_cast<int4*>(ep.c16 + o) = v;
+            else *reinterpret_cast<int4*>(ep.c32 + o) = v;
+        } else {
+            // Ragged or unaligned rows: element stores (constant register indices).
+            const int n_ok = N - col;
+            const uint32_t w[4] = {static_cast<uint32_t>(v.x), static_cast<uint32_t>(v.y),
+                                   static_cast<uint32_t>(v.z), static_cast<uint32_t>(v.w)};
+#pragma unroll
+            for (int t = 0; t < kPer; t++) {
+                if (t >= n_ok) break;
+                if constexpr (DEQUANT)
+                    ep.c16[o + t] = static_cast<uint16_t>(w[t >> 1] >> (16 * (t & 1)));
+                else
+                    ep.c32[o + t] = static_cast<int32_t>(w[t]);
+            }
+        }
+    }
+}
+
+// LDS bytes the epilogue needs: FP16 stages the whole wave tile, INT32 one 32-row strip.
+template <int BM, int BN, bool DEQUANT>
+constexpr int epilogue_lds_bytes() {
+    return DEQUANT ? BM * BN * 2 : 4 * 32 * (BN / 2) * 4;
+}
+
+// Writes the wave's (BM/2) x (BN/2) tile through a wave-private LDS staging area: each lane
+// deposits its 4-column groups (8 bytes FP16 / 16 bytes INT32), then the wave reads back
+// 16-byte row chunks for coalesced stores. FP16: the whole tile at once, loops ordered so
+// only 4 columns' w_scale/bias are live at a time. INT32: one 32-row strip at a time.
+// The caller's K loop must be finished with the LDS.
+template <int BM, int BN, bool DEQUANT>
+__device__ __forceinline__ void store_tile(const v16i (&acc)[BN / 64][BM / 64], const GemmEpilogue& ep,
+                                           int m0, int n0, int8_t* lds) {
+    constexpr int kTM = BM / 64, kTN = BN / 64;
+    constexpr int kEsz = DEQUANT ? 2 : 4;
+    constexpr int kCols = BN / 2;
+    constexpr int kU = kCols * kEsz / 16;            // 16-byte units per staged row
+    constexpr int kPer = 16 / kEsz;                  // elements per unit
+    constexpr int kRowBytes = kCols * kEsz;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int wm = m0 + (wave >> 1) * (BM / 2);
+    const int wn = n0 + (wave & 1) * (BN / 2);
+    const int l31 = lane & 31, hi = lane >> 5;
+    const int M = ep.M, N = ep.N;
+
+    if constexpr (DEQUANT) {
+        int8_t* stage = lds + wave * ((BM / 2) * kRowBytes);
+        float as[kTM];
+#pragma unroll
+        for (int i = 0; i < kTM; i++) {
+            const int m = wm + 32 * i + l31;
+            as[i] = ep.act_scale[m < M ? m : M - 1];
+        }
+        const bool has_bias = ep.bias != nullptr;
+#pragma unroll
+        for (int j = 0; j < kTN; j++) {
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int nl = 32 * j + 8 * g + 4 * hi;     // first of this lane's 4 columns
+                float ws[4], b[4];
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    int n = wn + nl + t;
+                    n = n < N ? n : N - 1;
+                    ws[t] = h2f(ep.w_scale[n]);
+                    b[t] = has_bias ? h2f(ep.bias[n]) : 0.0f;
+                }
+                const int u = nl / kPer;                   // unit of 8 columns; half = hi
+#pragma unroll
+                for (int i = 0; i < kTM; i++) {
+                    const int r = 32 * i + l31;
+                    uint16_t h[4];
+#pragma unroll
+                    for (int t = 0; t < 4; t++)
+                        h[t] = dequant_gemm(acc[j][i][4 * g + t], as[i], ws[t], b[t], has_bias);
+                    *reinterpret_cast<uint2*>(stage + r * kRowBytes + ((u ^ (r & (kU - 1))) << 4) + 8 * hi) =
+                        make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16),
+                                   h[2] | (static_cast<uint32_t>(h[3]) << 16));
+                }
+            }
+        }
+        flush_rows<kU, kEsz, true>(stage, BM / 2, ep, wm, wn);
+    } else {
+        int8_t* strip = lds + wave * (32 * kRowBytes);
+#pragma unroll
+        for (int i = 0; i < kTM; i++) {
+#pragma unroll
+            for (int j = 0; j < kTN; j++) {
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const int u = (32 * j + 8 * g + 4 * hi) / kPer;   // unit of 4 columns
+                    *reinterpret_cast<int4*>(strip + l31 * kRowBytes + ((u ^ (l31 & (kU - 1))) << 4)) =
+                        make_int4(acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]);
+                }
+            }
+            flush_rows<kU, kEsz, false>(strip, 32, ep, wm + 32 * i, wn);
+        }
+    }
+}
 
 // Tile index -> (tile_m, tile_n): consecutive workgroups land on different XCDs
 // (dispatch is round-robin over the 8 XCDs), so the linear id is first regrouped so each
