@@ -22,11 +22,11 @@
 // bytes land at M0 + 16*lane, no VGPR staging). Every row of a stage is one full 128-byte
 // cache line read by 8 consecutive lanes; on gfx950 this sustains ~30 B/clk per CU into
 // LDS, against ~26 B/clk for 64-byte half-line rows, whatever the number of stages in
-// flight. Stage kt+1 streams in while stage kt is multiplied; MFMA fragments are
-// double-buffered in registers (sub-step ks+1 loads during sub-step ks), and the last
-// sub-step of stage kt runs after the barrier that publishes stage kt+1, hiding that
-// stage's first LDS reads. Synchronisation is explicit: one s_waitcnt vmcnt(0) lgkmcnt(0)
-// (this wave's DMAs landed, its reads of the old slot done) and one s_barrier per stage.
+// flight. Stage kt+1 streams in while stage kt is multiplied; MFMA fragments are read two
+// 32-deep sub-steps ahead of use into 4 register buffers, and the barrier that publishes
+// stage kt+1 sits in the middle of stage kt, so the LDS latency never reaches the MFMA
+// pipe. Synchronisation is explicit: one s_waitcnt vmcnt(0) lgkmcnt(0) (this wave's DMAs
+// landed, its reads of the old slot done) and one s_barrier per stage.
 // LDS rows are 8 chunks with the (r ^ (r >> 3)) & 7 swizzle below; the DMA lanes are
 // assigned (row, chunk) pairs so that each 1 KB DMA write lands exactly in that layout.
 //
@@ -62,6 +62,26 @@ __device__ __forceinline__ void wait_vmcnt() {
 // function, so the host pass never sees the device-only builtin inside kernel templates.
 __device__ __forceinline__ void dma16(const int8_t* src, int8_t* lds_base) {
     __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
+}
+
+// Instruction-scheduling pattern for one MFMA sub-step: NMFMA MFMAs with NDS LDS reads and
+// NVM vector-memory (DMA) instructions spread evenly between them, in issue order. Without
+// it the scheduler clusters the loads behind the MFMAs.
+template <int NMFMA, int NDS, int NVM>
+__device__ __forceinline__ void sched_interleave() {
+    constexpr int kMfma = 0x008, kDsRead = 0x100, kVmem = 0x010;
+    constexpr int kLoads = NDS > NVM ? NDS : NVM;
+    constexpr int kGroups = NMFMA < kLoads ? NMFMA : kLoads;
+    constexpr int kPer = NMFMA / kGroups;
+    constexpr int kDsPer = (NDS + kGroups - 1) / kGroups;
+    constexpr int kVmPer = (NVM + kGroups - 1) / kGroups;
+    static_assert(kPer * kGroups == NMFMA, "pattern must tile the MFMAs");
+#pragma unroll
+    for (int g = 0; g < kGroups; g++) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, kPer, 0);
+        if (g * kDsPer < NDS) __builtin_amdgcn_sched_group_barrier(kDsRead, kDsPer, 0);
+        if (g * kVmPer < NVM) __builtin_amdgcn_sched_group_barrier(kVmem, kVmPer, 0);
+    }
 }
 
 // Workgroup barrier without the memory fence of __syncthreads (which would also drain the
@@ -369,33 +389,46 @@ struct DmaTile {
                 for (int i = 0; i < kTM; i++)
                     acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(F.b[j], F.a[i], acc[j][i], 0, 0, 0);
         };
-        // Sub-steps 0..2 of a stage: MFMAs of sub-step ks while sub-step ks+1's fragments load.
-        auto first3 = [&](int st, Frags& F0, Frags& F1) {
-            load_frags(st, 1, F1);
-            mfmas(F0);
-            load_frags(st, 2, F0);
-            mfmas(F1);
-            load_frags(st, 3, F1);
-            mfmas(F0);
-        };
-
+        // Fragments are read two 32-deep sub-steps ahead of their MFMAs (4 register buffers,
+        // one rotation per stage), the reads and DMAs spread between the MFMAs (the scheduler
+        // would otherwise cluster them and expose the LDS latency). The barrier that
+        // publishes stage kt+1 sits after sub-step 1 of stage kt, once all of stage kt's
+        // reads are done, so sub-steps 2-3 can already read stage kt+1 and refill stage kt's
+        // slot with stage kt+2.
+        constexpr int kMf = kTM * kTN, kRd = kTM + kTN, kVm = (kAIns + kBIns) / 2;
+        Frags F0, F1, F2, F3;
         issue(0);
         wait_vm_lgkm0();
         lds_barrier();
         issue(1);
-        Frags F0, F1;
         load_frags(0, 0, F0);
+        load_frags(0, 1, F1);
         for (int kt = 0; kt + 1 < nst; kt++) {
-            first3(kt, F0, F1);                    // F1 = sub-step 3 of stage kt
-            // Stage kt+1 landed (own DMAs) and every wave holds stage kt's last fragments.
+            load_frags(kt, 2, F2);
+            mfmas(F0);
+            sched_interleave<kMf, kRd, 0>();
+            load_frags(kt, 3, F3);
+            mfmas(F1);
+            sched_interleave<kMf, kRd, 0>();
+            // Stage kt+1 landed (own DMAs) and this wave's reads of stage kt are complete.
             wait_vm_lgkm0();
             lds_barrier();
             issue(kt + 2);                         // into stage kt's slot
             load_frags(kt + 1, 0, F0);
-            mfmas(F1);                             // sub-step 3 of stage kt
+            mfmas(F2);
+            load_frags(kt + 1, 1, F1);
+            mfmas(F3);
+            // The DMAs first (spread over sub-step 2), then the reads (over sub-step 3): a
+            // global_load_lds also matches the LDS-read group, so the two are not mixed.
+            sched_interleave<kMf, 0, 2 * kVm>();
+            sched_interleave<kMf, 2 * kRd, 0>();
         }
-        first3(nst - 1, F0, F1);
+        load_frags(nst - 1, 2, F2);
+        mfmas(F0);
+        load_frags(nst - 1, 3, F3);
         mfmas(F1);
+        mfmas(F2);
+        mfmas(F3);
         // Every wave is done with the ring (and no DMA is in flight) before the epilogue.
         wait_vm_lgkm0();
         lds_barrier();
