@@ -22,7 +22,8 @@ LIB = os.path.join(LIBDIR, "libforge_amd.so")
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-# Packed-FP32 VALU forms are disabled for all device code ("Build").
+# Packed-FP32 VALU forms (v_pk_*_f32) are disabled for all device code: some of their forms
+# have given wrong results on these GPUs without any error.
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-x", "hip",

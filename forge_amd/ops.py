@@ -45,10 +45,16 @@ def _call(name: str, *args) -> None:
 
 # ---- quantization (bindings.cpp:448-476) -----------------------------------------
 
-def fused_quantize_activation(input: torch.Tensor, M: int, K: int) -> Tuple[torch.Tensor, torch.Tensor]:
+def fused_quantize_activation(input: torch.Tensor, M: int, K: int, out: Optional[torch.Tensor] = None,
+                              scales: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """bindings.cpp:448-461 (allocating); `out` / `scales` may be passed to reuse buffers."""
     _need(input, torch.float16, "input", M * K)
-    out = torch.empty((M, K), dtype=torch.int8, device=input.device)
-    scales = torch.empty((M,), dtype=torch.float32, device=input.device)
+    if out is None:
+        out = torch.empty((M, K), dtype=torch.int8, device=input.device)
+    if scales is None:
+        scales = torch.empty((M,), dtype=torch.float32, device=input.device)
+    _need(out, torch.int8, "out", M * K)
+    _need(scales, torch.float32, "scales", M)
     _call("forge_quantize_activation", _p(input), _p(out), _p(scales), M, K, _stream())
     return out, scales
 
