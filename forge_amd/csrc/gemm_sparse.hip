@@ -256,6 +256,415 @@ __global__ __launch_bounds__(256) void splitk_reduce_f32_kernel(
     }
 }
 
+// ---- DMA-fed sparse engine (256 weight rows x BMT tokens, 128-deep dense K stages) -------
+//
+// The operands stream into a 2-slot LDS ring with global_load_lds_dwordx4 (mfma_tile.h):
+//   W: 256 weight rows x 64 compressed bytes (4 chunks; chunk c of row r at c ^ lds_swz4(r))
+//   X: BMT token rows x 128 bytes (one cache line; chunk c of row r at c ^ lds_swz8(r))
+//   I: 16 blocks x 64 index words, word (32-K chunk g, row r) of block b at b*64 + g*16 + r --
+//      the order pack_metadata stores them in HBM, so the DMA copies them verbatim and lane
+//      l of every SMFMAC reads word l of its block.
+// Each wave owns 128 weight rows x BMT/2 tokens: 8 x (BMT/32) blocks of
+// v_smfmac_i32_16x16x128_i8 (one per block per stage). A stage's token blocks are split in
+// two halves: the second half's operands are read while the first half's SMFMACs run, and
+// the next stage's weights, indices and first-half tokens while the second half runs, on the
+// far side of the barrier that publishes the next stage.
+
+template <int BMT>
+struct SpDmaTile {
+    static constexpr int BNW = 256;
+    static constexpr int kTN = BNW / 2 / 16;           // weight blocks per wave
+    static constexpr int kTM = BMT / 2 / 16;           // token blocks per wave
+    static constexpr int kTH = kTM / 2;                // token blocks per half
+    static constexpr int kWBytes = BNW * 64;
+    static constexpr int kXBytes = BMT * 128;
+    static constexpr int kIBytes = BNW / 16 * 256;
+    static constexpr int kSlotBytes = kWBytes + kXBytes + kIBytes;
+    static constexpr int kLdsBytes = 2 * kSlotBytes;
+    static constexpr int kWIns = BNW * 4 / kWave / 4;   // 1 KB DMA instructions per wave per stage
+    static constexpr int kXIns = BMT * 8 / kWave / 4;
+    static_assert(BNW / 16 * 16 == kWave * 4, "one index DMA instruction per wave");
+    static_assert(kTH >= 1, "tile too small");
+
+    v4i acc[kTN][kTM];   // acc[i][j]: C[n: 16i + 4*(l/16) + e][m: 16j + l%16]
+
+    struct WFrag { v4i a[kTN]; int idx[kTN]; };
+    struct XFrag { v8i b[kTH]; };
+
+    __device__ __forceinline__ void run(const int8_t* W, const int8_t* X, const uint32_t* meta, int M, int N,
+                                        int K, int n0, int m0, int8_t* lds) {
+        const int lane = threadIdx.x & (kWave - 1);
+        const int wave = threadIdx.x / kWave;
+        const int wn = (wave >> 1) * (BNW / 2);
+        const int wm = (wave & 1) * (BMT / 2);
+        const int r16 = lane & 15, g = lane >> 4;
+        const int Kc = K >> 1, cpr = K >> 5;
+
+#pragma unroll
+        for (int i = 0; i < kTN; i++)
+#pragma unroll
+            for (int j = 0; j < kTM; j++) acc[i][j] = v4i{0, 0, 0, 0};
+
+        const int8_t* pw[kWIns];
+        const int8_t* px[kXIns];
+#pragma unroll
+        for (int q = 0; q < kWIns; q++) {
+            const int s = (wave * kWIns + q) * kWave + lane;
+            const int r = s >> 2, c = (s & 3) ^ lds_swz4(r);
+            const int gr = (n0 + r) < N ? (n0 + r) : N - 1;
+            pw[q] = W + static_cast<size_t>(gr) * Kc + 16 * c;
+        }
+#pragma unroll
+        for (int q = 0; q < kXIns; q++) {
+            const int s = (wave * kXIns + q) * kWave + lane;
+            const int r = s >> 3, c = (s & 7) ^ lds_swz8(r);
+            const int gr = (m0 + r) < M ? (m0 + r) : M - 1;
+            px[q] = X + static_cast<size_t>(gr) * K + 16 * c;
+        }
+        const int8_t* pi;
+        {
+            const int s = wave * kWave + lane;            // 16-byte chunk of the stage's index area
+            int b = (n0 >> 4) + (s >> 4);
+            b = b < (N >> 4) ? b : (N >> 4) - 1;
+            pi = reinterpret_cast<const int8_t*>(meta + static_cast<size_t>(b) * cpr * 16) + 16 * (s & 15);
+        }
+        const int nst = K / 128;
+        auto issue = [&](int st) {
+            int8_t* slot = lds + (st & 1) * kSlotBytes;
+            const int sc = st < nst ? st : nst - 1;       // past the end: re-read (dead slot)
+#pragma unroll
+            for (int q = 0; q < kWIns; q++) dma16(pw[q] + sc * 64, slot + (wave * kWIns + q) * 1024);
+#pragma unroll
+            for (int q = 0; q < kXIns; q++) dma16(px[q] + sc * 128, slot + kWBytes + (wave * kXIns + q) * 1024);
+            dma16(pi + sc * 256, slot + kWBytes + kXBytes + wave * 1024);
+        };
+        auto load_w = [&](int st, WFrag& F) {
+            const int8_t* Ws = lds + (st & 1) * kSlotBytes;
+            const uint32_t* Is = reinterpret_cast<const uint32_t*>(Ws + kWBytes + kXBytes);
+#pragma unroll
+            for (int i = 0; i < kTN; i++) {
+                const int r = wn + 16 * i + r16;
+                F.a[i] = *reinterpret_cast<const v4i*>(Ws + lds_off64(r, g));
+                F.idx[i] = static_cast<int>(Is[((wn >> 4) + i) * 64 + lane]);
+            }
+        };
+        auto load_x = [&](int st, int half, XFrag& F) {
+            const int8_t* Xs = lds + (st & 1) * kSlotBytes + kWBytes;
+#pragma unroll
+            for (int j = 0; j < kTH; j++) {
+                const int r = wm + 16 * (half * kTH + j) + r16;
+                const v4i lo = *reinterpret_cast<const v4i*>(Xs + lds_off128(r, g));
+                const v4i hi = *reinterpret_cast<const v4i*>(Xs + lds_off128(r, g + 4));
+                F.b[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+        };
+        auto smfmacs = [&](const WFrag& Wf, const XFrag& Xf, int half) {
+#pragma unroll
+            for (int j = 0; j < kTH; j++)
+#pragma unroll
+                for (int i = 0; i < kTN; i++)
+                    acc[i][half * kTH + j] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(
+                        Wf.a[i], Xf.b[j], acc[i][half * kTH + j], Wf.idx[i], 0, 0);
+        };
+        constexpr int kMf = kTN * kTH;
+        constexpr int kRdW = 2 * kTN, kRdX = 2 * kTH, kVm = kWIns + kXIns + 1;
+        // One stage: first half with (Wc, Xlo), second half with (Wc, Xhi) after the barrier
+        // that publishes stage kt+1, whose operands (Wn, Xlo) load meanwhile.
+        auto stage = [&](int kt, WFrag& Wc, WFrag& Wn, XFrag& Xlo, XFrag& Xhi) {
+            load_x(kt, 1, Xhi);
+            smfmacs(Wc, Xlo, 0);
+            sched_interleave<kMf, kRdX, 0>();
+            wait_vm_lgkm0();
+            lds_barrier();
+            issue(kt + 2);
+            load_w(kt + 1, Wn);
+            load_x(kt + 1, 0, Xlo);
+            smfmacs(Wc, Xhi, 1);
+            sched_interleave<kMf / 2, 0, kVm>();
+            sched_interleave<kMf / 2, kRdW + kRdX, 0>();
+        };
+
+        issue(0);
+        wait_vm_lgkm0();
+        lds_barrier();
+        issue(1);
+        WFrag W0, W1;
+        XFrag Xlo, Xhi;
+        load_w(0, W0);
+        load_x(0, 0, Xlo);
+        int kt = 0;
+        for (; kt + 2 < nst; kt += 2) {
+            stage(kt, W0, W1, Xlo, Xhi);
+            stage(kt + 1, W1, W0, Xlo, Xhi);
+        }
+        if (kt + 1 < nst) {                  // two stages left: kt, kt+1
+            stage(kt, W0, W1, Xlo, Xhi);
+            load_x(kt + 1, 1, Xhi);
+            smfmacs(W1, Xlo, 0);
+            smfmacs(W1, Xhi, 1);
+        } else {                             // one stage left: kt
+            load_x(kt, 1, Xhi);
+            smfmacs(W0, Xlo, 0);
+            smfmacs(W0, Xhi, 1);
+        }
+        wait_vm_lgkm0();
+        lds_barrier();
+    }
+};
+
+// Same ring, v_smfmac_i32_32x32x64_i8 (256 weight rows x 256 tokens per workgroup; each wave
+// 128 tokens x 128 weight rows = 4 x 4 blocks of 32x32 INT32 accumulators, the dense engine's
+// layout, so the dense epilogue store_tile writes it). Lane layout measured on gfx950 with
+// one-hot operands: A lane l holds compressed bytes of weight row l%32 covering dense K
+// [32*(l/32), +32) of the 64-deep step, pair q = group q, indexed by nibble q of the lane's
+// own word; B lane l holds token l%32, bytes 0-15 = K [16*(l/32), +16) and bytes 16-31 =
+// K [32 + 16*(l/32), +16); the accumulator is the 32x32 MFMA layout (row = weight).
+struct SpDmaTile32 {
+    static constexpr int BNW = 256, BMT = 256;
+    static constexpr int kTN = 4, kTM = 4;             // 32-row weight / 32-token blocks per wave
+    static constexpr int kWBytes = BNW * 64;
+    static constexpr int kXBytes = BMT * 128;
+    static constexpr int kIBytes = BNW / 16 * 256;
+    static constexpr int kSlotBytes = kWBytes + kXBytes + kIBytes;
+    static constexpr int kLdsBytes = 2 * kSlotBytes;
+    static constexpr int kWIns = BNW * 4 / kWave / 4;
+    static constexpr int kXIns = BMT * 8 / kWave / 4;
+
+    v16i acc[kTN][kTM];   // acc[j][i]: D[n: 32j + row(e, l)][m: 32i + l%32]
+
+    struct Frags { v4i a[kTN]; int idx[kTN]; v8i b[kTM]; };
+
+    __device__ __forceinline__ void run(const int8_t* W, const int8_t* X, const uint32_t* meta, int M, int N,
+                                        int K, int n0, int m0, int8_t* lds) {
+        const int lane = threadIdx.x & (kWave - 1);
+        const int wave = threadIdx.x / kWave;
+        const int wm = (wave >> 1) * (BMT / 2);        // token offset (dense engine's wave layout)
+        const int wn = (wave & 1) * (BNW / 2);         // weight offset
+        const int l31 = lane & 31, g = lane >> 5;
+        const int Kc = K >> 1, cpr = K >> 5;
+
+#pragma unroll
+        for (int j = 0; j < kTN; j++)
+#pragma unroll
+            for (int i = 0; i < kTM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[j][i][e] = 0;
+
+        const int8_t* pw[kWIns];
+        const int8_t* px[kXIns];
+#pragma unroll
+        for (int q = 0; q < kWIns; q++) {
+            const int s = (wave * kWIns + q) * kWave + lane;
+            const int r = s >> 2, c = (s & 3) ^ lds_swz4(r);
+            const int gr = (n0 + r) < N ? (n0 + r) : N - 1;
+            pw[q] = W + static_cast<size_t>(gr) * Kc + 16 * c;
+        }
+#pragma unroll
+        for (int q = 0; q < kXIns; q++) {
+            const int s = (wave * kXIns + q) * kWave + lane;
+            const int r = s >> 3, c = (s & 7) ^ lds_swz8(r);
+            const int gr = (m0 + r) < M ? (m0 + r) : M - 1;
+            px[q] = X + static_cast<size_t>(gr) * K + 16 * c;
+        }
+        const int8_t* pi;
+        {
+            const int s = wave * kWave + lane;
+            int b = (n0 >> 4) + (s >> 4);
+            b = b < (N >> 4) ? b : (N >> 4) - 1;
+            pi = reinterpret_cast<const int8_t*>(meta + static_cast<size_t>(b) * cpr * 16) + 16 * (s & 15);
+        }
+        const int nst = K / 128;
+        auto issue = [&](int st) {
+            int8_t* slot = lds + (st & 1) * kSlotBytes;
+            const int sc = st < nst ? st : nst - 1;
+#pragma unroll
+            for (int q = 0; q < kWIns; q++) dma16(pw[q] + sc * 64, slot + (wave * kWIns + q) * 1024);
+#pragma unroll
+            for (int q = 0; q < kXIns; q++) dma16(px[q] + sc * 128, slot + kWBytes + (wave * kXIns + q) * 1024);
+            dma16(pi + sc * 256, slot + kWBytes + kXBytes + wave * 1024);
+        };
+        // Sub-step h (dense K [64h, 64h+64) of the stage).
+        auto load = [&](int st, int h, Frags& F) {
+            const int8_t* Ws = lds + (st & 1) * kSlotBytes;
+            const int8_t* Xs = Ws + kWBytes;
+            const uint32_t* Is = reinterpret_cast<const uint32_t*>(Xs + kXBytes);
+#pragma unroll
+            for (int j = 0; j < kTN; j++) {
+                const int r = wn + 32 * j + l31;
+                F.a[j] = *reinterpret_cast<const v4i*>(Ws + lds_off64(r, 2 * h + g));
+                F.idx[j] = static_cast<int>(Is[(r >> 4) * 64 + (2 * h + g) * 16 + (r & 15)]);
+            }
+#pragma unroll
+            for (int i = 0; i < kTM; i++) {
+                const int r = wm + 32 * i + l31;
+                const v4i lo = *reinterpret_cast<const v4i*>(Xs + lds_off128(r, 4 * h + g));
+                const v4i hi = *reinterpret_cast<const v4i*>(Xs + lds_off128(r, 4 * h + 2 + g));
+                F.b[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+        };
+        auto smfmacs = [&](const Frags& F) {
+#pragma unroll
+            for (int j = 0; j < kTN; j++)
+#pragma unroll
+                for (int i = 0; i < kTM; i++)
+                    acc[j][i] = __builtin_amdgcn_smfmac_i32_32x32x64_i8(F.a[j], F.b[i], acc[j][i], F.idx[j], 0, 0);
+        };
+        constexpr int kMf = kTN * kTM, kRd = 2 * kTN + 2 * kTM, kVm = kWIns + kXIns + 1;
+        // Stage kt: sub-step 0 with F0 while sub-step 1 loads into F1; barrier publishing
+        // stage kt+1; sub-step 1 with F1 while stage kt+1's sub-step 0 loads into F0.
+        auto stage = [&](int kt, Frags& F0, Frags& F1) {
+            load(kt, 1, F1);
+            smfmacs(F0);
+            sched_interleave<kMf, kRd, 0>();
+            wait_vm_lgkm0();
+            lds_barrier();
+            issue(kt + 2);
+            load(kt + 1, 0, F0);
+            smfmacs(F1);
+            sched_interleave<kMf / 2, 0, kVm>();
+            sched_interleave<kMf / 2, kRd, 0>();
+        };
+        issue(0);
+        wait_vm_lgkm0();
+        lds_barrier();
+        issue(1);
+        Frags F0, F1;
+        load(0, 0, F0);
+        for (int kt = 0; kt + 1 < nst; kt++) stage(kt, F0, F1);
+        load(nst - 1, 1, F1);
+        smfmacs(F0);
+        smfmacs(F1);
+        wait_vm_lgkm0();
+        lds_barrier();
+    }
+};
+
+template <bool DEQUANT>
+__global__ __launch_bounds__(256) void sparse_dma32_kernel(const int8_t* __restrict__ W, const int8_t* __restrict__ X,
+                                                           const uint32_t* __restrict__ meta, GemmEpilogue ep,
+                                                           int tiles_n, int tiles_m, int K)
+{
+    extern __shared__ __align__(16) int8_t lds[];
+    int tn, tm;
+    tile_coords(blockIdx.x, tiles_n, tiles_m, tn, tm);
+    const int n0 = tn * 256, m0 = tm * 256;
+    SpDmaTile32 t;
+    t.run(W, X, meta, ep.M, ep.N, K, n0, m0, lds);
+    store_tile<256, 256, DEQUANT>(t.acc, ep, m0, n0, lds);
+}
+
+template <bool DEQUANT>
+static int launch_sparse_dma32(const int8_t* W, const int8_t* X, const uint32_t* meta, const GemmEpilogue& ep,
+                               int K, hipStream_t s)
+{
+    constexpr int epi = epilogue_lds_bytes<256, 256, DEQUANT>();
+    constexpr int lds = SpDmaTile32::kLdsBytes > epi ? SpDmaTile32::kLdsBytes : epi;
+    const int tiles_n = divup(ep.N, 256), tiles_m = divup(ep.M, 256);
+    const long long total = static_cast<long long>(tiles_n) * tiles_m;
+    if (total > 0x7FFFFFFFLL) return FORGE_EINVAL;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&sparse_dma32_kernel<DEQUANT>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (attr != hipSuccess) return static_cast<int>(attr);
+    sparse_dma32_kernel<DEQUANT><<<static_cast<unsigned>(total), 256, lds, s>>>(W, X, meta, ep, tiles_n, tiles_m, K);
+    return launch_status();
+}
+
+// Epilogue of a SpDmaTile: lane l of block (i, j) holds outputs (m = 16j + l%16, n = 16i +
+// 4*(l/16) + e), 4 consecutive columns. FP16: the wave's whole (BMT/2) x 128 tile is staged in
+// LDS; INT32: one 16-row strip per token block. Rows are flushed with 16-byte stores.
+template <int BMT, bool DEQUANT>
+__device__ __forceinline__ void sp_store_tile(const v4i (&acc)[8][BMT / 32], const GemmEpilogue& ep, int n0,
+                                              int m0, int8_t* lds) {
+    constexpr int kTN = 8, kTM = BMT / 32;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int wn = n0 + (wave >> 1) * 128;
+    const int wm = m0 + (wave & 1) * (BMT / 2);
+    const int r16 = lane & 15, q = lane >> 4;
+    const int M = ep.M, N = ep.N;
+    if constexpr (DEQUANT) {
+        constexpr int kU = 16, kRowBytes = 256;              // 128 FP16 columns per staged row
+        int8_t* stage = lds + wave * ((BMT / 2) * kRowBytes);
+        const bool has_bias = ep.bias != nullptr;
+        float as[kTM];
+#pragma unroll
+        for (int j = 0; j < kTM; j++) {
+            const int m = wm + 16 * j + r16;
+            as[j] = ep.act_scale[m < M ? m : M - 1];
+        }
+#pragma unroll
+        for (int i = 0; i < kTN; i++) {
+            float ws[4], b[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                int n = wn + 16 * i + 4 * q + t;
+                n = n < N ? n : N - 1;
+                ws[t] = h2f(ep.w_scale[n]);
+                b[t] = has_bias ? h2f(ep.bias[n]) : 0.0f;
+            }
+            const int u = 2 * i + (q >> 1), half = q & 1;
+#pragma unroll
+            for (int j = 0; j < kTM; j++) {
+                const int r = 16 * j + r16;
+                uint16_t h[4];
+#pragma unroll
+                for (int t = 0; t < 4; t++) h[t] = dequant_gemm(acc[i][j][t], as[j], ws[t], b[t], has_bias);
+                *reinterpret_cast<uint2*>(stage + r * kRowBytes + ((u ^ (r & (kU - 1))) << 4) + 8 * half) =
+                    make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+            }
+        }
+        flush_rows<kU, 2, true>(stage, BMT / 2, ep, wm, wn);
+    } else {
+        constexpr int kU = 32, kRowBytes = 512;              // 128 INT32 columns per staged row
+        int8_t* strip = lds + wave * (16 * kRowBytes);
+#pragma unroll
+        for (int j = 0; j < kTM; j++) {
+#pragma unroll
+            for (int i = 0; i < kTN; i++) {
+                const int u = 4 * i + q;
+                *reinterpret_cast<int4*>(strip + r16 * kRowBytes + ((u ^ (r16 & (kU - 1))) << 4)) =
+                    make_int4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+            }
+            flush_rows<kU, 4, false>(strip, 16, ep, wm + 16 * j, wn);
+        }
+    }
+}
+
+template <int BMT, bool DEQUANT>
+constexpr int sp_dma_lds_bytes() {
+    constexpr int epi = DEQUANT ? 4 * (BMT / 2) * 256 : 4 * 16 * 512;
+    return SpDmaTile<BMT>::kLdsBytes > epi ? SpDmaTile<BMT>::kLdsBytes : epi;
+}
+
+template <int BMT, bool DEQUANT>
+__global__ __launch_bounds__(256) void sparse_dma_kernel(const int8_t* __restrict__ W, const int8_t* __restrict__ X,
+                                                         const uint32_t* __restrict__ meta, GemmEpilogue ep,
+                                                         int tiles_n, int tiles_m, int K)
+{
+    extern __shared__ __align__(16) int8_t lds[];
+    int tn, tm;
+    tile_coords(blockIdx.x, tiles_n, tiles_m, tn, tm);
+    const int n0 = tn * 256, m0 = tm * BMT;
+    SpDmaTile<BMT> t;
+    t.run(W, X, meta, ep.M, ep.N, K, n0, m0, lds);
+    sp_store_tile<BMT, DEQUANT>(t.acc, ep, n0, m0, lds);
+}
+
+template <int BMT, bool DEQUANT>
+static int launch_sparse_dma(const int8_t* W, const int8_t* X, const uint32_t* meta, const GemmEpilogue& ep,
+                             int K, hipStream_t s)
+{
+    constexpr int lds = sp_dma_lds_bytes<BMT, DEQUANT>();
+    const int tiles_n = divup(ep.N, 256), tiles_m = divup(ep.M, BMT);
+    const long long total = static_cast<long long>(tiles_n) * tiles_m;
+    if (total > 0x7FFFFFFFLL) return FORGE_EINVAL;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&sparse_dma_kernel<BMT, DEQUANT>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (attr != hipSuccess) return static_cast<int>(attr);
+    sparse_dma_kernel<BMT, DEQUANT><<<static_cast<unsigned>(total), 256, lds, s>>>(W, X, meta, ep, tiles_n, tiles_m, K);
+    return launch_status();
+}
+
 // ---- tile configurations ----------------------------------------------------------
 
 constexpr int kSpTileBW[FORGE_SPARSE_NUM_TILES] = {256, 128, 128};
@@ -379,6 +788,19 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
         const int fblocks = static_cast<int>(std::min<long long>(divupll(total, 256), 8192));
         splitk_finalize_kernel<<<fblocks, 256, 0, s>>>(ws, act_scale, w_scale, bias, out16, N, total);
         return launch_status();
+    }
+    // Unsplit plans on 128-deep K stages run on the DMA-fed engine: 256 weight rows x 256
+    // tokens when the planner chose freely, x 128 tokens for the reference's 256x128 tile.
+    if (K % 128 == 0 && M > 64 && (tile == FORGE_SPARSE_TILE_AUTO || pt == FORGE_SPARSE_TILE_256x128) &&
+        (tile == FORGE_SPARSE_TILE_AUTO || tile == FORGE_SPARSE_TILE_256x128)) {
+        void* o = out16 ? static_cast<void*>(out16) : static_cast<void*>(out32);
+        GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N, aligned(o, 16) ? 1 : 0};
+        const bool wide = tile == FORGE_SPARSE_TILE_AUTO && M > 128;
+        if (wide)
+            return out16 ? launch_sparse_dma32<true>(W_comp, x, meta, ep, K, s)
+                         : launch_sparse_dma32<false>(W_comp, x, meta, ep, K, s);
+        return out16 ? launch_sparse_dma<128, true>(W_comp, x, meta, ep, K, s)
+                     : launch_sparse_dma<128, false>(W_comp, x, meta, ep, K, s);
     }
     p.split_k = 1;
     p.steps_per_split = steps;

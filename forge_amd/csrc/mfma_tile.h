@@ -67,21 +67,25 @@ __device__ __forceinline__ void dma16(const int8_t* src, int8_t* lds_base) {
 // Instruction-scheduling pattern for one MFMA sub-step: NMFMA MFMAs with NDS LDS reads and
 // NVM vector-memory (DMA) instructions spread evenly between them, in issue order. Without
 // it the scheduler clusters the loads behind the MFMAs.
+template <int G, int NG, int NMFMA, int NDS, int NVM>
+__device__ __forceinline__ void sched_groups() {
+    if constexpr (G < NG) {
+        // Group G takes its even share (rounded so the shares sum exactly) of each kind.
+        constexpr int mf = NMFMA * (G + 1) / NG - NMFMA * G / NG;
+        constexpr int ds = NDS * (G + 1) / NG - NDS * G / NG;
+        constexpr int vm = NVM * (G + 1) / NG - NVM * G / NG;
+        if constexpr (mf > 0) __builtin_amdgcn_sched_group_barrier(0x008, mf, 0);   // MFMA
+        if constexpr (ds > 0) __builtin_amdgcn_sched_group_barrier(0x100, ds, 0);   // LDS read
+        if constexpr (vm > 0) __builtin_amdgcn_sched_group_barrier(0x010, vm, 0);   // VMEM
+        sched_groups<G + 1, NG, NMFMA, NDS, NVM>();
+    }
+}
+
 template <int NMFMA, int NDS, int NVM>
 __device__ __forceinline__ void sched_interleave() {
-    constexpr int kMfma = 0x008, kDsRead = 0x100, kVmem = 0x010;
     constexpr int kLoads = NDS > NVM ? NDS : NVM;
-    constexpr int kGroups = NMFMA < kLoads ? NMFMA : kLoads;
-    constexpr int kPer = NMFMA / kGroups;
-    constexpr int kDsPer = (NDS + kGroups - 1) / kGroups;
-    constexpr int kVmPer = (NVM + kGroups - 1) / kGroups;
-    static_assert(kPer * kGroups == NMFMA, "pattern must tile the MFMAs");
-#pragma unroll
-    for (int g = 0; g < kGroups; g++) {
-        __builtin_amdgcn_sched_group_barrier(kMfma, kPer, 0);
-        if (g * kDsPer < NDS) __builtin_amdgcn_sched_group_barrier(kDsRead, kDsPer, 0);
-        if (g * kVmPer < NVM) __builtin_amdgcn_sched_group_barrier(kVmem, kVmPer, 0);
-    }
+    constexpr int kGroups = NMFMA < kLoads ? NMFMA : (kLoads > 0 ? kLoads : 1);
+    sched_groups<0, kGroups, NMFMA, NDS, NVM>();
 }
 
 // Workgroup barrier without the memory fence of __syncthreads (which would also drain the
@@ -207,6 +211,11 @@ constexpr int kBK = 128;
 
 __device__ __forceinline__ int lds_swz8(int r) { return (r ^ (r >> 3)) & 7; }
 __device__ __forceinline__ int lds_off128(int r, int c) { return r * kBK + ((c ^ lds_swz8(r)) << 4); }
+
+// 64-byte LDS rows (4 chunks): chunk c of row r at c ^ (((r >> 1) ^ (r >> 3)) & 3), conflict
+// free for 16-byte reads of the same chunk from 8 (or 16) consecutive rows.
+__device__ __forceinline__ int lds_swz4(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+__device__ __forceinline__ int lds_off64(int r, int c) { return r * 64 + ((c ^ lds_swz4(r)) << 4); }
 
 template <int BM, int BN>
 struct NtTile {
