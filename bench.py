@@ -12,8 +12,9 @@ algorithmic ops 2*M*N*K per launch against MI355X's dense INT8 peak (5.0 POP/s).
 cpu_baseline: the oracle's single-threaded INT32 loop + dequant epilogue (oracle/) over as
 many rows of the same workload as fit in ~12 s (all 4096 on an EPYC host), timed on this host.
 extra: configs[2] (2:4 sparse vs dense at 4096x11008x4096) and configs[3] (decode
-M = 1/4/16, N = K = 8192, dense and 2:4, HBM GB/s with >= 5 rotating weight copies so
-the 256 MB MALL cannot hold them).
+M = 1/4/16, N = K = 8192, dense and 2:4, HBM GB/s with 6 rotating weight copies so the
+256 MB MALL cannot hold them; calls captured into a HIP graph and replayed so host launch
+overhead is not timed).
 """
 from __future__ import annotations
 
@@ -45,6 +46,34 @@ def events_time_ms(fn, reps: int) -> float:
     e.record()
     e.synchronize()
     return s.elapsed_time(e) / reps
+
+
+def graph_time_ms(calls, replays: int = 20) -> float:
+    """Average GPU time of one call: the calls (each one library call on torch's current
+    stream) are captured into one HIP graph and replayed, so host launch overhead is out of
+    the timing (the reference's bench_int8_sparse.cu:41-85 protocol)."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for c in calls:
+            c()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for c in calls:
+            c()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(replays):
+        graph.replay()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / (replays * len(calls))
 
 
 def make_c2(dev, seed=2):
@@ -141,20 +170,10 @@ def bench_extra(dev):
         xh = torch.randn((M, K), generator=g, device=dev).half()
         sq = torch.empty((M, K), dtype=torch.int8, device=dev)
         ss = torch.empty((M,), dtype=torch.float32, device=dev)
-        i = [0]
-
-        def dense():
-            ops.int8_linear(xh, Ws[i[0] % copies], ws, b, sq, ss)
-            i[0] += 1
-
-        def sparse():
-            ops.sparse_int8_linear(xh, comps[i[0] % copies], metas[i[0] % copies], ws, b, sq, ss)
-            i[0] += 1
-        for _ in range(copies):
-            dense()
-            sparse()
-        td = events_time_ms(dense, 6 * copies)
-        ts = events_time_ms(sparse, 6 * copies)
+        dense = [lambda c=c: ops.int8_linear(xh, Ws[c], ws, b, sq, ss) for c in range(copies)]
+        sparse = [lambda c=c: ops.sparse_int8_linear(xh, comps[c], metas[c], ws, b, sq, ss) for c in range(copies)]
+        td = graph_time_ms(dense * 6)
+        ts = graph_time_ms(sparse * 6)
         bytes_d = N * K + M * K * 2 + M * N * 2 + N * 2 + N * 2
         bytes_s = N * K // 2 + N * K // 8 + M * K * 2 + M * N * 2 + N * 2 + N * 2
         out[f"c4_M{M}_dense_GBs"] = bytes_d / td / 1e6

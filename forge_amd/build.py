@@ -37,6 +37,7 @@ SOURCES = [
     "sparsity.hip",
     "gemm_dense.hip",
     "gemm_skinny.hip",
+    "gemm_decode.hip",
     "gemm_sparse.hip",
     "conv.hip",
     "forge_api.cpp",

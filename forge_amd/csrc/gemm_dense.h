@@ -20,6 +20,14 @@ int gemm_dense(const int8_t* A, const int8_t* B, const float* act_scale, const u
 int launch_gemm_skinny(const int8_t* A, const int8_t* B, const GemmEpilogue& ep, int M, int K, int N,
                        hipStream_t s);
 
+// Decode GEMM (M <= kDecodeMaxM tokens, K % 128 == 0): weights W (N,K) dense or W_comp (N,K/2) +
+// gfx950 index words (sparse), tokens X (M,K) int8; 16-byte aligned operands.
+constexpr int kDecodeMaxM = 16;
+constexpr int kDecodeMaxK = 8 * 8 * 128;   // 8 waves x 8 stages of 128
+bool decode_supported(int M, int K);
+int launch_decode(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep, int K,
+                  bool sparse, hipStream_t s);
+
 // Implicit-GEMM NHWC conv through the dense tile engine (conv.hip supplies the geometry).
 int launch_conv_gemm(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep, int Co, bool vec,
                      hipStream_t s);

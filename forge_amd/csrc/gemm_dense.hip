@@ -170,6 +170,8 @@ int gemm_dense(const int8_t* A, const int8_t* B, const float* act_scale, const u
     const bool vec = (K % 16 == 0) && aligned(A, 16) && aligned(B, 16);
     GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N,
                     out16 ? out_vec(out16, N, 2) : out_vec(out32, N, 4)};
+    if (vec && decode_supported(M, K))
+        return launch_decode(B, nullptr, A, ep, K, false, s);
     if (M <= kSkinnyMaxM && vec)
         return launch_gemm_skinny(A, B, ep, M, K, N, s);
     if (vec && K % kBK == 0) {

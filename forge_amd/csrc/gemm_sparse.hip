@@ -766,6 +766,13 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
     device_info(&st);
     if (st != FORGE_OK) return st;
 
+    // Decode shapes stream the weights once on the decode kernel (any tile / split request
+    // gives the same bits, so those hints do not apply here).
+    if (decode_supported(M, K)) {
+        void* o = out16 ? static_cast<void*>(out16) : static_cast<void*>(out32);
+        GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N, aligned(o, 16) ? 1 : 0};
+        return launch_decode(W_comp, meta, x, ep, K, true, s);
+    }
     int pt = 1, ps = 1;
     sparse_plan_cost(M, K, N, out32 ? 1 : split_k, out32 ? false : ws != nullptr, tile,
                      cu_count_or_default(), &pt, &ps);

@@ -5,10 +5,10 @@
 //   scale[m] = max(absmax(x[m,:]), 1e-8f) / 127.0f      (IEEE division)
 //   q[m,k]   = clamp(rne(x[m,k] * (1.0f / scale[m])), -128, 127)
 //
-// MI355X design: the main kernel gives each row to ONE wavefront (4 rows per 256-thread
-// workgroup). A lane holds VPT 16-byte vectors of its row in VGPRs, so x is read from
-// HBM once; the row absmax is a 64-lane butterfly (no LDS, no barrier), then each lane
-// writes 8 int8 per vector. The exported two-pass kernel (any K, any alignment, any
+// MI355X design: the main kernel gives each row to one 256-thread workgroup. A lane holds
+// VPT 16-byte vectors of its row in VGPRs, so x is read from HBM once; the row absmax is a
+// 64-lane butterfly per wave plus a 4-entry LDS max, then each lane writes 8 int8 per
+// vector. The exported two-pass kernel (any K, any alignment, any
 // block size) reduces through LDS; both compute the same max (exact) and the same
 // IEEE-rounded arithmetic, so their outputs are bit-identical.
 #include "common.h"
@@ -52,36 +52,41 @@ __device__ __forceinline__ float absmax8(uint4 v, float m) {
     return m;
 }
 
-// One wavefront per row; K % 8 == 0, K <= VPT * 512, x 16-byte and q 8-byte aligned.
+// One 256-thread workgroup per row; K % 8 == 0, K <= VPT * 2048, x 16-byte and q 8-byte
+// aligned. Thread t holds 16-byte vectors t, t + 256, ... of its row in VGPRs (x is read
+// once), the row absmax is a 64-lane butterfly per wave then a 4-entry LDS max, and every
+// lane writes 8 int8 per vector. Spreading a row over 4 waves keeps decode-size calls (a
+// handful of rows) from serialising one wave's loads.
 template <int VPT>
-__global__ __launch_bounds__(256) void quantize_rows_wave_kernel(
-    const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scales,
-    int M, int K)
+__global__ __launch_bounds__(256) void quantize_rows_block_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scales, int K)
 {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int row = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
-    if (row >= M) return;   // whole wave exits together: no barrier below
+    __shared__ float wmax[4];
+    const int row = blockIdx.x;
+    const int t = threadIdx.x;
     const int nvec = K >> 3;
     const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<size_t>(row) * K);
     uint2* dst = reinterpret_cast<uint2*>(q + static_cast<size_t>(row) * K);
-
     uint4 v[VPT];
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPT; i++) {
-        const int idx = lane + i * kWave;
+        const int idx = t + i * 256;
         if (idx < nvec) {
             v[i] = src[idx];
             amax = absmax8(v[i], amax);
         }
     }
     amax = wave_max(amax);
+    if ((t & (kWave - 1)) == 0) wmax[t / kWave] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
     const float scale = row_scale(amax);
     const float inv = 1.0f / scale;
-    if (lane == 0) scales[row] = scale;
+    if (t == 0) scales[row] = scale;
 #pragma unroll
     for (int i = 0; i < VPT; i++) {
-        const int idx = lane + i * kWave;
+        const int idx = t + i * 256;
         if (idx < nvec) dst[idx] = quant8(v[i], inv);
     }
 }
@@ -182,16 +187,13 @@ namespace forge_amd {
 
 int launch_quantize(const uint16_t* x, int8_t* q, float* scales, int M, int K, hipStream_t s)
 {
-    const bool vec_ok = (K % 8 == 0) && K <= 16 * 512 && aligned(x, 16) && aligned(q, 8);
+    const bool vec_ok = (K % 8 == 0) && K <= 8 * 2048 && aligned(x, 16) && aligned(q, 8);
     if (vec_ok) {
-        const int rows_per_block = 4;
-        const dim3 grid(divup(M, rows_per_block)), block(rows_per_block * kWave);
-        const int vpt = divup(K, 512);
-        if (vpt <= 1)      quantize_rows_wave_kernel<1><<<grid, block, 0, s>>>(x, q, scales, M, K);
-        else if (vpt <= 2) quantize_rows_wave_kernel<2><<<grid, block, 0, s>>>(x, q, scales, M, K);
-        else if (vpt <= 4) quantize_rows_wave_kernel<4><<<grid, block, 0, s>>>(x, q, scales, M, K);
-        else if (vpt <= 8) quantize_rows_wave_kernel<8><<<grid, block, 0, s>>>(x, q, scales, M, K);
-        else               quantize_rows_wave_kernel<16><<<grid, block, 0, s>>>(x, q, scales, M, K);
+        const int vpt = divup(K, 2048);
+        if (vpt <= 1)      quantize_rows_block_kernel<1><<<M, 256, 0, s>>>(x, q, scales, K);
+        else if (vpt <= 2) quantize_rows_block_kernel<2><<<M, 256, 0, s>>>(x, q, scales, K);
+        else if (vpt <= 4) quantize_rows_block_kernel<4><<<M, 256, 0, s>>>(x, q, scales, K);
+        else               quantize_rows_block_kernel<8><<<M, 256, 0, s>>>(x, q, scales, K);
     } else {
         forge::quant::fused_quantize_activation_kernel<<<M, 256, 0, s>>>(
             reinterpret_cast<const __half*>(x), q, scales, K);

@@ -1,0 +1,99 @@
+"""GPU parity: decode-shape GEMMs (M <= 16 tokens) on the weight-streaming decode kernel,
+dense and 2:4 sparse, against the oracle.
+
+Bar: INT32 bit-exact; FP16 bit-exact to the oracle's epilogue. Shapes exercise the kernel's
+K split over 8 wavefronts (K = 128: one wave works; K = 1152: 9 stages, uneven slices and
+idle waves), ragged N (not a multiple of the 32-row workgroup tile), M from 1 to 16, and
+configs[3] at full size (M = 16, N = K = 8192; sampled output columns)."""
+import numpy as np
+import pytest
+
+from helpers import fp16_normal, int8_uniform, poison, say, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+DENSE = [(1, 128, 32), (3, 1152, 96), (16, 2048, 50), (7, 4096, 200), (16, 1024, 8)]
+SPARSE = [(1, 128, 32), (5, 1152, 48), (16, 2048, 208), (9, 4096, 1024), (16, 1024, 16)]
+
+
+@pytest.mark.parametrize("M,K,N", DENSE)
+def test_decode_dense(dev, orc, M, K, N):
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(M * 31 + K + N)
+    A = int8_uniform(rng, (M, K))
+    B = int8_uniform(rng, (N, K))
+    act = rng.uniform(0.001, 0.05, M).astype(np.float32)
+    ws = rng.uniform(0.001, 0.05, N).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
+    acc = orc.gemm_s32(A, B)
+    say(f"decode dense M={M} K={K} N={N}")
+    C = torch.empty((M, N), dtype=torch.int32, device=dev)
+    poison(C, 0x7B)
+    assert np.array_equal(to_host(ops.int8_gemm_s32(to_dev(A, dev), to_dev(B, dev), out=C)), acc)
+    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    poison(Y, 0x7B)
+    ops.int8_gemm_dequant(to_dev(A, dev), to_dev(B, dev), to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev), out=Y)
+    assert np.array_equal(to_host(Y).view(np.uint16), orc.dequant_epilogue(acc, act, ws, b).view(np.uint16))
+
+
+@pytest.mark.parametrize("M,K,N", SPARSE)
+def test_decode_sparse(dev, orc, M, K, N):
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(M * 17 + K * 3 + N)
+    W = int8_uniform(rng, (N, K))
+    x = int8_uniform(rng, (M, K))
+    act = rng.uniform(0.001, 0.05, M).astype(np.float32)
+    ws = rng.uniform(0.001, 0.05, N).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
+    cr, mr = orc.prune_compress_24(W)
+    acc = orc.sparse_gemm_s32(cr, x, mr, N, K)
+    comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+    raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+    meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+    ops.prune_compress_24(to_dev(W, dev), comp, raw, N, K)
+    ops.pack_metadata(raw, meta, N, K)
+    say(f"decode sparse M={M} K={K} N={N}")
+    xd = to_dev(x, dev)
+    C = torch.empty((M, N), dtype=torch.int32, device=dev)
+    poison(C, 0x7B)
+    assert np.array_equal(to_host(ops.sparse_int8_gemm_s32(comp, xd, meta, out=C)), acc)
+    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    for split in (1, 4):
+        poison(Y, 0x7B)
+        ops.sparse_int8_gemm(comp, xd, meta, to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev), split_k=split, out=Y)
+        assert np.array_equal(to_host(Y).view(np.uint16), orc.dequant_epilogue(acc, act, ws, b).view(np.uint16))
+
+
+def test_config4_full_size_sampled(dev, orc):
+    """M = 16 tokens, N = K = 8192, dense and 2:4, FP16 tokens quantized per
+    token, dequant + bias; sampled output columns against the oracle."""
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(4)
+    M, K, N = 16, 8192, 8192
+    W = int8_uniform(rng, (N, K))
+    x = fp16_normal(rng, (M, K))
+    ws = rng.uniform(1e-3, 1e-2, N).astype(np.float16)
+    b = fp16_normal(rng, (N,), 0.1)
+    cols = np.array([0, 1, 31, 32, 4095, 4096, 8160, 8191])
+    q, s = orc.quantize_rows(x)
+    ref_d = orc.dequant_epilogue(orc.gemm_s32(q, W[cols]), s, ws[cols], b[cols]).view(np.uint16)
+    cr, mr = orc.prune_compress_24(W)
+    Wp = orc.decompress_24(cr, mr, N, K)
+    ref_s = orc.dequant_epilogue(orc.gemm_s32(q, Wp[cols]), s, ws[cols], b[cols]).view(np.uint16)
+    xd, Wd, wsd, bd = to_dev(x, dev), to_dev(W, dev), to_dev(ws, dev), to_dev(b, dev)
+    sq = torch.empty((M, K), dtype=torch.int8, device=dev)
+    ss = torch.empty((M,), dtype=torch.float32, device=dev)
+    say("config4 dense 16x8192x8192")
+    yd = to_host(ops.int8_linear(xd, Wd, wsd, bd, sq, ss)).view(np.uint16)
+    assert np.array_equal(yd[:, cols], ref_d)
+    comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+    raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+    meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+    ops.prune_compress_24(Wd, comp, raw, N, K)
+    ops.pack_metadata(raw, meta, N, K)
+    say("config4 sparse 16x8192x8192")
+    ys = to_host(ops.sparse_int8_linear(xd, comp, meta, wsd, bd, sq, ss)).view(np.uint16)
+    assert np.array_equal(ys[:, cols], ref_s)
