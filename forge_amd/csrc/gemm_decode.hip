@@ -5,43 +5,51 @@
 // with a handful of tokens, src/gemm/int8_sparse.cu:1005-1043, src/gemm/int8_dense.cu:213-232),
 // where the weights are read once per call and every other operand is tiny.
 //
-// One 512-thread workgroup owns 32 weight rows and all of K; its 8 wavefronts split K into
-// contiguous slices of 128-deep stages. Each wave streams its slice of the 32 weight rows
-// through a PRIVATE LDS ring with global_load_lds_dwordx4 (full 128-byte lines per row: the
-// fastest load path into a CU), so only the wave's own vmcnt orders the ring -- no barrier in
-// the K loop. The stage's 16 token rows ride in the same slot, also by DMA. Dense: 3 slots of
-// 6 KB, 2 stages in flight per wave; sparse: 4 slots of 4.5 KB, 3 in flight (144 KB of LDS,
-// one workgroup per CU). Dense stages feed
-// 2 x 2 v_mfma_i32_16x16x64_i8 (weights as the A operand); sparse stages feed 2
-// v_smfmac_i32_16x16x128_i8 (compressed weights + index words as A, lane layout as in
-// gemm_sparse.hip). The 8 per-wave INT32 partials are summed exactly through LDS, then the
-// dequant epilogue writes the outputs.
+// Dense (decode_dense_kernel): a 256-thread workgroup owns 32 weight rows and all of K; its 4
+// wavefronts split K into contiguous slices of 128-deep stages. Operands are loaded straight
+// into registers with coalesced 8-row x 128-byte instructions (non-temporal for the weights,
+// which are read once), rearranged into the matrix-core layout by one DPP lane swap, and fed
+// to v_mfma_i32_16x16x64_i8. Measured on MI355X, this streams a 64 MB weight matrix from HBM
+// faster than staging it through LDS: coalesced register loads at this shape reach ~6 TB/s in
+// isolation, LDS DMA rings of any shape stay under 4.8 TB/s.
 //
-// Each wave's stage count is padded to S in {1, 2, 4, 8} (K <= 8192): padding stages
-// re-read the last real weights (into a slot never read again) and multiply them by zero
-// tokens, and the whole per-wave sequence is unrolled, so it has no branches, constant ring
-// indices and exact waits.
+// Sparse (decode_sparse_kernel): a 512-thread workgroup owns 32 weight rows and all of K; its 8
+// wavefronts split K into 128-deep stages, each wave streaming its slice of the compressed
+// rows, index words and token rows through a PRIVATE LDS ring with global_load_lds_dwordx4,
+// so only the wave's own vmcnt orders the ring -- no barrier in the K loop (4 slots of
+// 4.5 KB, 3 stages in flight per wave). Stages feed 2 v_smfmac_i32_16x16x128_i8 (compressed
+// weights + index words as A, lane layout as in gemm_sparse.hip).
+//
+// Both: the per-wave INT32 partials are summed exactly through LDS, then the dequant epilogue
+// writes the outputs. Each wave's stage count is padded to S in {1, 2, 4, 8, 16} (K <= 8192):
+// padding stages re-read the wave's last real stage and multiply it by zero tokens, and the
+// per-wave stage sequence is unrolled, so it has no branches, constant ring slots and exact
+// waits.
 #include "common.h"
 #include "gemm_dense.h"
 #include "mfma_tile.h"
 
 namespace forge_amd {
 
+// Sparse decode geometry.
 constexpr int kDecRows = 32;       // weight rows per workgroup
 constexpr int kDecWaves = 8;
 constexpr int kDecTokRows = 16;    // token rows staged per stage (the MFMA's 16 columns)
+// Dense decode geometry: 16-row blocks per workgroup, waves (K split), stages in flight.
+constexpr int kDecDenseBlocks = 2;
+constexpr int kDecDenseWaves = 4;
+constexpr int kDecDenseAhead = 6;
 
-template <bool SPARSE>
-struct DecodeCfg {
-    // Per-wave ring slot: weights (dense 32 rows x 128 B; sparse 32 rows x 64 compressed B and
-    // 2 x 64 index words), then the stage's 16 token rows x 128 B.
-    static constexpr int kWBytes = SPARSE ? kDecRows * 64 : kDecRows * 128;
-    static constexpr int kIBytes = SPARSE ? 2 * 256 : 0;
+struct SparseDecodeCfg {
+    // Per-wave ring slot: 32 rows x 64 compressed bytes, 2 x 64 index words, then the stage's
+    // 16 token rows x 128 B.
+    static constexpr int kWBytes = kDecRows * 64;
+    static constexpr int kIBytes = 2 * 256;
     static constexpr int kXBytes = kDecTokRows * 128;
     static constexpr int kSlotBytes = kWBytes + kIBytes + kXBytes;
-    static constexpr int kSlots = SPARSE ? 4 : 3;                // ring depth: 144 KB of LDS either way
+    static constexpr int kSlots = 4;                             // ring depth: 144 KB of LDS
     static constexpr int kWIns = kWBytes / 1024;                 // 1 KB DMA instructions per stage
-    static constexpr int kVmPerStage = kWIns + (SPARSE ? 1 : 0) + kXBytes / 1024;
+    static constexpr int kVmPerStage = kWIns + 1 + kXBytes / 1024;
     static_assert(kDecWaves * kSlots * kSlotBytes <= 160 * 1024, "ring fits in LDS");
     static_assert(kDecWaves * 2 * 64 * 16 <= kDecWaves * kSlotBytes, "reduction area fits in slot 0");
 };
@@ -65,11 +73,6 @@ __device__ __forceinline__ void lds_read4(const int8_t* p0, const int8_t* p1, co
                  : "v"(lds_addr(p0)), "v"(lds_addr(p1)), "v"(lds_addr(p2)), "v"(lds_addr(p3))
                  : "memory");
 }
-__device__ __forceinline__ void lds_read2(const int8_t* p0, const int8_t* p1, v4i& a0, v4i& a1)
-{
-    asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
-                 : "=&v"(a0), "=&v"(a1) : "v"(lds_addr(p0)), "v"(lds_addr(p1)) : "memory");
-}
 __device__ __forceinline__ void lds_read_idx(const uint32_t* q0, const uint32_t* q1, int& i0, int& i1)
 {
     asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %3\n\ts_waitcnt lgkmcnt(0)"
@@ -79,20 +82,21 @@ __device__ __forceinline__ void lds_read_idx(const uint32_t* q0, const uint32_t*
 // S: stages per wave after padding (1, 2, 4 or 8). The per-wave stage sequence is
 // straight-line code with constant ring slots; every load in it is a DMA into LDS, so the only
 // vmcnt waits are the ring's own (whole stages, counted from the end).
-template <bool SPARSE, bool DEQUANT, int S>
-__global__ __launch_bounds__(kDecWaves * kWave) void decode_kernel(
+template <bool DEQUANT, int S>
+__global__ __launch_bounds__(kDecWaves * kWave) void decode_sparse_kernel(
     const int8_t* __restrict__ W, const uint32_t* __restrict__ meta, const int8_t* __restrict__ X,
     GemmEpilogue ep, int K)
 {
-    using Cfg = DecodeCfg<SPARSE>;
+    using Cfg = SparseDecodeCfg;
     constexpr int D = Cfg::kSlots;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    // One LDS array per ring slot (all waves' copies of that slot).
+    // One LDS array per ring slot (all waves' copies of that slot): distinct arrays carry
+    // distinct alias scopes.
     __shared__ __align__(16) int8_t slot0[kDecWaves * Cfg::kSlotBytes];
     __shared__ __align__(16) int8_t slot1[kDecWaves * Cfg::kSlotBytes];
     __shared__ __align__(16) int8_t slot2[kDecWaves * Cfg::kSlotBytes];
-    __shared__ __align__(16) int8_t slot3[SPARSE ? kDecWaves * Cfg::kSlotBytes : 16];
+    __shared__ __align__(16) int8_t slot3[kDecWaves * Cfg::kSlotBytes];
     auto slot_base = [&](int slot) -> int8_t* {
         int8_t* b = slot == 0 ? slot0 : slot == 1 ? slot1 : slot == 2 ? slot2 : slot3;
         return b + wave * Cfg::kSlotBytes;
@@ -107,17 +111,16 @@ __global__ __launch_bounds__(kDecWaves * kWave) void decode_kernel(
     const int ns = (s0 + S < nst ? s0 + S : nst) - s0;
 
     // DMA sources at K stage 0. Lane s of a 1 KB instruction fills LDS bytes [16 s, +16) of
-    // its part of the slot: row s >> 3 (dense, tokens) or s >> 2 (sparse weights), at the
-    // swizzled chunk position.
+    // its part of the slot: compressed row s >> 2 or token row s >> 3, at the swizzled chunk
+    // position.
     const int8_t* pw[Cfg::kWIns];
-    const int wrow_bytes = SPARSE ? K / 2 : K;
 #pragma unroll
     for (int q = 0; q < Cfg::kWIns; q++) {
         const int s = q * kWave + lane;
-        const int r = SPARSE ? (s >> 2) : (s >> 3);
-        const int c = SPARSE ? ((s & 3) ^ lds_swz4(r)) : ((s & 7) ^ lds_swz8(r));
+        const int r = s >> 2;
+        const int c = (s & 3) ^ lds_swz4(r);
         const int gr = (n0 + r) < N ? (n0 + r) : N - 1;
-        pw[q] = W + static_cast<size_t>(gr) * wrow_bytes + 16 * c;
+        pw[q] = W + static_cast<size_t>(gr) * (K / 2) + 16 * c;
     }
     const int8_t* px[2];
 #pragma unroll
@@ -127,24 +130,17 @@ __global__ __launch_bounds__(kDecWaves * kWave) void decode_kernel(
         const int c = (s & 7) ^ lds_swz8(r);
         px[q] = X + static_cast<size_t>(r < M ? r : M - 1) * K + 16 * c;   // rows >= M: zeroed on read
     }
-    const int8_t* pi = nullptr;
-    if constexpr (SPARSE) {
-        // 2 blocks of 16 rows x 64 words per stage; lanes 0..31 each copy 16 bytes.
-        const int cpr = K / 32;
-        int b = (n0 >> 4) + ((lane & 31) >> 4);
-        b = b < (N >> 4) ? b : (N >> 4) - 1;
-        pi = reinterpret_cast<const int8_t*>(meta + static_cast<size_t>(b) * cpr * 16) + 16 * (lane & 15);
-    }
+    // 2 blocks of 16 rows x 64 index words per stage; lanes 0..31 each copy 16 bytes.
+    int blk = (n0 >> 4) + ((lane & 31) >> 4);
+    blk = blk < (N >> 4) ? blk : (N >> 4) - 1;
+    const int8_t* pi = reinterpret_cast<const int8_t*>(meta + static_cast<size_t>(blk) * (K / 2)) + 16 * (lane & 15);
 
     auto issue = [&](int t, int slot) {
         const int st = s0 + (t < ns ? t : ns - 1);
         int8_t* dst = slot_base(slot);
-        const int wk = SPARSE ? st * 64 : st * 128;
 #pragma unroll
-        for (int q = 0; q < Cfg::kWIns; q++) dma16(pw[q] + wk, dst + q * 1024);
-        if constexpr (SPARSE) {
-            if (lane < 32) dma16(pi + st * 256, dst + Cfg::kWBytes);
-        }
+        for (int q = 0; q < Cfg::kWIns; q++) dma16(pw[q] + st * 64, dst + q * 1024);
+        if (lane < 32) dma16(pi + st * 256, dst + Cfg::kWBytes);
 #pragma unroll
         for (int q = 0; q < 2; q++) dma16(px[q] + st * 128, dst + Cfg::kWBytes + Cfg::kIBytes + q * 1024);
         // Keep the stages' DMAs in stage order for the counted waits.
@@ -156,37 +152,20 @@ __global__ __launch_bounds__(kDecWaves * kWave) void decode_kernel(
     auto compute = [&](int slot, bool real) {
         const int8_t* src = slot_base(slot);
         const int8_t* xs = src + Cfg::kWBytes + Cfg::kIBytes;
-        const bool live = tok && real;
-        if constexpr (SPARSE) {
-            // B: token row r16, K [16g, +16) and [64 + 16g, +16); A: compressed rows, chunk g.
-            v4i a0, a1, xlo, xhi;
-            lds_read4(src + lds_off64(r16, g), src + lds_off64(16 + r16, g), xs + lds_off128(r16, g),
-                      xs + lds_off128(r16, 4 + g), a0, a1, xlo, xhi);
-            int i0, i1;
-            const uint32_t* idx = reinterpret_cast<const uint32_t*>(src + Cfg::kWBytes);
-            lds_read_idx(idx + lane, idx + 64 + lane, i0, i1);
-            if (!live) {
-                xlo = v4i{0, 0, 0, 0};
-                xhi = v4i{0, 0, 0, 0};
-            }
-            const v8i b = __builtin_shufflevector(xlo, xhi, 0, 1, 2, 3, 4, 5, 6, 7);
-            acc[0] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a0, b, acc[0], i0, 0, 0);
-            acc[1] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a1, b, acc[1], i1, 0, 0);
-        } else {
-            // Two 16x16x64 steps h = 0, 1 over K [64h, +64): lane chunk g of each half.
-            v4i xlo, xhi, a00, a01, a10, a11;
-            lds_read4(src + lds_off128(r16, g), src + lds_off128(r16, 4 + g), src + lds_off128(16 + r16, g),
-                      src + lds_off128(16 + r16, 4 + g), a00, a01, a10, a11);
-            lds_read2(xs + lds_off128(r16, g), xs + lds_off128(r16, 4 + g), xlo, xhi);
-            if (!live) {
-                xlo = v4i{0, 0, 0, 0};
-                xhi = v4i{0, 0, 0, 0};
-            }
-            acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a00, xlo, acc[0], 0, 0, 0);
-            acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a01, xhi, acc[0], 0, 0, 0);
-            acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a10, xlo, acc[1], 0, 0, 0);
-            acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a11, xhi, acc[1], 0, 0, 0);
+        // B: token row r16, K [16g, +16) and [64 + 16g, +16); A: compressed rows, chunk g.
+        v4i a0, a1, xlo, xhi;
+        lds_read4(src + lds_off64(r16, g), src + lds_off64(16 + r16, g), xs + lds_off128(r16, g),
+                  xs + lds_off128(r16, 4 + g), a0, a1, xlo, xhi);
+        int i0, i1;
+        const uint32_t* idx = reinterpret_cast<const uint32_t*>(src + Cfg::kWBytes);
+        lds_read_idx(idx + lane, idx + 64 + lane, i0, i1);
+        if (!(tok && real)) {
+            xlo = v4i{0, 0, 0, 0};
+            xhi = v4i{0, 0, 0, 0};
         }
+        const v8i b = __builtin_shufflevector(xlo, xhi, 0, 1, 2, 3, 4, 5, 6, 7);
+        acc[0] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a0, b, acc[0], i0, 0, 0);
+        acc[1] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a1, b, acc[1], i1, 0, 0);
     };
 
     // Ring of D slots: stage t lives in slot t % D; issuing stage t + D - 1 reuses the slot of
@@ -216,13 +195,13 @@ __global__ __launch_bounds__(kDecWaves * kWave) void decode_kernel(
     red[(wave * 2 + 1) * kWave + lane] = acc[1];
     __syncthreads();
     if (threadIdx.x < 2 * kWave) {
-        const int blk = threadIdx.x / kWave;
-        v4i s = v4i{0, 0, 0, 0};
+        const int b = threadIdx.x / kWave;
+        v4i sum = v4i{0, 0, 0, 0};
 #pragma unroll
-        for (int w = 0; w < kDecWaves; w++) s += red[(w * 2 + blk) * kWave + lane];
+        for (int w = 0; w < kDecWaves; w++) sum += red[(w * 2 + b) * kWave + lane];
         const int m = r16;
         if (m < M) {
-            const int nb = n0 + 16 * blk + 4 * g;
+            const int nb = n0 + 16 * b + 4 * g;
             const float as = DEQUANT ? ep.act_scale[m] : 0.0f;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -230,34 +209,180 @@ __global__ __launch_bounds__(kDecWaves * kWave) void decode_kernel(
                 if (n >= N) continue;
                 const size_t o = static_cast<size_t>(m) * N + n;
                 if constexpr (DEQUANT) {
-                    const float b = ep.bias ? h2f(ep.bias[n]) : 0.0f;
-                    ep.c16[o] = dequant_gemm(s[e], as, h2f(ep.w_scale[n]), b, ep.bias != nullptr);
+                    const float bv = ep.bias ? h2f(ep.bias[n]) : 0.0f;
+                    ep.c16[o] = dequant_gemm(sum[e], as, h2f(ep.w_scale[n]), bv, ep.bias != nullptr);
                 } else {
-                    ep.c32[o] = s[e];
+                    ep.c32[o] = sum[e];
                 }
             }
         }
     }
 }
 
-template <bool SPARSE, bool DEQUANT, int S>
-static int launch_decode_s(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep, int K,
-                           hipStream_t s)
+template <typename T>
+__device__ __forceinline__ T ld_stream(const void* p)
 {
-    const unsigned grid = static_cast<unsigned>(divup(ep.N, kDecRows));
-    decode_kernel<SPARSE, DEQUANT, S><<<grid, kDecWaves * kWave, 0, s>>>(W, meta, X, ep, K);
+    return __builtin_nontemporal_load(reinterpret_cast<const T*>(p));
+}
+
+// 16 rows x 128 K of a row-major int8 matrix, loaded as two coalesced instructions (rows
+// 0..7 and 8..15; lane l reads row l % 8, 16-byte chunk l / 8, so each lane quad covers 64
+// contiguous bytes), then rearranged with one 8-lane swap (DPP row_ror:8) into the matrix-core
+// layout: lane l = 16 G + 8 b + i holds row l % 16 = 8 b + i, K chunks 2 G (step 0) and
+// 2 G + 1 (step 1). Both operands of the 16x16x64 product use this K order, so the dot
+// products are unchanged.
+__device__ __forceinline__ void swap8_rows(v4i own0, v4i own1, bool hi, v4i& h0, v4i& h1)
+{
+    const v4i x = hi ? own0 : own1;   // lanes of the low half send rows 8..15, the high half rows 0..7
+    v4i y;
+#pragma unroll
+    for (int k = 0; k < 4; k++) y[k] = __builtin_amdgcn_mov_dpp(x[k], 0x128, 0xF, 0xF, false);
+    h0 = hi ? y : own0;
+    h1 = hi ? own1 : y;
+}
+
+template <bool DEQUANT, int S, int RB, int WV, int AH>
+__global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void decode_dense_kernel(
+    const int8_t* __restrict__ W, const int8_t* __restrict__ X, GemmEpilogue ep, int K)
+{
+    __shared__ v4i red[WV * RB * kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int n0 = blockIdx.x * 16 * RB;
+    const int M = ep.M, N = ep.N;
+    const int r16 = lane & 15, g = lane >> 4;
+    const bool hi = (lane >> 3) & 1;
+
+    const int nst = K / 128;
+    const int s0 = wave * S < nst ? wave * S : nst;
+    const int ns = (s0 + S < nst ? s0 + S : nst) - s0;
+
+    // Load addresses: instruction j of block b reads row 16 b + 8 j + (lane % 8), chunk lane / 8.
+    const int8_t* pw[RB][2];
+#pragma unroll
+    for (int b = 0; b < RB; b++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int r = n0 + 16 * b + 8 * j + (lane & 7);
+            pw[b][j] = W + static_cast<size_t>(r < N ? r : N - 1) * K + 16 * (lane >> 3);
+        }
+    const int8_t* px[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int r = 8 * j + (lane & 7);
+        px[j] = X + static_cast<size_t>(r < M ? r : M - 1) * K + 16 * (lane >> 3);
+    }
+    const bool tok = r16 < M;   // after the swap, lane l holds token row l % 16
+
+    // Epilogue operands of waves 0..RB-1 (block b = wave: rows n0 + 16 b + 4 g + e, token
+    // r16), fetched before the K loop so that their latency hides behind it.
+    float e_as = 0.0f, e_ws[4] = {0.0f, 0.0f, 0.0f, 0.0f}, e_b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (DEQUANT && wave < RB) {
+        e_as = ep.act_scale[tok ? r16 : 0];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int n = n0 + 16 * wave + 4 * g + e;
+            const int nc = n < N ? n : N - 1;
+            e_ws[e] = h2f(ep.w_scale[nc]);
+            e_b[e] = ep.bias ? h2f(ep.bias[nc]) : 0.0f;
+        }
+    }
+
+    struct Stage { v4i w[RB][2], x[2]; };
+    auto load = [&](int t, Stage& f) {
+        const int st = s0 + (t < ns ? t : ns - 1);
+#pragma unroll
+        for (int b = 0; b < RB; b++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) f.w[b][j] = ld_stream<v4i>(pw[b][j] + st * 128);
+#pragma unroll
+        for (int j = 0; j < 2; j++) f.x[j] = *reinterpret_cast<const v4i*>(px[j] + st * 128);
+    };
+
+    v4i acc[RB];
+#pragma unroll
+    for (int b = 0; b < RB; b++) acc[b] = v4i{0, 0, 0, 0};
+    auto compute = [&](Stage& f, bool real) {
+        v4i x0, x1;
+        swap8_rows(f.x[0], f.x[1], hi, x0, x1);
+        if (!(tok && real)) {
+            x0 = v4i{0, 0, 0, 0};
+            x1 = v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int b = 0; b < RB; b++) {
+            v4i a0, a1;
+            swap8_rows(f.w[b][0], f.w[b][1], hi, a0, a1);
+            acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, x0, acc[b], 0, 0, 0);
+            acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, x1, acc[b], 0, 0, 0);
+        }
+    };
+
+    if (ns > 0) {
+        constexpr int A = AH < S ? AH : S;
+        Stage f[S];
+#pragma unroll
+        for (int t = 0; t < A; t++) load(t, f[t]);
+#pragma unroll
+        for (int t = 0; t < S; t++) {
+            if (t + A < S) load(t + A, f[t + A]);
+            compute(f[t], t < ns);
+        }
+    }
+
+#pragma unroll
+    for (int b = 0; b < RB; b++) red[(wave * RB + b) * kWave + lane] = acc[b];
+    __syncthreads();
+    if (wave < RB) {
+        const int b = wave;
+        v4i sum = red[b * kWave + lane];
+#pragma unroll
+        for (int w = 1; w < WV; w++) sum += red[(w * RB + b) * kWave + lane];
+        const int m = r16;
+        if (m < M) {
+            const int nb = n0 + 16 * b + 4 * g;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int n = nb + e;
+                if (n >= N) continue;
+                const size_t o = static_cast<size_t>(m) * N + n;
+                if constexpr (DEQUANT)
+                    ep.c16[o] = dequant_gemm(sum[e], e_as, e_ws[e], e_b[e], ep.bias != nullptr);
+                else
+                    ep.c32[o] = sum[e];
+            }
+        }
+    }
+}
+
+template <bool DEQUANT, int RB, int WV, int AH>
+static int launch_decode_dense(const int8_t* W, const int8_t* X, const GemmEpilogue& ep, int K, hipStream_t s)
+{
+    const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
+    const int per = divup(K / 128, WV);
+#define FORGE_DEC_DENSE(SS) decode_dense_kernel<DEQUANT, SS, RB, WV, AH><<<grid, WV * kWave, 0, s>>>(W, X, ep, K)
+    if (per <= 1) FORGE_DEC_DENSE(1);
+    else if (per <= 2) FORGE_DEC_DENSE(2);
+    else if (per <= 4) FORGE_DEC_DENSE(4);
+    else if (per <= 8) FORGE_DEC_DENSE(8);
+    else FORGE_DEC_DENSE(16);
+#undef FORGE_DEC_DENSE
     return launch_status();
 }
 
-template <bool SPARSE, bool DEQUANT>
-static int launch_decode_t(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep, int K,
-                           hipStream_t s)
+template <bool DEQUANT>
+static int launch_decode_sparse(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep,
+                                int K, hipStream_t s)
 {
+    const unsigned grid = static_cast<unsigned>(divup(ep.N, kDecRows));
     const int per = divup(K / 128, kDecWaves);
-    if (per <= 1) return launch_decode_s<SPARSE, DEQUANT, 1>(W, meta, X, ep, K, s);
-    if (per <= 2) return launch_decode_s<SPARSE, DEQUANT, 2>(W, meta, X, ep, K, s);
-    if (per <= 4) return launch_decode_s<SPARSE, DEQUANT, 4>(W, meta, X, ep, K, s);
-    return launch_decode_s<SPARSE, DEQUANT, 8>(W, meta, X, ep, K, s);
+#define FORGE_DEC_SPARSE(SS) decode_sparse_kernel<DEQUANT, SS><<<grid, kDecWaves * kWave, 0, s>>>(W, meta, X, ep, K)
+    if (per <= 1) FORGE_DEC_SPARSE(1);
+    else if (per <= 2) FORGE_DEC_SPARSE(2);
+    else if (per <= 4) FORGE_DEC_SPARSE(4);
+    else FORGE_DEC_SPARSE(8);
+#undef FORGE_DEC_SPARSE
+    return launch_status();
 }
 
 bool decode_supported(int M, int K) { return M <= kDecodeMaxM && K % 128 == 0 && K <= kDecodeMaxK; }
@@ -266,8 +391,9 @@ int launch_decode(const int8_t* W, const uint32_t* meta, const int8_t* X, const 
                   bool sparse, hipStream_t s)
 {
     if (!decode_supported(ep.M, K)) return FORGE_EINVAL;
-    if (sparse) return ep.c16 ? launch_decode_t<true, true>(W, meta, X, ep, K, s) : launch_decode_t<true, false>(W, meta, X, ep, K, s);
-    return ep.c16 ? launch_decode_t<false, true>(W, meta, X, ep, K, s) : launch_decode_t<false, false>(W, meta, X, ep, K, s);
+    if (sparse) return ep.c16 ? launch_decode_sparse<true>(W, meta, X, ep, K, s) : launch_decode_sparse<false>(W, meta, X, ep, K, s);
+    return ep.c16 ? launch_decode_dense<true, kDecDenseBlocks, kDecDenseWaves, kDecDenseAhead>(W, X, ep, K, s)
+                  : launch_decode_dense<false, kDecDenseBlocks, kDecDenseWaves, kDecDenseAhead>(W, X, ep, K, s);
 }
 
 }  // namespace forge_amd

@@ -23,7 +23,7 @@ int launch_gemm_skinny(const int8_t* A, const int8_t* B, const GemmEpilogue& ep,
 // Decode GEMM (M <= kDecodeMaxM tokens, K % 128 == 0): weights W (N,K) dense or W_comp (N,K/2) +
 // gfx950 index words (sparse), tokens X (M,K) int8; 16-byte aligned operands.
 constexpr int kDecodeMaxM = 16;
-constexpr int kDecodeMaxK = 8 * 8 * 128;   // 8 waves x 8 stages of 128
+constexpr int kDecodeMaxK = 8192;   // dense: 4 waves x 16 stages of 128; sparse: 8 waves x 8 stages
 bool decode_supported(int M, int K);
 int launch_decode(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep, int K,
                   bool sparse, hipStream_t s);
