@@ -1,6 +1,7 @@
 """Benchmark of the INT8 quantized-inference path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+    python bench.py --traffic-probe     (kernels for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)
 
 Headline (`value`): configs[1] of BASELINE.json -- the fused W8A8 linear at M=N=K=4096
 (FP16 activations with 8 outlier channels x20, per-token quantize, INT8 MFMA GEMM with
@@ -11,10 +12,13 @@ roofline: the dominant kernel (the GEMM) timed alone with HIP events on the laun
 algorithmic ops 2*M*N*K per launch against MI355X's dense INT8 peak (5.0 POP/s).
 cpu_baseline: the oracle's single-threaded INT32 loop + dequant epilogue (oracle/) over as
 many rows of the same workload as fit in ~12 s (all 4096 on an EPYC host), timed on this host.
-extra: configs[2] (2:4 sparse vs dense at 4096x11008x4096) and configs[3] (decode
+roofline.traffic: HBM bytes per launch of the GEMM, read from TRAFFIC_FILE, which records two
+rocprofv3 --pmc runs of `bench.py --traffic-probe` (FETCH_SIZE, then WRITE_SIZE) scaled by
+what the same counters read for a device copy of known size in the same runs.
+extra: configs[2] (2:4 sparse vs dense at 4096x11008x4096), configs[3] (decode
 M = 1/4/16, N = K = 8192, dense and 2:4, HBM GB/s with 6 rotating weight copies so the
 256 MB MALL cannot hold them; calls captured into a HIP graph and replayed so host launch
-overhead is not timed).
+overhead is not timed) and configs[4] (INT8 NHWC 3x3 conv, INT32 and dequant outputs).
 """
 from __future__ import annotations
 
@@ -33,6 +37,45 @@ sys.path.insert(0, ROOT)
 METRIC = "INT8 dense/2:4-sparse GEMM TOPS @4096^3 (% MFMA peak); M=16 HBM GB/s"
 PEAK_INT8_TOPS = 5000.0      # MI355X dense INT8 MFMA, 5.0 POP/s
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "int8_linear_c2_gemm_traffic.json")
+COPY_PROBE_BYTES = 256 << 20  # calibration copy for the traffic counters
+
+
+def measured_traffic():
+    """HBM bytes per GEMM launch from the committed counter runs, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return int(json.load(f)["gemm_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def traffic_probe() -> int:
+    """Launches for the two counter runs: the configs[1] dequant GEMM 5 times on the quantized
+    activations, then a COPY_PROBE_BYTES device-to-device copy 5 times (its FETCH_SIZE and
+    WRITE_SIZE give the counters' scale: COPY_PROBE_BYTES each, by construction)."""
+    import torch
+    import forge_amd
+    from forge_amd import ops
+    forge_amd.load()
+    dev = torch.device("cuda:0")
+    x, W, ws, b = make_c2(dev)
+    M, K = x.shape
+    N = W.shape[0]
+    sq = torch.empty((M, K), dtype=torch.int8, device=dev)
+    ss = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    ops.fused_quantize_activation(x, M, K, out=sq, scales=ss)
+    for _ in range(5):
+        ops.int8_gemm_dequant(sq, W, ss, ws, b, out=y)
+    src = torch.empty((COPY_PROBE_BYTES,), dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("traffic probe done", flush=True)
+    return 0
 
 
 def events_time_ms(fn, reps: int) -> float:
@@ -180,6 +223,32 @@ def bench_extra(dev):
         out[f"c4_M{M}_sparse_GBs"] = bytes_s / ts / 1e6
         out[f"c4_M{M}_dense_us"] = td * 1e3
         out[f"c4_M{M}_sparse_us"] = ts * 1e3
+    del Ws, comps, metas
+    torch.cuda.empty_cache()
+
+    # INT8 NHWC conv 3x3, pad 1, stride 1: (32,56,56,256) x (256,3,3,256) -> INT32,
+    # and the same with the per-channel dequant + bias epilogue (FP16 out). Implicit GEMM
+    # M = 32*56*56 = 100,352, N = 256, K = 2,304.
+    xc = torch.randint(-127, 128, (32, 56, 56, 256), generator=g, device=dev, dtype=torch.int8)
+    wc = torch.randint(-127, 128, (256, 3, 3, 256), generator=g, device=dev, dtype=torch.int8)
+    Mc = 32 * 56 * 56
+    asc = torch.full((Mc,), 0.02, dtype=torch.float32, device=dev)
+    wsc = (torch.rand((256,), generator=g, device=dev) * 9e-3 + 1e-3).half()
+    bc = (torch.randn((256,), generator=g, device=dev) * 0.1).half()
+    o32 = torch.empty((32, 56, 56, 256), dtype=torch.int32, device=dev)
+    o16 = torch.empty((32, 56, 56, 256), dtype=torch.float16, device=dev)
+    conv32 = lambda: ops.int8_conv2d_nhwc_s32(xc, wc, pad=(1, 1), out=o32)
+    conv16 = lambda: ops.int8_conv2d_nhwc_dequant(xc, wc, asc, wsc, bc, pad=(1, 1), out=o16)
+    for _ in range(3):
+        conv32()
+        conv16()
+    t32 = events_time_ms(conv32, 10)
+    t16 = events_time_ms(conv16, 10)
+    ops_c = 2.0 * Mc * 256 * 2304
+    out["c5_conv_s32_tops"] = ops_c / t32 / 1e9
+    out["c5_conv_s32_us"] = t32 * 1e3
+    out["c5_conv_dequant_tops"] = ops_c / t16 / 1e9
+    out["c5_conv_dequant_us"] = t16 * 1e3
     return out
 
 
@@ -190,7 +259,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true")
     args = ap.parse_args()
+    if args.traffic_probe:
+        return traffic_probe()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(the W8A8 kernels shard by token rows or weight columns with no communication).",
@@ -235,8 +307,9 @@ def main() -> int:
         gemm()
     t_gemm = events_time_ms(gemm, 50)
     achieved = 2.0 * M * N * K / (t_gemm * 1e-3) / 1e12
+    # quantize is short enough that per-call host launch cost would dominate events: graph replay
     quant = lambda: ops.fused_quantize_activation(x, M, K, out=sq, scales=ss)
-    t_q = events_time_ms(quant, 50)
+    t_q = graph_time_ms([quant] * 20)
 
     line = {
         "metric": METRIC,
@@ -255,7 +328,7 @@ def main() -> int:
         "config": {"workload": "configs[1] fused W8A8 linear, M=N=K=4096, fp16 in/out",
                    "M": M, "N": N, "K": K, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": measured_traffic(),
                      "kernel": "gemm_dma_kernel<256,256,dequant>", "kernel_ms": round(t_gemm, 5),
                      "quantize_ms": round(t_q, 5)},
     }
