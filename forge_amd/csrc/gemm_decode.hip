@@ -13,7 +13,11 @@
 // faster than staging it through LDS: coalesced register loads at this shape reach ~6 TB/s in
 // isolation, LDS DMA rings of any shape stay under 4.8 TB/s.
 //
-// Sparse (decode_sparse_kernel): a 512-thread workgroup owns 32 weight rows and all of K; its 8
+// Sparse, up to 8 tokens (decode_sparse_reg_kernel): the dense kernel's structure on 256-deep
+// segments of compressed rows, with a K permutation that keeps the SMFMAC operands consistent
+// (described at the kernel).
+//
+// Sparse, 9-16 tokens (decode_sparse_kernel): a 512-thread workgroup owns 32 weight rows and all of K; its 8
 // wavefronts split K into 128-deep stages, each wave streaming its slice of the compressed
 // rows, index words and token rows through a PRIVATE LDS ring with global_load_lds_dwordx4,
 // so only the wave's own vmcnt orders the ring -- no barrier in the K loop (4 slots of
@@ -39,6 +43,7 @@ constexpr int kDecTokRows = 16;    // token rows staged per stage (the MFMA's 16
 constexpr int kDecDenseBlocks = 2;
 constexpr int kDecDenseWaves = 4;
 constexpr int kDecDenseAhead = 6;
+constexpr int kDecSparseRegMaxM = 8;   // register sparse kernel up to this many tokens
 
 struct SparseDecodeCfg {
     // Per-wave ring slot: 32 rows x 64 compressed bytes, 2 x 64 index words, then the stage's
@@ -355,6 +360,151 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
     }
 }
 
+// 2:4 sparse decode on coalesced register loads. A stage is a 256-deep dense K segment:
+// per 16-row block, two coalesced instructions read 8 compressed rows x 128 bytes each (the
+// segment's 2 x 64 compressed bytes per row), and the 8-lane swap leaves lane l = 16 G + 8 b + i
+// with row l % 16 and compressed chunks 2 G and 2 G + 1. SMFMAC step h (0, 1) takes chunk
+// 2 G + h in lane group G, i.e. the dense K range [32 (2 G + h), +32) of the segment stands in
+// for the instruction's K range [32 G, +32) of its 128-deep step. Whole 4-groups move, so the
+// index nibbles stay valid: the lane's index word is the packed word of 32-K chunk
+// 8 seg + 2 G + h, and the token operand is gathered with the same permutation.
+template <bool DEQUANT, int S, int RB, int WV, int AH>
+__global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void decode_sparse_reg_kernel(
+    const int8_t* __restrict__ W, const uint32_t* __restrict__ meta, const int8_t* __restrict__ X,
+    GemmEpilogue ep, int K)
+{
+    __shared__ v4i red[WV * RB * kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int n0 = blockIdx.x * 16 * RB;
+    const int M = ep.M, N = ep.N;
+    const int r16 = lane & 15, g = lane >> 4;
+    const bool hi = (lane >> 3) & 1;
+
+    const int nseg = K / 256;
+    const int s0 = wave * S < nseg ? wave * S : nseg;
+    const int ns = (s0 + S < nseg ? s0 + S : nseg) - s0;
+
+    // Compressed rows (K/2 bytes): instruction j of block b reads row 16 b + 8 j + lane % 8,
+    // chunk lane / 8 of the segment's 128 bytes.
+    const int8_t* pw[RB][2];
+    const uint32_t* pi[RB][2];
+#pragma unroll
+    for (int b = 0; b < RB; b++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int r = n0 + 16 * b + 8 * j + (lane & 7);
+            pw[b][j] = W + static_cast<size_t>(r < N ? r : N - 1) * (K / 2) + 16 * (lane >> 3);
+        }
+        // Packed index words of block b: stage s (128 dense K) holds 64 words, the word of
+        // (row r, 32-K chunk 4 s + q) at 16 q + r. Chunk 8 seg + 2 g + h lies in stage
+        // 2 seg + (2 g + h) / 4 at q = (2 g + h) % 4.
+        const int blk = (n0 >> 4) + b < (N >> 4) ? (n0 >> 4) + b : (N >> 4) - 1;
+        const uint32_t* base = meta + static_cast<size_t>(blk) * (K / 2) + r16;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int c = 2 * g + h;
+            pi[b][h] = base + (c >> 2) * 64 + 16 * (c & 3);
+        }
+    }
+    // Tokens: row r16 (clamped; rows >= M are zeroed). Step h reads the segment's dense bytes
+    // [64 (g >> 1) + 32 h + 16 (g & 1), +16) and the same + 128.
+    const bool tok = r16 < M;
+    const int8_t* px = X + static_cast<size_t>(tok ? r16 : M - 1) * K + 64 * (g >> 1) + 16 * (g & 1);
+
+    struct Stage { v4i w[RB][2], x[4]; int ix[RB][2]; };
+    auto load = [&](int t, Stage& f) {
+        const int sg = s0 + (t < ns ? t : ns - 1);
+#pragma unroll
+        for (int b = 0; b < RB; b++) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) f.w[b][j] = ld_stream<v4i>(pw[b][j] + sg * 128);
+#pragma unroll
+            for (int h = 0; h < 2; h++) f.ix[b][h] = static_cast<int>(ld_stream<uint32_t>(pi[b][h] + sg * 128));
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            f.x[2 * h] = *reinterpret_cast<const v4i*>(px + sg * 256 + 32 * h);
+            f.x[2 * h + 1] = *reinterpret_cast<const v4i*>(px + sg * 256 + 32 * h + 128);
+        }
+    };
+
+    v4i acc[RB];
+#pragma unroll
+    for (int b = 0; b < RB; b++) acc[b] = v4i{0, 0, 0, 0};
+    auto compute = [&](Stage& f, bool real) {
+        const bool live = tok && real;
+        v8i xb[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const v4i lo = live ? f.x[2 * h] : v4i{0, 0, 0, 0};
+            const v4i hi4 = live ? f.x[2 * h + 1] : v4i{0, 0, 0, 0};
+            xb[h] = __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+#pragma unroll
+        for (int b = 0; b < RB; b++) {
+            v4i a0, a1;
+            swap8_rows(f.w[b][0], f.w[b][1], hi, a0, a1);
+            acc[b] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a0, xb[0], acc[b], f.ix[b][0], 0, 0);
+            acc[b] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a1, xb[1], acc[b], f.ix[b][1], 0, 0);
+        }
+    };
+
+    if (ns > 0) {
+        constexpr int A = AH < S ? AH : S;
+        Stage f[S];
+#pragma unroll
+        for (int t = 0; t < A; t++) load(t, f[t]);
+#pragma unroll
+        for (int t = 0; t < S; t++) {
+            if (t + A < S) load(t + A, f[t + A]);
+            compute(f[t], t < ns);
+        }
+    }
+
+#pragma unroll
+    for (int b = 0; b < RB; b++) red[(wave * RB + b) * kWave + lane] = acc[b];
+    __syncthreads();
+    if (wave < RB) {
+        const int b = wave;
+        v4i sum = red[b * kWave + lane];
+#pragma unroll
+        for (int w = 1; w < WV; w++) sum += red[(w * RB + b) * kWave + lane];
+        const int m = r16;
+        if (m < M) {
+            const int nb = n0 + 16 * b + 4 * g;
+            const float as = DEQUANT ? ep.act_scale[m] : 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int n = nb + e;
+                if (n >= N) continue;
+                const size_t o = static_cast<size_t>(m) * N + n;
+                if constexpr (DEQUANT) {
+                    const float bv = ep.bias ? h2f(ep.bias[n]) : 0.0f;
+                    ep.c16[o] = dequant_gemm(sum[e], as, h2f(ep.w_scale[n]), bv, ep.bias != nullptr);
+                } else {
+                    ep.c32[o] = sum[e];
+                }
+            }
+        }
+    }
+}
+
+template <bool DEQUANT, int RB, int WV, int AH>
+static int launch_decode_sparse_reg(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep,
+                                    int K, hipStream_t s)
+{
+    const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
+    const int per = divup(K / 256, WV);
+#define FORGE_DEC_SPREG(SS) decode_sparse_reg_kernel<DEQUANT, SS, RB, WV, AH><<<grid, WV * kWave, 0, s>>>(W, meta, X, ep, K)
+    if (per <= 1) FORGE_DEC_SPREG(1);
+    else if (per <= 2) FORGE_DEC_SPREG(2);
+    else if (per <= 4) FORGE_DEC_SPREG(4);
+    else FORGE_DEC_SPREG(8);
+#undef FORGE_DEC_SPREG
+    return launch_status();
+}
+
 template <bool DEQUANT, int RB, int WV, int AH>
 static int launch_decode_dense(const int8_t* W, const int8_t* X, const GemmEpilogue& ep, int K, hipStream_t s)
 {
@@ -391,6 +541,11 @@ int launch_decode(const int8_t* W, const uint32_t* meta, const int8_t* X, const 
                   bool sparse, hipStream_t s)
 {
     if (!decode_supported(ep.M, K)) return FORGE_EINVAL;
+    // Sparse: up to 8 tokens the register kernel is faster (its token loads are light); at
+    // 9-16 tokens the token stream equals the weight stream and the DMA ring is ahead.
+    if (sparse && K % 256 == 0 && ep.M <= kDecSparseRegMaxM)
+        return ep.c16 ? launch_decode_sparse_reg<true, 2, 4, 4>(W, meta, X, ep, K, s)
+                      : launch_decode_sparse_reg<false, 2, 4, 4>(W, meta, X, ep, K, s);
     if (sparse) return ep.c16 ? launch_decode_sparse<true>(W, meta, X, ep, K, s) : launch_decode_sparse<false>(W, meta, X, ep, K, s);
     return ep.c16 ? launch_decode_dense<true, kDecDenseBlocks, kDecDenseWaves, kDecDenseAhead>(W, X, ep, K, s)
                   : launch_decode_dense<false, kDecDenseBlocks, kDecDenseWaves, kDecDenseAhead>(W, X, ep, K, s);

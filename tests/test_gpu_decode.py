@@ -3,8 +3,9 @@ dense and 2:4 sparse, against the oracle.
 
 Bar: INT32 bit-exact; FP16 bit-exact to the oracle's epilogue. Shapes exercise the kernel's
 K split over 8 wavefronts (K = 128: one wave works; K = 1152: 9 stages, uneven slices and
-idle waves), ragged N (not a multiple of the 32-row workgroup tile), M from 1 to 16, and
-configs[3] at full size (M = 16, N = K = 8192; sampled output columns)."""
+idle waves), ragged N (not a multiple of the 32-row workgroup tile), M from 1 to 16 (the
+sparse register kernel for M <= 8 with K % 256 == 0, the DMA-ring kernel otherwise), and
+configs[3] at full size (M = 16 and 1, N = K = 8192; sampled output columns)."""
 import numpy as np
 import pytest
 
@@ -13,7 +14,9 @@ from helpers import fp16_normal, int8_uniform, poison, say, to_dev, to_host
 pytestmark = pytest.mark.gpu
 
 DENSE = [(1, 128, 32), (3, 1152, 96), (16, 2048, 50), (7, 4096, 200), (16, 1024, 8)]
-SPARSE = [(1, 128, 32), (5, 1152, 48), (16, 2048, 208), (9, 4096, 1024), (16, 1024, 16)]
+# K % 256 == 0 with M <= 8 runs the register kernel; the rest run the DMA-ring kernel.
+SPARSE = [(1, 128, 32), (5, 1152, 48), (16, 2048, 208), (9, 4096, 1024), (16, 1024, 16),
+          (1, 256, 32), (5, 1280, 48), (8, 2048, 208), (3, 768, 16), (4, 8192, 1024)]
 
 
 @pytest.mark.parametrize("M,K,N", DENSE)
@@ -66,13 +69,14 @@ def test_decode_sparse(dev, orc, M, K, N):
         assert np.array_equal(to_host(Y).view(np.uint16), orc.dequant_epilogue(acc, act, ws, b).view(np.uint16))
 
 
-def test_config4_full_size_sampled(dev, orc):
-    """M = 16 tokens, N = K = 8192, dense and 2:4, FP16 tokens quantized per
+@pytest.mark.parametrize("M", [16, 1])
+def test_config4_full_size_sampled(dev, orc, M):
+    """M = 16 and 1 tokens, N = K = 8192, dense and 2:4, FP16 tokens quantized per
     token, dequant + bias; sampled output columns against the oracle."""
     import torch
     from forge_amd import ops
-    rng = np.random.default_rng(4)
-    M, K, N = 16, 8192, 8192
+    rng = np.random.default_rng(4 + M)
+    K, N = 8192, 8192
     W = int8_uniform(rng, (N, K))
     x = fp16_normal(rng, (M, K))
     ws = rng.uniform(1e-3, 1e-2, N).astype(np.float16)
@@ -86,7 +90,7 @@ def test_config4_full_size_sampled(dev, orc):
     xd, Wd, wsd, bd = to_dev(x, dev), to_dev(W, dev), to_dev(ws, dev), to_dev(b, dev)
     sq = torch.empty((M, K), dtype=torch.int8, device=dev)
     ss = torch.empty((M,), dtype=torch.float32, device=dev)
-    say("config4 dense 16x8192x8192")
+    say(f"config4 dense {M}x8192x8192")
     yd = to_host(ops.int8_linear(xd, Wd, wsd, bd, sq, ss)).view(np.uint16)
     assert np.array_equal(yd[:, cols], ref_d)
     comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
@@ -94,6 +98,6 @@ def test_config4_full_size_sampled(dev, orc):
     meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
     ops.prune_compress_24(Wd, comp, raw, N, K)
     ops.pack_metadata(raw, meta, N, K)
-    say("config4 sparse 16x8192x8192")
+    say(f"config4 sparse {M}x8192x8192")
     ys = to_host(ops.sparse_int8_linear(xd, comp, meta, wsd, bd, sq, ss)).view(np.uint16)
     assert np.array_equal(ys[:, cols], ref_s)
