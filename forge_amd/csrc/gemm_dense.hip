@@ -41,17 +41,18 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_nt_kernel(
     store_tile<BM, BN, DEQUANT>(t.acc, ep, m0, n0, lds);
 }
 
-// DMA engine: row-major operands, K % 128 == 0, 16-byte aligned.
-template <int BM, int BN, bool DEQUANT>
+// DMA engine: K % 128 == 0, 16-byte aligned; OpA is a row-major matrix or the NHWC im2col
+// gather (DmaRowMajor / DmaConv), OpB the row-major weights.
+template <int BM, int BN, bool DEQUANT, class OpA = DmaRowMajor>
 __global__ __launch_bounds__(kGemmThreads) void gemm_dma_kernel(
-    const int8_t* __restrict__ A, const int8_t* __restrict__ B, GemmEpilogue ep, int tiles_m, int tiles_n, int K)
+    OpA opa, DmaRowMajor opb, GemmEpilogue ep, int tiles_m, int tiles_n, int K)
 {
     extern __shared__ __align__(16) int8_t lds[];
     int tm, tn;
     tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     DmaTile<BM, BN> t;
-    t.run(A, B, ep.M, ep.N, K, m0, n0, lds);
+    t.run(opa, opb, K, m0, n0, lds);
     store_tile<BM, BN, DEQUANT>(t.acc, ep, m0, n0, lds);
 }
 
@@ -80,20 +81,22 @@ static int launch_tile(const OpA& opa, const OpB& opb, const GemmEpilogue& ep, i
     return launch_status();
 }
 
-template <int BM, int BN, bool DEQUANT>
-static int launch_dma(const int8_t* A, const int8_t* B, const GemmEpilogue& ep, int M, int N, int K,
+template <int BM, int BN, bool DEQUANT, class OpA>
+static int launch_dma(const OpA& opa, const DmaRowMajor& opb, const GemmEpilogue& ep, int M, int N, int K,
                       hipStream_t s)
 {
     constexpr int lds = tile_lds_bytes<DmaTile<BM, BN>, BM, BN, DEQUANT>();
     const int tiles_m = divup(M, BM), tiles_n = divup(N, BN);
     const long long total = static_cast<long long>(tiles_m) * tiles_n;
     if (total > 0x7FFFFFFFLL) return FORGE_EINVAL;
-    auto kern = gemm_dma_kernel<BM, BN, DEQUANT>;
+    auto kern = gemm_dma_kernel<BM, BN, DEQUANT, OpA>;
     static const int attr = allow_lds(kern, lds);
     if (attr != FORGE_OK) return attr;
-    gemm_dma_kernel<BM, BN, DEQUANT><<<static_cast<unsigned>(total), kGemmThreads, lds, s>>>(A, B, ep, tiles_m, tiles_n, K);
+    gemm_dma_kernel<BM, BN, DEQUANT, OpA>
+        <<<static_cast<unsigned>(total), kGemmThreads, lds, s>>>(opa, opb, ep, tiles_m, tiles_n, K);
     return launch_status();
 }
+
 
 // Tile choice: the largest tile whose grid still covers the chip's CUs; smaller tiles
 // trade MFMA efficiency (operand reuse) for parallelism.
@@ -110,6 +113,24 @@ static TileCfg pick_tile(int M, int N, int cu) {
 static int cu_count(int* st) {
     const DeviceInfo& d = device_info(st);
     return d.cu_count;
+}
+
+// DMA engine with the tile chosen for the grid (256 or 128; smaller grids take the
+// register-staged engine): returns -1 when the DMA engine does not apply.
+template <class OpA>
+static int dispatch_dma(const OpA& opa, const DmaRowMajor& opb, const GemmEpilogue& ep, int M, int N, int K,
+                        hipStream_t s)
+{
+    int st = FORGE_OK;
+    const int cu = cu_count(&st);
+    if (st != FORGE_OK) return st;
+    const TileCfg t = pick_tile(M, N, cu);
+    const bool out16 = ep.c16 != nullptr;
+    if (t == TileCfg::k256)
+        return out16 ? launch_dma<256, 256, true>(opa, opb, ep, M, N, K, s) : launch_dma<256, 256, false>(opa, opb, ep, M, N, K, s);
+    if (t == TileCfg::k128)
+        return out16 ? launch_dma<128, 128, true>(opa, opb, ep, M, N, K, s) : launch_dma<128, 128, false>(opa, opb, ep, M, N, K, s);
+    return -1;
 }
 
 // MAX256: whether the 256 x 256 tile may be used (the byte-gather operands of odd shapes
@@ -143,6 +164,13 @@ int launch_conv_gemm(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep,
                      hipStream_t s)
 {
     const int M = g.rows, K = g.K;
+    // DMA engine when every 128-deep stage of a patch row is one pixel's contiguous channels.
+    if (vec && g.C % kBK == 0 && aligned(w, 16)) {
+        DmaConv a;
+        static_cast<ConvGeom&>(a) = g;
+        const int r = dispatch_dma(a, DmaRowMajor{w, Co, K}, ep, M, Co, K, s);
+        if (r != -1) return r;
+    }
     if (vec) {
         ConvOperand a;
         static_cast<ConvGeom&>(a) = g;
@@ -175,14 +203,8 @@ int gemm_dense(const int8_t* A, const int8_t* B, const float* act_scale, const u
     if (M <= kSkinnyMaxM && vec)
         return launch_gemm_skinny(A, B, ep, M, K, N, s);
     if (vec && K % kBK == 0) {
-        int st = FORGE_OK;
-        const int cu = cu_count(&st);
-        if (st != FORGE_OK) return st;
-        const TileCfg t = pick_tile(M, N, cu);
-        if (t == TileCfg::k256)
-            return out16 ? launch_dma<256, 256, true>(A, B, ep, M, N, K, s) : launch_dma<256, 256, false>(A, B, ep, M, N, K, s);
-        if (t == TileCfg::k128)
-            return out16 ? launch_dma<128, 128, true>(A, B, ep, M, N, K, s) : launch_dma<128, 128, false>(A, B, ep, M, N, K, s);
+        const int r = dispatch_dma(DmaRowMajor{A, M, K}, DmaRowMajor{B, N, K}, ep, M, N, K, s);
+        if (r != -1) return r;
     }
     if (vec) {
         RowMajorOperand a{A, M, K}, b{B, N, K};

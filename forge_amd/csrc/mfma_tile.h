@@ -316,6 +316,50 @@ struct NtTile {
 // s_waitcnt vmcnt(0) lgkmcnt(0) (expcnt unconstrained).
 __device__ __forceinline__ void wait_vm_lgkm0() { __builtin_amdgcn_s_waitcnt(0x7 << 4); }
 
+// DMA operand policies: where lane chunk c (16 bytes) of tile row r comes from at 128-deep
+// stage st. lane() runs once per DMA instruction; src() once per stage.
+
+// Row-major (rows, K) matrix, K % 128 == 0; rows past the end are clamped (never stored).
+struct DmaRowMajor {
+    const int8_t* p;
+    int rows, K;
+    using Lane = const int8_t*;
+    __device__ __forceinline__ Lane lane(int r, int c) const {
+        return p + static_cast<size_t>(r < rows ? r : rows - 1) * K + 16 * c;
+    }
+    __device__ __forceinline__ const int8_t* src(const Lane& l, int st) const { return l + st * kBK; }
+};
+
+// 128 zero bytes: the DMA source for im2col taps that fall in the padding.
+__device__ __align__(128) const int8_t g_dma_zero_line[128] = {};
+
+// Implicit im2col of an NHWC image, K order (kh, kw, c): with C % 128 == 0 a 128-deep stage of a
+// patch row is one contiguous run of one input pixel's channels, or padding (read from the zero
+// line). Needs a 16-byte aligned image.
+struct DmaConv : ConvGeom {
+    struct Lane {
+        const int8_t* img;   // this patch row's image
+        int hb, wb;          // top-left input coordinate of the patch
+        int c16;             // 16 * chunk
+    };
+    __device__ __forceinline__ Lane lane(int r, int c) const {
+        r = r < rows ? r : rows - 1;
+        const int wo = r % Wo;
+        const int t = r / Wo;
+        const int ho = t % Ho;
+        const int n = t / Ho;
+        return Lane{x + static_cast<size_t>(n) * H * W * C, ho * strideH - padH, wo * strideW - padW, 16 * c};
+    }
+    __device__ __forceinline__ const int8_t* src(const Lane& l, int st) const {
+        const int cps = C / kBK;                    // stages per tap (wave-uniform)
+        const int tap = st / cps, c0 = (st - tap * cps) * kBK;
+        const int kh = tap / kW, kw = tap - kh * kW;
+        const int hi = l.hb + kh * dilH, wi = l.wb + kw * dilW;
+        const bool ok = hi >= 0 && hi < H && wi >= 0 && wi < W;
+        return ok ? l.img + (static_cast<size_t>(hi) * W + wi) * C + c0 + l.c16 : g_dma_zero_line + l.c16;
+    }
+};
+
 template <int BM, int BN>
 struct DmaTile {
     static constexpr int kTM = BM / 2 / 32;
@@ -334,8 +378,8 @@ struct DmaTile {
 
     v16i acc[kTN][kTM];
 
-    __device__ __forceinline__ void run(const int8_t* A, const int8_t* B, int M, int N, int K, int m0, int n0,
-                                        int8_t* lds) {
+    template <class OpA, class OpB>
+    __device__ __forceinline__ void run(const OpA& opa, const OpB& opb, int K, int m0, int n0, int8_t* lds) {
         const int lane = threadIdx.x & (kWave - 1);
         const int wave = threadIdx.x / kWave;
         const int wm = (wave >> 1) * (BM / 2);
@@ -353,32 +397,30 @@ struct DmaTile {
         // DMA instruction q of this wave fills slot chunks s = (wave*kIns + q)*64 + lane:
         // row s/8 (8 lanes read one 128-byte line), physical chunk s%8 = logical chunk
         // (s%8) ^ swz(row) of that row.
-        const int8_t* pa[kAIns];
-        const int8_t* pb[kBIns];
+        typename OpA::Lane la[kAIns];
+        typename OpB::Lane lb[kBIns];
 #pragma unroll
         for (int q = 0; q < kAIns; q++) {
             const int s = (wave * kAIns + q) * kWave + lane;
             const int r = s >> 3, c = (s & 7) ^ lds_swz8(r);
-            const int gr = (m0 + r) < M ? (m0 + r) : M - 1;
-            pa[q] = A + static_cast<size_t>(gr) * K + 16 * c;
+            la[q] = opa.lane(m0 + r, c);
         }
 #pragma unroll
         for (int q = 0; q < kBIns; q++) {
             const int s = (wave * kBIns + q) * kWave + lane;
             const int r = s >> 3, c = (s & 7) ^ lds_swz8(r);
-            const int gr = (n0 + r) < N ? (n0 + r) : N - 1;
-            pb[q] = B + static_cast<size_t>(gr) * K + 16 * c;
+            lb[q] = opb.lane(n0 + r, c);
         }
         const int nst = K / kBK;
         // Stage st into slot st % 2; stages past the end re-read the last one (their slot is
         // never read again), so the issue needs no branch.
         auto issue = [&](int st) {
             int8_t* slot = lds + (st & 1) * kSlotBytes;
-            const int k0 = (st < nst ? st : nst - 1) * kBK;
+            const int sc = st < nst ? st : nst - 1;
 #pragma unroll
-            for (int q = 0; q < kAIns; q++) dma16(pa[q] + k0, slot + (wave * kAIns + q) * 1024);
+            for (int q = 0; q < kAIns; q++) dma16(opa.src(la[q], sc), slot + (wave * kAIns + q) * 1024);
 #pragma unroll
-            for (int q = 0; q < kBIns; q++) dma16(pb[q] + k0, slot + BM * kBK + (wave * kBIns + q) * 1024);
+            for (int q = 0; q < kBIns; q++) dma16(opb.src(lb[q], sc), slot + BM * kBK + (wave * kBIns + q) * 1024);
         };
         auto load_frags = [&](int st, int ks, Frags& F) {
             const int8_t* As = lds + (st & 1) * kSlotBytes;

@@ -1,8 +1,8 @@
 """GPU parity: INT8 conv2d.
 
 NHWC implicit GEMM: INT32 bit-exact vs the oracle's direct convolution (golden cases from
-torch float64 conv2d, padding / stride / dilation, C % 16 != 0 byte path, configs[4] at its
-full spatial size); FP16 dequant bit-exact to the oracle epilogue. NCHW FP16 API
+torch float64 conv2d, padding / stride / dilation, C % 16 != 0 byte path, the DMA gather for
+C % 128 == 0 at 128- and 256-row tiles, configs[4] at its full spatial size); FP16 dequant bit-exact to the oracle epilogue. NCHW FP16 API
 (src/nn/int8_conv2d.cu:126-223): bit-exact to the oracle composition im2col -> per-row
 quantize -> GEMM dequant -> NCHW, and within the reference test's float tolerance
 (tests/test_int8_conv2d.cu:166-176) of a float convolution."""
@@ -41,6 +41,28 @@ def test_conv_random(dev, orc, N, H, W, C, Co, k, pad, stride, dil):
     say(f"conv N={N} H={H} W={W} C={C} Co={Co} k={k}")
     out = ops.int8_conv2d_nhwc_s32(to_dev(x, dev), to_dev(w, dev), (pad, pad), (stride, stride), (dil, dil))
     assert np.array_equal(to_host(out), ref)
+
+
+# C % 128 == 0 with grids large enough for the DMA engine (128- and 256-row tiles): the
+# implicit-im2col gather by DMA, padding read from the zero line, ragged last tile.
+@pytest.mark.parametrize("N,H,W,C,Co,k,pad,stride,dil,check", [
+    (2, 64, 64, 128, 256, 3, 1, 1, 1, "all"),      # 128x128 tiles, padding
+    (2, 63, 61, 128, 384, 3, 1, 1, 1, "all"),      # ragged rows (7686)
+    (8, 130, 130, 128, 256, 3, 2, 2, 2, "ends"),   # 256x256 tiles, stride 2, dilation 2
+    (4, 40, 40, 256, 256, 1, 0, 1, 1, "all"),      # pointwise, two stages per tap
+])
+def test_conv_dma_gather(dev, orc, N, H, W, C, Co, k, pad, stride, dil, check):
+    from forge_amd import ops
+    rng = np.random.default_rng(H * W + C + Co)
+    x = int8_uniform(rng, (N, H, W, C))
+    w = int8_uniform(rng, (Co, k, k, C))
+    say(f"conv dma N={N} H={H} W={W} C={C} Co={Co} k={k} p={pad} s={stride} d={dil}")
+    out = to_host(ops.int8_conv2d_nhwc_s32(to_dev(x, dev), to_dev(w, dev), (pad, pad), (stride, stride),
+                                           (dil, dil)))
+    imgs = range(N) if check == "all" else (0, N - 1)
+    for n in imgs:
+        ref = orc.conv2d_nhwc_s32(x[n:n + 1], w, (pad, pad), (stride, stride), (dil, dil))
+        assert np.array_equal(out[n:n + 1], ref)
 
 
 def test_config5_full_size(dev, orc):
