@@ -83,7 +83,9 @@ def fused_dequantize_bias(input: torch.Tensor, act_scale: torch.Tensor, w_scale:
 # ---- dense GEMM (bindings.cpp:498-519) -------------------------------------------
 
 def int8_linear(x: torch.Tensor, w_int8: torch.Tensor, w_scale: torch.Tensor, bias: Optional[torch.Tensor],
-                scratch_a_int8: torch.Tensor, scratch_a_scale: torch.Tensor) -> torch.Tensor:
+                scratch_a_int8: torch.Tensor, scratch_a_scale: torch.Tensor,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """int8_dense.cuh:37-48; `out` may be passed to reuse an (M, N) FP16 buffer."""
     M, K = x.shape
     N = w_int8.shape[0]
     _need(x, torch.float16, "x")
@@ -93,7 +95,9 @@ def int8_linear(x: torch.Tensor, w_int8: torch.Tensor, w_scale: torch.Tensor, bi
         _need(bias, torch.float16, "bias", N)
     _need(scratch_a_int8, torch.int8, "scratch_a_int8", M * K)
     _need(scratch_a_scale, torch.float32, "scratch_a_scale", M)
-    out = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    _need(out, torch.float16, "out", M * N)
     _call("forge_int8_linear", _p(x), _p(w_int8), _p(w_scale), _p(bias), _p(out), M, K, N,
           _p(scratch_a_int8), _p(scratch_a_scale), _stream())
     return out

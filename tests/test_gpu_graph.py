@@ -1,0 +1,105 @@
+"""GPU: the hot-path entry points captured into HIP graphs.
+
+The reference's benchmark captures sparse_int8_gemm into a CUDA graph (bench_int8_sparse.cu:60-63),
+so every launcher must be capturable: no synchronisation, allocation, attribute or device query
+inside the capture, and no memset nodes (the split-K workspace is cleared by a kernel). Each graph
+is replayed several times with eager work and synchronisations between the replays, and every
+replay is compared bit-for-bit with the eager result of the same calls."""
+import numpy as np
+import pytest
+
+from helpers import fp16_normal, int8_uniform, say, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _replay_check(dev, calls, outputs, replays=4):
+    """Eager results of `calls`, then a captured graph of the same calls replayed `replays`
+    times; every output tensor must match the eager bits after each replay."""
+    import torch
+    for c in calls:
+        c()
+    torch.cuda.synchronize()
+    want = [o.clone() for o in outputs]
+    for o in outputs:
+        o.view(torch.uint8).fill_(0x7B)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for c in calls:          # warm-up on the capture stream (first-call attributes etc.)
+            c()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for c in calls:
+            c()
+    scratch = torch.empty((1 << 20,), dtype=torch.int32, device=dev)
+    for r in range(replays):
+        for o in outputs:
+            o.view(torch.uint8).fill_(0x5A)
+        scratch.fill_(r)                           # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, w in zip(outputs, want):
+            assert torch.equal(o.view(torch.uint8), w.view(torch.uint8)), f"replay {r} differs"
+
+
+def test_graph_int8_linear(dev):
+    """configs[1]-style fused linear (quantize + dequantizing GEMM), plus the decode shape."""
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(21)
+    for (M, K, N) in [(512, 1024, 768), (16, 4096, 1024), (3, 1152, 96)]:
+        say(f"graph int8_linear M={M} K={K} N={N}")
+        x = to_dev(fp16_normal(rng, (M, K)), dev)
+        w = to_dev(int8_uniform(rng, (N, K)), dev)
+        ws = to_dev(rng.uniform(1e-3, 1e-2, N).astype(np.float16), dev)
+        b = to_dev(fp16_normal(rng, (N,), 0.1), dev)
+        q = torch.empty((M, K), dtype=torch.int8, device=dev)
+        s = torch.empty((M,), dtype=torch.float32, device=dev)
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        c32 = torch.empty((M, N), dtype=torch.int32, device=dev)
+        calls = [lambda: ops.int8_linear(x, w, ws, b, q, s, out=y),
+                 lambda: ops.int8_gemm_s32(q, w, out=c32)]
+        _replay_check(dev, calls, [q, s, y, c32])
+
+
+def test_graph_sparse_splitk(dev):
+    """2:4 sparse GEMM with split-K (workspace cleared by a kernel, integer atomics, finalize),
+    the unsplit path and the decode shape."""
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(22)
+    for (M, K, N, split) in [(256, 2048, 512, 4), (256, 2048, 512, 1), (8, 2048, 256, 1)]:
+        say(f"graph sparse M={M} K={K} N={N} split={split}")
+        W = to_dev(int8_uniform(rng, (N, K)), dev)
+        comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+        raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+        meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+        ops.prune_compress_24(W, comp, raw, N, K)
+        ops.pack_metadata(raw, meta, N, K)
+        x = to_dev(int8_uniform(rng, (M, K)), dev)
+        act = to_dev(rng.uniform(1e-3, 5e-2, M).astype(np.float32), dev)
+        ws = to_dev(rng.uniform(1e-3, 1e-2, N).astype(np.float16), dev)
+        b = to_dev(fp16_normal(rng, (N,), 0.1), dev)
+        wsp = torch.empty((M * N,), dtype=torch.float32, device=dev)
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        calls = [lambda: ops.sparse_int8_gemm(comp, x, meta, act, ws, b, splitk_workspace=wsp, split_k=split,
+                                              out=y)]
+        _replay_check(dev, calls, [y])
+
+
+def test_graph_conv(dev):
+    """NHWC conv on the DMA gather (C % 128 == 0) and on the register engine (C = 48)."""
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(23)
+    for (N, H, W, C, Co) in [(2, 64, 64, 128, 256), (2, 9, 11, 48, 40)]:
+        say(f"graph conv N={N} H={H} W={W} C={C} Co={Co}")
+        x = to_dev(int8_uniform(rng, (N, H, W, C)), dev)
+        w = to_dev(int8_uniform(rng, (Co, 3, 3, C)), dev)
+        out = torch.empty((N, H, W, Co), dtype=torch.int32, device=dev)
+        calls = [lambda: ops.int8_conv2d_nhwc_s32(x, w, (1, 1), out=out)]
+        _replay_check(dev, calls, [out])
