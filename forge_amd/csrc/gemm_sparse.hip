@@ -466,12 +466,17 @@ struct SpDmaTile32 {
             const int gr = (m0 + r) < M ? (m0 + r) : M - 1;
             px[q] = X + static_cast<size_t>(gr) * K + 16 * c;
         }
+        // Index words: LDS chunk position s (16 blocks x 16 chunks of 4 words) takes chunk
+        // (s % 16) ^ 12 of its block in odd blocks (read below as word w ^ 48). The 16-lane
+        // groups of an index read (block parity x g) then start at banks {0, 48, 16, 32}
+        // (+32 for the odd step): distinct over all 64 lanes and within each 32-lane half.
         const int8_t* pi;
         {
             const int s = wave * kWave + lane;
             int b = (n0 >> 4) + (s >> 4);
             b = b < (N >> 4) ? b : (N >> 4) - 1;
-            pi = reinterpret_cast<const int8_t*>(meta + static_cast<size_t>(b) * cpr * 16) + 16 * (s & 15);
+            const int k = (s & 15) ^ (((s >> 4) & 1) * 12);
+            pi = reinterpret_cast<const int8_t*>(meta + static_cast<size_t>(b) * cpr * 16) + 16 * k;
         }
         const int nst = K / 128;
         auto issue = [&](int st) {
@@ -492,7 +497,8 @@ struct SpDmaTile32 {
             for (int j = 0; j < kTN; j++) {
                 const int r = wn + 32 * j + l31;
                 F.a[j] = *reinterpret_cast<const v4i*>(Ws + lds_off64(r, 2 * h + g));
-                F.idx[j] = static_cast<int>(Is[(r >> 4) * 64 + (2 * h + g) * 16 + (r & 15)]);
+                const int w = ((2 * h + g) * 16 + (r & 15)) ^ (((r >> 4) & 1) * 48);
+                F.idx[j] = static_cast<int>(Is[(r >> 4) * 64 + w]);
             }
 #pragma unroll
             for (int i = 0; i < kTM; i++) {
