@@ -631,7 +631,7 @@ __device__ __forceinline__ void sp_store_tile(const v4i (&acc)[8][BMT / 32], con
                 *reinterpret_cast<int4*>(strip + r16 * kRowBytes + ((u ^ (r16 & (kU - 1))) << 4)) =
                     make_int4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
             }
-            flush_rows<kU, 4, false>(strip, 16, ep, wm + 16 * j, wn);
+            flush_rows<kU, 4, false, true>(strip, 16, ep, wm + 16 * j, wn);
         }
     }
 }
