@@ -7,10 +7,9 @@
 //
 // Dense (decode_dense_kernel): a 256-thread workgroup owns 32 weight rows (16 for up to 4
 // tokens) and all of K; its 4 wavefronts split K into contiguous slices of 128-deep stages.
-// Operands are loaded straight
-// into registers with coalesced 8-row x 128-byte instructions (non-temporal for the weights,
-// which are read once), rearranged into the matrix-core layout by one DPP lane swap, and fed
-// to v_mfma_i32_16x16x64_i8. Measured on MI355X, this streams a 64 MB weight matrix from HBM
+// Operands are loaded straight into registers with coalesced 8-row x 128-byte instructions
+// (non-temporal for the weights, which are read once), rearranged into the matrix-core layout
+// by one DPP lane swap, and fed to v_mfma_i32_16x16x64_i8. Measured on MI355X, this streams a 64 MB weight matrix from HBM
 // faster than staging it through LDS: coalesced register loads at this shape reach ~6 TB/s in
 // isolation, LDS DMA rings of any shape stay under 4.8 TB/s.
 //
