@@ -9,9 +9,9 @@
 // tokens) and all of K; its 4 wavefronts split K into contiguous slices of 128-deep stages.
 // Operands are loaded straight into registers with coalesced 8-row x 128-byte instructions
 // (non-temporal for the weights, which are read once), rearranged into the matrix-core layout
-// by one DPP lane swap, and fed to v_mfma_i32_16x16x64_i8. Measured on MI355X, this streams a 64 MB weight matrix from HBM
-// faster than staging it through LDS: coalesced register loads at this shape reach ~6 TB/s in
-// isolation, LDS DMA rings of any shape stay under 4.8 TB/s.
+// by one DPP lane swap, and fed to v_mfma_i32_16x16x64_i8. Measured on MI355X, this streams a
+// 64 MB weight matrix from HBM faster than staging it through LDS: coalesced register loads at
+// this shape reach ~6 TB/s in isolation, LDS DMA rings of any shape stay under 4.8 TB/s.
 //
 // Sparse, up to 8 tokens (decode_sparse_reg_kernel): the dense kernel's structure on 256-deep
 // segments of compressed rows, with a K permutation that keeps the SMFMAC operands consistent
