@@ -212,9 +212,11 @@ constexpr int kBK = 128;
 __device__ __forceinline__ int lds_swz8(int r) { return (r ^ (r >> 3)) & 7; }
 __device__ __forceinline__ int lds_off128(int r, int c) { return r * kBK + ((c ^ lds_swz8(r)) << 4); }
 
-// 64-byte LDS rows (4 chunks): chunk c of row r at c ^ (((r >> 1) ^ (r >> 3)) & 3), conflict
-// free for 16-byte reads of the same chunk from 8 (or 16) consecutive rows.
-__device__ __forceinline__ int lds_swz4(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+// 64-byte LDS rows (4 chunks): chunk c of row r at c ^ (((r >> 1) ^ (r >> 4)) & 3). Measured
+// bank-conflict free (SQ_LDS_BANK_CONFLICT = 0) on gfx950 for ds_read_b128 in both matrix-core
+// operand orders over 64-byte rows: lane l -> row l % 32, chunk 2h + l / 32 (32x32 SMFMAC) and
+// lane l -> row l % 16, chunk l / 16 (16x16 SMFMAC); ((r >> 1) ^ (r >> 3)) & 3 is 2-way there.
+__device__ __forceinline__ int lds_swz4(int r) { return ((r >> 1) ^ (r >> 4)) & 3; }
 __device__ __forceinline__ int lds_off64(int r, int c) { return r * 64 + ((c ^ lds_swz4(r)) << 4); }
 
 template <int BM, int BN>
