@@ -106,3 +106,25 @@ def test_ops_module_imports_like_the_gpu_tests():
     from forge_amd import ops
     assert ops is forge_amd.ops
     assert callable(ops.int8_linear) and callable(ops.sparse_int8_gemm)
+
+
+def test_nn_modules_match_reference_state_dict_layout():
+    """QuantizedLinear / SparseLinear expose the reference's parameter and buffer names,
+    shapes and dtypes (python/forge/nn/linear.py:135-154, :206-226), so its state_dict loads."""
+    import torch
+    from forge_amd.nn import QuantizedLinear, SparseLinear
+    q = QuantizedLinear(256, 96)
+    sd = q.state_dict()
+    assert set(sd) == {"w_int8", "w_scale", "bias"}
+    assert sd["w_int8"].shape == (96, 256) and sd["w_int8"].dtype == torch.int8
+    assert sd["w_scale"].shape == (96,) and sd["w_scale"].dtype == torch.float16
+    assert sd["bias"].dtype == torch.float16
+    assert "bias" not in QuantizedLinear(256, 96, bias=False).state_dict()
+    s = SparseLinear(256, 96)
+    sd = s.state_dict()
+    assert set(sd) == {"W_comp", "w_meta", "w_scale", "bias"}
+    assert sd["W_comp"].shape == (96, 128) and sd["W_comp"].dtype == torch.int8
+    assert sd["w_meta"].shape == (96, 8) and sd["w_meta"].dtype == torch.int32
+    import pytest
+    with pytest.raises(ValueError):
+        SparseLinear(100, 96)
