@@ -5,7 +5,8 @@
 //   scale[m] = max(absmax(x[m,:]), 1e-8f) / 127.0f      (IEEE division)
 //   q[m,k]   = clamp(rne(x[m,k] * (1.0f / scale[m])), -128, 127)
 //
-// MI355X design: the main kernel gives each row to one 256-thread workgroup. A lane holds
+// MI355X design: the main kernel gives each row to one 256-thread workgroup (short rows at
+// large M: one wavefront per row, 4 rows per workgroup). A lane holds
 // VPT 16-byte vectors of its row in VGPRs, so x is read from HBM once; the row absmax is a
 // 64-lane butterfly per wave plus a 4-entry LDS max, then each lane writes 8 int8 per
 // vector. The exported two-pass kernel (any K, any alignment, any
@@ -87,6 +88,41 @@ __global__ __launch_bounds__(256) void quantize_rows_block_kernel(
 #pragma unroll
     for (int i = 0; i < VPT; i++) {
         const int idx = t + i * 256;
+        if (idx < nvec) dst[idx] = quant8(v[i], inv);
+    }
+}
+
+// Short rows (K <= 2048) at large M: one wavefront per row, 4 rows per workgroup, so a
+// workgroup moves 4 rows and the grid is M/4 workgroups instead of M tiny ones (at
+// M = 147,456, K = 1280 the per-row workgroups ran at 3.6 TB/s). Lane t holds vectors t, t + 64,
+// ... of its row; the absmax is a 64-lane butterfly. Same arithmetic as the kernels above.
+template <int VPT>
+__global__ __launch_bounds__(256) void quantize_rows_wave_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scales, int M, int K)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row = blockIdx.x * 4 + static_cast<int>(threadIdx.x / kWave);
+    if (row >= M) return;
+    const int nvec = K >> 3;
+    const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<size_t>(row) * K);
+    uint2* dst = reinterpret_cast<uint2*>(q + static_cast<size_t>(row) * K);
+    uint4 v[VPT];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const int idx = lane + i * kWave;
+        if (idx < nvec) {
+            v[i] = src[idx];
+            amax = absmax8(v[i], amax);
+        }
+    }
+    amax = wave_max(amax);
+    const float scale = row_scale(amax);
+    const float inv = 1.0f / scale;
+    if (lane == 0) scales[row] = scale;
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const int idx = lane + i * kWave;
         if (idx < nvec) dst[idx] = quant8(v[i], inv);
     }
 }
@@ -185,9 +221,21 @@ using namespace forge_amd;
 
 namespace forge_amd {
 
+// Rows per launch from which the wave-per-row kernel takes short rows: below it the grid is
+// small and a whole workgroup per row spreads each row's loads wider.
+constexpr int kWaveRowsMinM = 2048;
+
 int launch_quantize(const uint16_t* x, int8_t* q, float* scales, int M, int K, hipStream_t s)
 {
     const bool vec_ok = (K % 8 == 0) && K <= 8 * 2048 && aligned(x, 16) && aligned(q, 8);
+    if (vec_ok && K <= 2048 && M >= kWaveRowsMinM) {
+        const int vpt = divup(K, 8 * kWave);
+        const unsigned grid = static_cast<unsigned>(divup(M, 4));
+        if (vpt <= 1)      quantize_rows_wave_kernel<1><<<grid, 256, 0, s>>>(x, q, scales, M, K);
+        else if (vpt <= 2) quantize_rows_wave_kernel<2><<<grid, 256, 0, s>>>(x, q, scales, M, K);
+        else               quantize_rows_wave_kernel<4><<<grid, 256, 0, s>>>(x, q, scales, M, K);
+        return launch_status();
+    }
     if (vec_ok) {
         const int vpt = divup(K, 2048);
         if (vpt <= 1)      quantize_rows_block_kernel<1><<<M, 256, 0, s>>>(x, q, scales, K);

@@ -14,8 +14,11 @@ pytestmark = pytest.mark.gpu
 
 # tests/test_quantize.cu:103-113: vector path VPT 1..4, K > 8192, K % 8 != 0, misaligned,
 # and an input larger than L2.
+# The last four (M >= 2048, K <= 2048) run the wave-per-row kernel (1, 2 and 4 vectors per lane,
+# a ragged last workgroup).
 REF_CASES = [(32, 256, 0), (7, 8, 0), (64, 2056, 0), (16, 6144, 0), (16, 8192, 0), (5, 8200, 0),
-             (9, 100, 0), (9, 256, 1), (8192, 5120, 0)]
+             (9, 100, 0), (9, 256, 1), (8192, 5120, 0),
+             (2048, 1280, 0), (3001, 2048, 0), (2050, 8, 0), (4096, 1000, 0)]
 
 
 @pytest.mark.parametrize("M,K,offset", REF_CASES)
