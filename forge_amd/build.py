@@ -40,6 +40,8 @@ SOURCES = [
     "gemm_decode.hip",
     "gemm_sparse.hip",
     "conv.hip",
+    "conv_transpose.hip",
+    "conv_depthwise.hip",
     "forge_api.cpp",
 ]
 

@@ -15,6 +15,8 @@
 #include "forge/sparsity/prune_compress.h"
 #include "forge/sparsity/pack_metadata.h"
 #include "forge/nn/int8_conv2d.h"
+#include "forge/nn/int8_conv_transpose2d.h"
+#include "forge/nn/int8_depthwise_conv2d.h"
 
 namespace {
 thread_local int t_status = FORGE_OK;
@@ -172,6 +174,25 @@ void int8_conv2d_nhwc_dequant(const int8_t* x, const int8_t* w, const float* act
                               hipStream_t stream) {
     rec(forge_int8_conv2d_nhwc_dequant(x, w, act_scale, hb(w_scale), hb(bias), hb(out), N, H, W, C, Co, kH, kW, padH,
                                        padW, strideH, strideW, dilH, dilW, S(stream)));
+}
+
+size_t int8_conv_transpose2d_k2s2_workspace_size(int C_in, int H, int W, int C_out) {
+    return forge_int8_conv_transpose2d_k2s2_workspace_size(C_in, H, W, C_out);
+}
+
+void int8_conv_transpose2d_k2s2_forward(const __half* input, const int8_t* weight, const __half* w_scale,
+                                        const __half* bias, __half* output, int N, int C_in, int H, int W,
+                                        int C_out, void* workspace, hipStream_t stream) {
+    rec(forge_int8_conv_transpose2d_k2s2_forward(hb(input), weight, hb(w_scale), hb(bias), hb(output), N, C_in, H, W,
+                                                 C_out, workspace, S(stream)));
+}
+
+void int8_depthwise_conv2d_forward(const __half* input, const int8_t* weight, const __half* w_scale,
+                                   const __half* bias, __half* output, int N, int C, int H, int W, int kH, int kW,
+                                   int padH, int padW, int strideH, int strideW, int dilH, int dilW,
+                                   hipStream_t stream) {
+    rec(forge_int8_depthwise_conv2d_forward(hb(input), weight, hb(w_scale), hb(bias), hb(output), N, C, H, W, kH, kW,
+                                            padH, padW, strideH, strideW, dilH, dilW, S(stream)));
 }
 
 }  // namespace nn

@@ -10,11 +10,18 @@ namespace forge_amd {
 constexpr int kSkinnyMaxM = 16;
 
 int launch_quantize(const uint16_t* x, int8_t* q, float* scales, int M, int K, hipStream_t s);
+// Per-pixel rows of NCHW FP16 images: q (images*HW, C) int8 and scales (images*HW,).
+int launch_quantize_pixels_nchw(const uint16_t* x, int8_t* q, float* scales, int images, int C, int HW,
+                                hipStream_t s);
 
 // Dense C = A (M,K) x B (N,K)^T; writes out16 (dequant) if non-null, else out32.
 int gemm_dense(const int8_t* A, const int8_t* B, const float* act_scale, const uint16_t* w_scale,
                const uint16_t* bias, uint16_t* out16, int32_t* out32, int M, int K, int N,
                hipStream_t s);
+
+// The tile engines only (no decode or skinny kernels): every GemmEpilogue mode, including
+// the upsample scatter, which the decode and skinny kernels do not implement.
+int gemm_tiles(const int8_t* A, const int8_t* B, const GemmEpilogue& ep, int M, int K, int N, hipStream_t s);
 
 // Skinny (M <= kSkinnyMaxM) weight-streaming GEMM; needs K % 16 == 0 and 16-byte bases.
 int launch_gemm_skinny(const int8_t* A, const int8_t* B, const GemmEpilogue& ep, int M, int K, int N,

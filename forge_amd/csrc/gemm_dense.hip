@@ -105,7 +105,8 @@ enum class TileCfg { k256, k128, k64 };
 static TileCfg pick_tile(int M, int N, int cu) {
     const long long t256 = static_cast<long long>(divup(M, 256)) * divup(N, 256);
     const long long t128 = static_cast<long long>(divup(M, 128)) * divup(N, 128);
-    if (t256 * 2 >= cu) return TileCfg::k256;
+    // A side of 128 or less would leave half of a 256 tile (two of its four waves) idle.
+    if (t256 * 2 >= cu && M > 128 && N > 128) return TileCfg::k256;
     if (t128 * 2 >= cu) return TileCfg::k128;
     return TileCfg::k64;
 }
@@ -202,6 +203,13 @@ int gemm_dense(const int8_t* A, const int8_t* B, const float* act_scale, const u
         return launch_decode(B, nullptr, A, ep, K, false, s);
     if (M <= kSkinnyMaxM && vec)
         return launch_gemm_skinny(A, B, ep, M, K, N, s);
+    return gemm_tiles(A, B, ep, M, K, N, s);
+}
+
+int gemm_tiles(const int8_t* A, const int8_t* B, const GemmEpilogue& ep, int M, int K, int N, hipStream_t s)
+{
+    const bool vec = (K % 16 == 0) && aligned(A, 16) && aligned(B, 16);
+    const bool out16 = ep.c16 != nullptr;
     if (vec && K % kBK == 0) {
         const int r = dispatch_dma(DmaRowMajor{A, M, K}, DmaRowMajor{B, N, K}, ep, M, N, K, s);
         if (r != -1) return r;

@@ -495,10 +495,18 @@ struct GemmEpilogue {
     int32_t* c32;
     uint16_t* c16;
     const float* act_scale;     // (M,)  FP16 mode only
-    const uint16_t* w_scale;    // (N,)
+    const uint16_t* w_scale;    // (N,), or (N/4,) in the upsample scatter
     const uint16_t* bias;       // (N,) or nullptr
     int M, N;
-    int vec_out;                // 16-byte row stores allowed (N * elem % 16 == 0, base aligned)
+    int vec_out;                // 16-byte row stores allowed (N * elem % 16 == 0, base aligned);
+                                // in the upsample scatter: W % 4 == 0 and c16 16-byte aligned
+    // ConvTranspose2d kernel-2 stride-2 scatter (FP16 only; up_w == 0 = plain (M, N) rows):
+    // row m is pixel (img, h, w) of img * up_hw + h * up_w + w, column n = co*4 + kh*2 + kw,
+    // and the value goes to c16[img][co][2h + kh][2w + kw] (NCHW, (2H) x (2W) planes). The
+    // scale is w_scale[co]; the GEMM value is rounded to FP16, then post_bias[co] (if any) is
+    // added in fp32 and rounded again (src/nn/int8_conv_transpose2d.cu:70-102, 174-189).
+    int up_w, up_hw;
+    const uint16_t* post_bias;
 };
 
 // Copies `rows` x kU 16-byte units of a wave-private staging area (rows of kRowBytes, unit u
@@ -540,6 +548,76 @@ __device__ __forceinline__ void flush_rows(const int8_t* stage, int rows, const 
                     ep.c16[o + t] = static_cast<uint16_t>(w[t >> 1] >> (16 * (t & 1)));
                 else
                     ep.c32[o + t] = static_cast<int32_t>(w[t]);
+            }
+        }
+    }
+}
+
+// Adds an fp16 bias to both halves of a packed pair, each in fp32 and rounded again.
+__device__ __forceinline__ uint32_t add_bias_pair(uint32_t d, float b) {
+    const uint32_t lo = f2h(h2f(static_cast<uint16_t>(d & 0xFFFFu)) + b);
+    const uint32_t hi = f2h(h2f(static_cast<uint16_t>(d >> 16)) + b);
+    return lo | (hi << 16);
+}
+
+// The upsample scatter of a wave's staged FP16 tile (kRows pixels x kU*8 columns, same
+// staging layout as flush_rows). Column pair (co, kh) with kw = 0, 1 is one 4-byte LDS word,
+// and the two kw values of a pixel are adjacent in the output row 2h + kh. vec_out: groups
+// of 4 pixels (one image row, since W % 4 == 0) become one 16-byte store of 8 halves, and
+// each lane keeps one group across its loop, so the pixel coordinates are computed once.
+template <int kU, int kRows>
+__device__ __forceinline__ void flush_up2x2(const int8_t* stage, const GemmEpilogue& ep, int row0, int col0) {
+    constexpr int kRowBytes = kU * 16;
+    constexpr int kPairs = kU * 4;                   // (co, kh) column pairs in the wave tile
+    const int lane = threadIdx.x & (kWave - 1);
+    const int M = ep.M, N = ep.N, W = ep.up_w, HW = ep.up_hw;
+    const int Co = N >> 2;
+    const size_t plane = 4 * static_cast<size_t>(HW);
+    const size_t W2 = 2 * static_cast<size_t>(W);
+    const bool has_bias = ep.post_bias != nullptr;
+    auto word = [&](int r, int cw) {
+        return *reinterpret_cast<const uint32_t*>(stage + r * kRowBytes + (((cw >> 3) ^ (r & (kU - 1))) << 4) +
+                                                  (cw & 7) * 2);
+    };
+    if (ep.vec_out) {
+        constexpr int kQuads = kRows / 4;
+        static_assert(kWave % kQuads == 0, "quads per wave tile must divide the wave");
+        const int g = lane % kQuads;
+        const int m = row0 + 4 * g;
+        if (m >= M) return;                          // M % 4 == 0: a group is all in or all out
+        const int img = m / HW, p = m - img * HW, h = p / W, w = p - h * W;
+        uint16_t* base = ep.c16 + static_cast<size_t>(img) * Co * plane + 2 * h * W2 + 2 * w;
+        for (int j = lane / kQuads; j < kPairs; j += kWave / kQuads) {
+            const int cw = 2 * j, n = col0 + cw;
+            if (n >= N) break;
+            const int co = n >> 2, kh = (n >> 1) & 1;
+            uint32_t d[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) d[t] = word(4 * g + t, cw);
+            if (has_bias) {
+                const float b = h2f(ep.post_bias[co]);
+#pragma unroll
+                for (int t = 0; t < 4; t++) d[t] = add_bias_pair(d[t], b);
+            }
+            *reinterpret_cast<int4*>(base + co * plane + kh * W2) =
+                make_int4(static_cast<int>(d[0]), static_cast<int>(d[1]), static_cast<int>(d[2]),
+                          static_cast<int>(d[3]));
+        }
+    } else {
+        for (int r = lane; r < kRows; r += kWave) {
+            const int m = row0 + r;
+            if (m >= M) break;
+            const int img = m / HW, p = m - img * HW, h = p / W, w = p - h * W;
+            uint16_t* base = ep.c16 + static_cast<size_t>(img) * Co * plane + 2 * h * W2 + 2 * w;
+            for (int j = 0; j < kPairs; j++) {
+                const int cw = 2 * j, n = col0 + cw;
+                if (n >= N) break;
+                const int co = n >> 2, kh = (n >> 1) & 1;
+                uint32_t d = word(r, cw);
+                if (has_bias) d = add_bias_pair(d, h2f(ep.post_bias[co]));
+                uint16_t* o = base + co * plane + kh * W2;
+                o[0] = static_cast<uint16_t>(d & 0xFFFFu);
+                o[1] = static_cast<uint16_t>(d >> 16);
             }
         }
     }
@@ -591,7 +669,7 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[BN / 64][BM / 64], 
                 for (int t = 0; t < 4; t++) {
                     int n = wn + nl + t;
                     n = n < N ? n : N - 1;
-                    ws[t] = h2f(ep.w_scale[n]);
+                    ws[t] = h2f(ep.w_scale[ep.up_w ? n >> 2 : n]);
                     b[t] = has_bias ? h2f(ep.bias[n]) : 0.0f;
                 }
                 const int u = nl / kPer;                   // unit of 8 columns; half = hi
@@ -608,7 +686,8 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[BN / 64][BM / 64], 
                 }
             }
         }
-        flush_rows<kU, kEsz, true>(stage, BM / 2, ep, wm, wn);
+        if (ep.up_w) flush_up2x2<kU, BM / 2>(stage, ep, wm, wn);
+        else flush_rows<kU, kEsz, true>(stage, BM / 2, ep, wm, wn);
     } else {
         int8_t* strip = lds + wave * (32 * kRowBytes);
 #pragma unroll

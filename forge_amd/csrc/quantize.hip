@@ -127,6 +127,76 @@ __global__ __launch_bounds__(256) void quantize_rows_wave_kernel(
     }
 }
 
+// Per-pixel quantization of NCHW FP16 images (the transposed conv's input rows): pixel p of
+// image i is the row x[i, :, p] (C channels at stride HW), quantized with the row arithmetic
+// above and written as row i*HW + p of q (C contiguous int8) with its scale. A workgroup
+// takes 64 consecutive pixels of one image: each wave reads every 4th channel as 128-byte
+// coalesced runs (x is read from HBM once), the four partial absmaxes meet in LDS, and the
+// 64 rows -- one contiguous block of q -- are written G channels (4 bytes or 1) per lane.
+// STASH keeps the tile in LDS (64 x (C + 4) halves; the +4 pad spreads the column writes
+// over the banks and keeps 8-byte row reads aligned); without it the second pass re-reads x.
+constexpr int kPixTile = 64;
+constexpr int kPixStashMaxC = 512;
+
+template <int G, bool STASH>
+__global__ __launch_bounds__(256) void quantize_pixels_nchw_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scales, int C, int HW,
+    int tiles)
+{
+    extern __shared__ __align__(16) uint16_t stash[];
+    __shared__ float red[4][kPixTile];
+    __shared__ float sinv[kPixTile];
+    const int img = blockIdx.x / tiles;
+    const int p0 = (blockIdx.x - img * tiles) * kPixTile;
+    const int np = min(kPixTile, HW - p0);
+    const int t = threadIdx.x, pl = t & (kPixTile - 1), cg = t >> 6;
+    const int pitch = C + 4;
+    const uint16_t* xi = x + static_cast<size_t>(img) * C * HW + p0;
+    float amax = 0.0f;
+    if (pl < np) {
+        for (int c = cg; c < C; c += 4) {
+            const uint16_t v = xi[static_cast<size_t>(c) * HW + pl];
+            amax = fmaxf(amax, fabsf(h2f(v)));
+            if constexpr (STASH) stash[pl * pitch + c] = v;
+        }
+    }
+    red[cg][pl] = amax;
+    __syncthreads();
+    if (t < kPixTile) {
+        const float a = fmaxf(fmaxf(red[0][t], red[1][t]), fmaxf(red[2][t], red[3][t]));
+        const float scale = row_scale(a);
+        sinv[t] = 1.0f / scale;
+        if (t < np) scales[static_cast<size_t>(img) * HW + p0 + t] = scale;
+    }
+    __syncthreads();
+    int8_t* qb = q + (static_cast<size_t>(img) * HW + p0) * C;
+    const int items = np * (C / G);
+    for (int i = t; i < items; i += 256) {
+        const int e = i * G;
+        const int p = e / C, c = e - p * C;
+        const float inv = sinv[p];
+        if constexpr (G == 4) {
+            uint16_t v[4];
+            if constexpr (STASH) {
+                const uint2 w = *reinterpret_cast<const uint2*>(stash + p * pitch + c);
+                v[0] = static_cast<uint16_t>(w.x & 0xFFFFu); v[1] = static_cast<uint16_t>(w.x >> 16);
+                v[2] = static_cast<uint16_t>(w.y & 0xFFFFu); v[3] = static_cast<uint16_t>(w.y >> 16);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) v[j] = xi[static_cast<size_t>(c + j) * HW + p];
+            }
+            uint32_t packed = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                packed |= (static_cast<uint32_t>(quant1(h2f(v[j]), inv)) & 0xFFu) << (8 * j);
+            *reinterpret_cast<uint32_t*>(qb + e) = packed;
+        } else {
+            const uint16_t v = STASH ? stash[p * pitch + c] : xi[static_cast<size_t>(c) * HW + p];
+            qb[e] = static_cast<int8_t>(quant1(h2f(v), inv));
+        }
+    }
+}
+
 // Two-pass body shared by the exported kernel: any K, any alignment, any blockDim.
 __device__ void quantize_row_twopass(const uint16_t* __restrict__ in_row, int8_t* __restrict__ out_row,
                                      float* __restrict__ scale_out, int K)
@@ -245,6 +315,35 @@ int launch_quantize(const uint16_t* x, int8_t* q, float* scales, int M, int K, h
     } else {
         forge::quant::fused_quantize_activation_kernel<<<M, 256, 0, s>>>(
             reinterpret_cast<const __half*>(x), q, scales, K);
+    }
+    return launch_status();
+}
+
+int launch_quantize_pixels_nchw(const uint16_t* x, int8_t* q, float* scales, int images, int C, int HW,
+                                hipStream_t s)
+{
+    const int tiles = divup(HW, kPixTile);
+    const long long blocks = static_cast<long long>(images) * tiles;
+    if (blocks > 0x7FFFFFFFLL) return FORGE_EINVAL;
+    const bool g4 = (C % 4 == 0) && aligned(q, 4);
+    const bool stash = C <= kPixStashMaxC;
+    const size_t lds = stash ? static_cast<size_t>(kPixTile) * (C + 4) * sizeof(uint16_t) : 0;
+    const unsigned grid = static_cast<unsigned>(blocks);
+    if (stash) {
+        // At most 64 x 516 halves = 66 KB: above the default 64 KB, so raise the limit once.
+        static const hipError_t a4 = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(quantize_pixels_nchw_kernel<4, true>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, kPixTile * (kPixStashMaxC + 4) * 2);
+        static const hipError_t a1 = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(quantize_pixels_nchw_kernel<1, true>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, kPixTile * (kPixStashMaxC + 4) * 2);
+        if (a4 != hipSuccess) return static_cast<int>(a4);
+        if (a1 != hipSuccess) return static_cast<int>(a1);
+        if (g4) quantize_pixels_nchw_kernel<4, true><<<grid, 256, lds, s>>>(x, q, scales, C, HW, tiles);
+        else    quantize_pixels_nchw_kernel<1, true><<<grid, 256, lds, s>>>(x, q, scales, C, HW, tiles);
+    } else {
+        if (g4) quantize_pixels_nchw_kernel<4, false><<<grid, 256, 0, s>>>(x, q, scales, C, HW, tiles);
+        else    quantize_pixels_nchw_kernel<1, false><<<grid, 256, 0, s>>>(x, q, scales, C, HW, tiles);
     }
     return launch_status();
 }

@@ -319,3 +319,56 @@ def int8_conv2d_nhwc_dequant(x: torch.Tensor, w: torch.Tensor, act_scale: torch.
     _call("forge_int8_conv2d_nhwc_dequant", _p(x), _p(w), _p(act_scale), _p(w_scale), _p(bias), _p(out), N, H, W,
           C, Co, kH, kW, pad[0], pad[1], stride[0], stride[1], dil[0], dil[1], _stream())
     return out
+
+
+def int8_conv_transpose2d_k2s2_workspace_size(C_in: int, H: int, W: int, C_out: int) -> int:
+    return _lib.load().forge_int8_conv_transpose2d_k2s2_workspace_size(C_in, H, W, C_out)
+
+
+def int8_conv_transpose2d_k2s2_forward(input: torch.Tensor, weight: torch.Tensor, w_scale: torch.Tensor,
+                                       bias: Optional[torch.Tensor], workspace: Optional[torch.Tensor] = None,
+                                       out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """ConvTranspose2d, kernel 2, stride 2 (int8_conv_transpose2d.cuh:37-46): input (N, C_in, H, W)
+    fp16, weight (4*C_out, C_in) int8 repacked (row co*4 + kh*2 + kw = weight[ci, co, kh, kw])."""
+    N, C_in, H, W = input.shape
+    Ng = weight.shape[0]
+    if Ng % 4 != 0 or weight.dim() != 2 or weight.shape[1] != C_in:
+        raise ValueError("weight must be (4*C_out, C_in)")
+    C_out = Ng // 4
+    _need(input, torch.float16, "input")
+    _need(weight, torch.int8, "weight")
+    _need(w_scale, torch.float16, "w_scale", C_out)
+    if bias is not None:
+        _need(bias, torch.float16, "bias", C_out)
+    nbytes = int8_conv_transpose2d_k2s2_workspace_size(C_in, H, W, C_out)
+    if workspace is None:
+        workspace = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=input.device)
+    if workspace.numel() * workspace.element_size() < nbytes:
+        raise ValueError(f"workspace needs {nbytes} bytes")
+    if out is None:
+        out = torch.empty((N, C_out, 2 * H, 2 * W), dtype=torch.float16, device=input.device)
+    _need(out, torch.float16, "out", N * C_out * 4 * H * W)
+    _call("forge_int8_conv_transpose2d_k2s2_forward", _p(input), _p(weight), _p(w_scale), _p(bias), _p(out),
+          N, C_in, H, W, C_out, _p(workspace), _stream())
+    return out
+
+
+def int8_depthwise_conv2d_forward(input: torch.Tensor, weight: torch.Tensor, w_scale: torch.Tensor,
+                                  bias: Optional[torch.Tensor], kH: int, kW: int, pad=(0, 0), stride=(1, 1),
+                                  dil=(1, 1), out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Depthwise conv2d (int8_depthwise_conv2d.cuh:28-41): input (N, C, H, W) fp16, weight
+    (C, kH*kW) int8 (any shape holding C*kH*kW values), per-channel w_scale and bias."""
+    N, C, H, W = input.shape
+    _need(input, torch.float16, "input")
+    _need(weight, torch.int8, "weight", C * kH * kW)
+    _need(w_scale, torch.float16, "w_scale", C)
+    if bias is not None:
+        _need(bias, torch.float16, "bias", C)
+    Ho = conv_out_size(H, pad[0], dil[0], kH, stride[0])
+    Wo = conv_out_size(W, pad[1], dil[1], kW, stride[1])
+    if out is None:
+        out = torch.empty((N, C, max(Ho, 0), max(Wo, 0)), dtype=torch.float16, device=input.device)
+    _need(out, torch.float16, "out", N * C * max(Ho, 0) * max(Wo, 0))
+    _call("forge_int8_depthwise_conv2d_forward", _p(input), _p(weight), _p(w_scale), _p(bias), _p(out), N, C, H, W,
+          kH, kW, pad[0], pad[1], stride[0], stride[1], dil[0], dil[1], _stream())
+    return out

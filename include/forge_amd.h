@@ -201,6 +201,34 @@ int forge_int8_conv2d_nhwc_dequant(const int8_t* x, const int8_t* w, const float
                                    int kH, int kW, int padH, int padW, int strideH,
                                    int strideW, int dilH, int dilW, void* stream);
 
+/* ---- INT8 ConvTranspose2d (kernel 2, stride 2) and depthwise conv2d ------------------ */
+
+/* Replaces forge::nn::int8_conv_transpose2d_k2s2_workspace_size
+ * (include/forge/nn/int8_conv_transpose2d.cuh:25-27, src/nn/int8_conv_transpose2d.cu:107-123):
+ * the same byte count as the reference's formula; 0 for a non-positive dimension. */
+size_t forge_int8_conv_transpose2d_k2s2_workspace_size(int C_in, int H, int W, int C_out);
+
+/* Replaces forge::nn::int8_conv_transpose2d_k2s2_forward
+ * (include/forge/nn/int8_conv_transpose2d.cuh:37-46, src/nn/int8_conv_transpose2d.cu:128-191):
+ * input (N,C_in,H,W) fp16, weight (4*C_out, C_in) int8 with row co*4 + kh*2 + kw holding
+ * ConvTranspose2d weight[ci, co, kh, kw], w_scale (C_out) fp16, bias (C_out) fp16 or NULL,
+ * output (N,C_out,2H,2W) fp16; workspace of at least the size above. Per-pixel activation
+ * quantization; output = half(half(acc * as * w_scale[co]) + bias[co]). */
+int forge_int8_conv_transpose2d_k2s2_forward(const uint16_t* input, const int8_t* weight,
+                                             const uint16_t* w_scale, const uint16_t* bias,
+                                             uint16_t* output, int N, int C_in, int H, int W,
+                                             int C_out, void* workspace, void* stream);
+
+/* Replaces forge::nn::int8_depthwise_conv2d_forward
+ * (include/forge/nn/int8_depthwise_conv2d.cuh:28-41, src/nn/int8_depthwise_conv2d.cu:72-103):
+ * input (N,C,H,W) fp16, weight (C, kH*kW) int8, w_scale (C) fp16, bias (C) fp16 or NULL,
+ * output (N,C,H_out,W_out) fp16; no workspace. Float arithmetic, no activation quantization. */
+int forge_int8_depthwise_conv2d_forward(const uint16_t* input, const int8_t* weight,
+                                        const uint16_t* w_scale, const uint16_t* bias,
+                                        uint16_t* output, int N, int C, int H, int W,
+                                        int kH, int kW, int padH, int padW, int strideH,
+                                        int strideW, int dilH, int dilW, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -323,6 +323,94 @@ void orc_conv2d_nhwc_s32(const int8_t* x, const int8_t* w, int32_t* out,
 }
 
 /* ------------------------------------------------------------------------- */
+/* INT8 depthwise conv2d, NCHW FP16 in and out                               */
+/* src/nn/int8_depthwise_conv2d.cu:25-70: per output, taps in (kh, kw) order, */
+/* out-of-image taps skipped, w = (float)q * scale (one rounded product),     */
+/* sum += inp * w as nvcc contracts it by default (-fmad=true): one fmaf per  */
+/* tap from sum = +0; then sum + bias (when given) and fp16 RNE. The inputs   */
+/* are fp16 and the scales fp16, so no fp32 denormal arises and the kernel's  */
+/* fast-math flush-to-zero does not change a result.                          */
+/* ------------------------------------------------------------------------- */
+
+void orc_depthwise_conv2d(const uint16_t* in, const int8_t* w, const uint16_t* w_scale,
+                          const uint16_t* bias, uint16_t* out, int N, int C, int H, int W,
+                          int kH, int kW, int padH, int padW, int strideH, int strideW,
+                          int dilH, int dilW)
+{
+    const int Ho = orc_conv_out_size(H, padH, dilH, kH, strideH);
+    const int Wo = orc_conv_out_size(W, padW, dilW, kW, strideW);
+    if (Ho <= 0 || Wo <= 0) return;
+    for (int n = 0; n < N; n++)
+        for (int c = 0; c < C; c++) {
+            const float scale = orc_f16_to_f32(w_scale[c]);
+            const int8_t* wc = w + (size_t)c * kH * kW;
+            const uint16_t* x = in + ((size_t)n * C + c) * H * W;
+            uint16_t* y = out + ((size_t)n * C + c) * Ho * Wo;
+            for (int ho = 0; ho < Ho; ho++)
+                for (int wo = 0; wo < Wo; wo++) {
+                    float sum = 0.0f;
+                    for (int kh = 0; kh < kH; kh++) {
+                        const int hi = ho * strideH + kh * dilH - padH;
+                        if (hi < 0 || hi >= H) continue;
+                        for (int kw = 0; kw < kW; kw++) {
+                            const int wi = wo * strideW + kw * dilW - padW;
+                            if (wi < 0 || wi >= W) continue;
+                            const float wf = (float)wc[kh * kW + kw] * scale;
+                            sum = fmaf(orc_f16_to_f32(x[(size_t)hi * W + wi]), wf, sum);
+                        }
+                    }
+                    if (bias) sum = sum + orc_f16_to_f32(bias[c]);
+                    y[(size_t)ho * Wo + wo] = orc_f32_to_f16(sum);
+                }
+        }
+}
+
+/* ------------------------------------------------------------------------- */
+/* INT8 ConvTranspose2d, kernel 2, stride 2, NCHW FP16 in and out             */
+/* src/nn/int8_conv_transpose2d.cu:128-191. Per image: pixel p's channel      */
+/* vector x[:, p] is quantized as one row (quantize.cu arithmetic, above);    */
+/* GEMM row p against weight rows n = co*4 + kh*2 + kw (repacked (4*C_out,    */
+/* C_in)); the GEMM epilogue runs without bias with w_scale replicated per    */
+/* co (:50-60, :174-181): g = half((float)acc * (as * ws[co])); the scatter   */
+/* (:70-102) writes out[co, 2h+kh, 2w+kw] = half((float)g + bias[co]), or g   */
+/* unchanged without bias. acc32 (optional) receives the INT32 GEMM stage in  */
+/* the output's NCHW layout.                                                  */
+/* ------------------------------------------------------------------------- */
+
+void orc_conv_transpose2d_k2s2(const uint16_t* in, const int8_t* w, const uint16_t* w_scale,
+                               const uint16_t* bias, uint16_t* out, int32_t* acc32,
+                               int N, int C_in, int H, int W, int C_out)
+{
+    const size_t HW = (size_t)H * W;
+    const int Ng = 4 * C_out;
+    uint16_t* col = (uint16_t*)malloc((size_t)C_in * sizeof(uint16_t));
+    int8_t* q = (int8_t*)malloc((size_t)C_in);
+    for (int n = 0; n < N; n++) {
+        const uint16_t* x = in + (size_t)n * C_in * HW;
+        for (size_t p = 0; p < HW; p++) {
+            const int h = (int)(p / W), wi = (int)(p % W);
+            for (int ci = 0; ci < C_in; ci++) col[ci] = x[(size_t)ci * HW + p];
+            float as;
+            orc_quantize_rows(col, q, &as, 1, C_in);
+            for (int j = 0; j < Ng; j++) {
+                const int8_t* wr = w + (size_t)j * C_in;
+                int32_t acc = 0;
+                for (int ci = 0; ci < C_in; ci++) acc += (int32_t)q[ci] * (int32_t)wr[ci];
+                const int co = j >> 2, kh = (j >> 1) & 1, kw = j & 1;
+                const float s = as * orc_f16_to_f32(w_scale[co]);
+                uint16_t g = orc_f32_to_f16((float)acc * s);
+                if (bias) g = orc_f32_to_f16(orc_f16_to_f32(g) + orc_f16_to_f32(bias[co]));
+                const size_t o = (((size_t)n * C_out + co) * 2 * H + 2 * h + kh) * (size_t)(2 * W) + 2 * wi + kw;
+                if (out) out[o] = g;
+                if (acc32) acc32[o] = acc;
+            }
+        }
+    }
+    free(col);
+    free(q);
+}
+
+/* ------------------------------------------------------------------------- */
 /* MT19937 (Matsumoto & Nishimura 1998), as std::mt19937 specifies it.        */
 /* Used to regenerate the reference test's pack_metadata input vectors        */
 /* (tests/test_pack_metadata.cu:124-126: std::mt19937 rng(42); rng() & 0xF).  */

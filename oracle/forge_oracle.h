@@ -24,6 +24,14 @@
  *   orc_sparse_gemm_s32               dense GEMM of the decompressed weights == dense GEMM of the
  *                                     pruned weights (numpy)
  *   orc_conv2d_nhwc_s32               torch.nn.functional.conv2d in float64 (exact for these ints)
+ *   orc_depthwise_conv2d              torch conv2d (groups = C) in float64 on the dequantized weights
+ *                                     (<= 1 fp16 ulp + fp32 sum error); 1x1 kernels as one rounded
+ *                                     product; the reference test's three shapes at its tolerance
+ *   orc_conv_transpose2d_k2s2         INT32 stage == torch conv_transpose2d in float64 on the
+ *                                     quantized integers (exact), with the (C_in, C_out, 2, 2)
+ *                                     weight rebuilt from the repacked rows; FP16 output vs the
+ *                                     float64 dequantized conv_transpose2d (<= 2 fp16 ulps);
+ *                                     the quantize stage is orc_quantize_rows (pinned above)
  *   orc_mt19937                       the C++ standard's 10000th-output check (4123659995)
  */
 #ifndef FORGE_ORACLE_H
@@ -63,6 +71,14 @@ int  orc_conv_out_size(int in, int pad, int dil, int k, int stride);
 void orc_conv2d_nhwc_s32(const int8_t* x, const int8_t* w, int32_t* out,
                          int N, int H, int W, int C, int Co, int kH, int kW,
                          int padH, int padW, int strideH, int strideW, int dilH, int dilW);
+
+void orc_depthwise_conv2d(const uint16_t* in, const int8_t* w, const uint16_t* w_scale,
+                          const uint16_t* bias, uint16_t* out, int N, int C, int H, int W,
+                          int kH, int kW, int padH, int padW, int strideH, int strideW,
+                          int dilH, int dilW);
+void orc_conv_transpose2d_k2s2(const uint16_t* in, const int8_t* w, const uint16_t* w_scale,
+                               const uint16_t* bias, uint16_t* out, int32_t* acc32,
+                               int N, int C_in, int H, int W, int C_out);
 
 typedef struct { uint32_t mt[624]; int idx; } orc_mt19937_t;
 void     orc_mt19937_seed(orc_mt19937_t* s, uint32_t seed);

@@ -56,6 +56,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_conv_out_size.argtypes = [_I, _I, _I, _I, _I]
     L.orc_conv_out_size.restype = _I
     L.orc_conv2d_nhwc_s32.argtypes = [_P, _P, _P] + [_I] * 13
+    L.orc_depthwise_conv2d.argtypes = [_P] * 5 + [_I] * 12
+    L.orc_conv_transpose2d_k2s2.argtypes = [_P] * 6 + [_I] * 5
     L.orc_mt19937_seed.argtypes = [_P, ctypes.c_uint32]
     L.orc_mt19937_next.argtypes = [_P]
     L.orc_mt19937_next.restype = ctypes.c_uint32
@@ -195,6 +197,39 @@ def conv2d_nhwc_s32(x, w, pad=(0, 0), stride=(1, 1), dil=(1, 1)):
     lib().orc_conv2d_nhwc_s32(_p(x), _p(w), _p(out), N, H, W, C, Co, kH, kW,
                               pad[0], pad[1], stride[0], stride[1], dil[0], dil[1])
     return out
+
+
+def depthwise_conv2d(x16, w, w_scale16, bias16=None, pad=(0, 0), stride=(1, 1), dil=(1, 1)):
+    """x16 (N, C, H, W) fp16, w (C, kH, kW) int8 -> (N, C, Ho, Wo) fp16."""
+    x = _u16(x16)
+    w = np.ascontiguousarray(w, np.int8)
+    N, C, H, W = x.shape
+    C2, kH, kW = w.shape
+    assert C2 == C
+    Ho = conv_out_size(H, pad[0], dil[0], kH, stride[0])
+    Wo = conv_out_size(W, pad[1], dil[1], kW, stride[1])
+    out = np.zeros((N, C, max(Ho, 0), max(Wo, 0)), np.uint16)
+    ws = _u16(w_scale16)
+    b = None if bias16 is None else _u16(bias16)
+    lib().orc_depthwise_conv2d(_p(x), _p(w), _p(ws), _p(b), _p(out), N, C, H, W, kH, kW,
+                               pad[0], pad[1], stride[0], stride[1], dil[0], dil[1])
+    return out.view(np.float16)
+
+
+def conv_transpose2d_k2s2(x16, w_rep, w_scale16, bias16=None, with_acc=False):
+    """x16 (N, C_in, H, W) fp16, w_rep (4*C_out, C_in) int8 (row co*4 + kh*2 + kw) ->
+    (N, C_out, 2H, 2W) fp16, and the INT32 GEMM stage in the same layout if with_acc."""
+    x = _u16(x16)
+    w = np.ascontiguousarray(w_rep, np.int8)
+    N, C_in, H, W = x.shape
+    C_out = w.shape[0] // 4
+    assert w.shape == (4 * C_out, C_in)
+    out = np.empty((N, C_out, 2 * H, 2 * W), np.uint16)
+    acc = np.empty((N, C_out, 2 * H, 2 * W), np.int32) if with_acc else None
+    ws = _u16(w_scale16)
+    b = None if bias16 is None else _u16(bias16)
+    lib().orc_conv_transpose2d_k2s2(_p(x), _p(w), _p(ws), _p(b), _p(out), _p(acc), N, C_in, H, W, C_out)
+    return (out.view(np.float16), acc) if with_acc else out.view(np.float16)
 
 
 def mt19937(seed: int, count: int) -> np.ndarray:

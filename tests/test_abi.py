@@ -30,7 +30,9 @@ def test_header_declares_the_path():
     for s in ["forge_quantize_activation", "forge_dequantize_bias", "forge_int8_gemm_dequant",
               "forge_int8_linear", "forge_int8_gemm", "forge_sparse_int8_gemm", "forge_sparse_int8_linear",
               "forge_sparse_int8_gemm_plan", "forge_prune_compress_24", "forge_pack_metadata",
-              "forge_splitk_reduce", "forge_int8_conv2d_forward", "forge_int8_conv2d_workspace_size"]:
+              "forge_splitk_reduce", "forge_int8_conv2d_forward", "forge_int8_conv2d_workspace_size",
+              "forge_int8_conv_transpose2d_k2s2_forward", "forge_int8_conv_transpose2d_k2s2_workspace_size",
+              "forge_int8_depthwise_conv2d_forward"]:
         assert s in syms
 
 
@@ -54,7 +56,9 @@ def test_cpp_api_symbols_exported():
                 "forge::gemm::splitk_reduce(", "forge::sparsity::prune_compress_24(",
                 "forge::sparsity::pack_metadata(", "forge::sparsity::prune_compress_kernel(",
                 "forge::sparsity::pack_metadata_kernel(", "forge::nn::int8_conv2d_forward(",
-                "forge::nn::int8_conv2d_workspace_size(", "forge::last_error("]:
+                "forge::nn::int8_conv2d_workspace_size(", "forge::nn::int8_conv_transpose2d_k2s2_forward(",
+                "forge::nn::int8_conv_transpose2d_k2s2_workspace_size(", "forge::nn::int8_depthwise_conv2d_forward(",
+                "forge::last_error("]:
         assert sym in out, sym
 
 
@@ -98,6 +102,30 @@ def test_conv_workspace_size(lib):
     up = lambda b: (b + 255) // 256 * 256
     assert n == up(M * K * 2) + up(M * K) + up(M * 4) + up(M * 16 * 2)
     assert n >= M * K * 2 + M * K + M * 4 + M * 16 * 2     # at least the reference's size
+
+
+def test_conv_transpose_workspace_size(lib):
+    # int8_conv_transpose2d.cu:107-123: col fp16 + col int8 + act_scale + w_scale_rep + gemm_out
+    M, K, Ng = 16 * 16, 32, 4 * 64
+    assert lib.forge_int8_conv_transpose2d_k2s2_workspace_size(32, 16, 16, 64) == \
+        M * K * 2 + M * K + M * 4 + Ng * 2 + M * Ng * 2
+    assert lib.forge_int8_conv_transpose2d_k2s2_workspace_size(0, 16, 16, 64) == 0
+
+
+def test_special_conv_argument_checks(lib):
+    fake = ctypes.c_void_p(4096)   # never dereferenced: validation fails first
+    # N, C_in or C_out <= 0 returns early, as the reference does (int8_conv_transpose2d.cu:139)
+    assert lib.forge_int8_conv_transpose2d_k2s2_forward(None, None, None, None, None, 0, 8, 4, 4, 8, None, None) == 0
+    assert lib.forge_int8_conv_transpose2d_k2s2_forward(fake, fake, fake, None, fake, 1, 8, 4, 4, 8, None, None) == -1
+    assert lib.forge_int8_depthwise_conv2d_forward(None, None, None, None, None, 1, 0, 4, 4, 3, 3, 1, 1, 1, 1, 1, 1,
+                                                   None) == 0
+    assert lib.forge_int8_depthwise_conv2d_forward(fake, fake, None, None, fake, 1, 4, 4, 4, 3, 3, 1, 1, 1, 1, 1, 1,
+                                                   None) == -1
+    assert lib.forge_int8_depthwise_conv2d_forward(fake, fake, fake, None, fake, 1, 4, 4, 4, 3, 3, 1, 1, 0, 1, 1, 1,
+                                                   None) == -1
+    # an empty output (kernel larger than the padded input) launches nothing
+    assert lib.forge_int8_depthwise_conv2d_forward(fake, fake, fake, None, fake, 1, 4, 2, 2, 5, 5, 0, 0, 1, 1, 1, 1,
+                                                   None) == 0
 
 
 def test_ops_module_imports_like_the_gpu_tests():

@@ -103,3 +103,28 @@ def test_graph_conv(dev):
         out = torch.empty((N, H, W, Co), dtype=torch.int32, device=dev)
         calls = [lambda: ops.int8_conv2d_nhwc_s32(x, w, (1, 1), out=out)]
         _replay_check(dev, calls, [out])
+
+
+def test_graph_conv_special(dev):
+    """Depthwise conv (tile and direct kernels) and the k2s2 transposed conv (pixel quantizer
+    + scatter GEMM, two images per chunk)."""
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(24)
+    x = to_dev(rng.uniform(-1, 1, (2, 8, 33, 40)).astype(np.float16), dev)
+    w = to_dev(int8_uniform(rng, (8, 9)), dev)
+    ws = to_dev(rng.uniform(0.005, 0.05, 8).astype(np.float16), dev)
+    b = to_dev(rng.uniform(-0.5, 0.5, 8).astype(np.float16), dev)
+    y1 = torch.empty((2, 8, 33, 40), dtype=torch.float16, device=dev)
+    y2 = torch.empty((2, 8, 17, 20), dtype=torch.float16, device=dev)
+    wt = to_dev(int8_uniform(rng, (4 * 12, 8)), dev)
+    wts = to_dev(rng.uniform(0.005, 0.05, 12).astype(np.float16), dev)
+    bt = to_dev(rng.uniform(-0.5, 0.5, 12).astype(np.float16), dev)
+    nbytes = ops.int8_conv_transpose2d_k2s2_workspace_size(8, 33, 40, 12)
+    wsp = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+    y3 = torch.empty((2, 12, 66, 80), dtype=torch.float16, device=dev)
+    say("graph depthwise + conv_transpose")
+    calls = [lambda: ops.int8_depthwise_conv2d_forward(x, w, ws, b, 3, 3, (1, 1), out=y1),
+             lambda: ops.int8_depthwise_conv2d_forward(x, w, ws, b, 3, 3, (1, 1), (2, 2), out=y2),
+             lambda: ops.int8_conv_transpose2d_k2s2_forward(x, wt, wts, bt, workspace=wsp, out=y3)]
+    _replay_check(dev, calls, [y1, y2, y3])

@@ -266,3 +266,166 @@ def test_conv_matches_torch_asymmetric(orc):
                                      torch.from_numpy(w).permute(0, 3, 1, 2).double(),
                                      stride=(2, 1), padding=(1, 0), dilation=(1, 2))
     assert np.array_equal(out, ref.permute(0, 2, 3, 1).numpy().astype(np.int32))
+
+
+# ---- depthwise conv2d (src/nn/int8_depthwise_conv2d.cu) -------------------------------
+
+def _ulp16(v):
+    """Spacing of fp16 values at |v| (subnormal spacing below the normal range)."""
+    a = np.abs(np.asarray(v, np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+def _dw_case(rng, N, C, H, W, k, bias=True):
+    x = rng.uniform(-1, 1, (N, C, H, W)).astype(np.float16)
+    w = rng.integers(-127, 128, (C,) + k).astype(np.int8)
+    ws = rng.uniform(0.005, 0.05, C).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, C).astype(np.float16) if bias else None
+    return x, w, ws, b
+
+
+def _dw_torch64(x, w, ws, b, pad, stride, dil):
+    """float64 depthwise conv (groups = C) with the weights dequantized as the reference does
+    ((float)q * scale, one fp32 product), plus the bias, and sum |terms| for the error bound."""
+    import torch
+    wf = (w.astype(np.float32) * ws.astype(np.float32)[:, None, None]).astype(np.float64)
+    C = w.shape[0]
+    xt = torch.from_numpy(x.astype(np.float64))
+    y = torch.nn.functional.conv2d(xt, torch.from_numpy(wf)[:, None], stride=stride, padding=pad,
+                                   dilation=dil, groups=C)
+    s = torch.nn.functional.conv2d(xt.abs(), torch.from_numpy(np.abs(wf))[:, None], stride=stride,
+                                   padding=pad, dilation=dil, groups=C)
+    if b is not None:
+        bb = torch.from_numpy(b.astype(np.float64))[None, :, None, None]
+        y = y + bb
+        s = s + bb.abs()
+    return y.numpy(), s.numpy()
+
+
+@pytest.mark.parametrize("N,C,H,W,k,pad,stride,dil", [
+    (1, 16, 16, 16, (3, 3), (1, 1), (1, 1), (1, 1)),
+    (2, 5, 9, 13, (3, 2), (2, 0), (2, 1), (1, 2)),
+    (1, 3, 20, 7, (5, 5), (2, 3), (1, 2), (2, 1)),
+    (3, 4, 6, 6, (1, 1), (0, 0), (1, 1), (1, 1)),
+    (1, 2, 11, 17, (7, 1), (3, 0), (3, 1), (1, 1)),
+])
+def test_depthwise_matches_torch_float64(orc, N, C, H, W, k, pad, stride, dil):
+    rng = np.random.default_rng(N * 100 + C)
+    x, w, ws, b = _dw_case(rng, N, C, H, W, k, bias=(C % 2 == 0))
+    y = orc.depthwise_conv2d(x, w, ws, b, pad, stride, dil).astype(np.float64)
+    ref, s = _dw_torch64(x, w, ws, b, pad, stride, dil)
+    assert y.shape == ref.shape
+    taps = k[0] * k[1] + 1
+    bound = _ulp16(ref) / 2 + 2.0 ** -23 * taps * s + 2.0 ** -25
+    assert np.all(np.abs(y - ref) <= bound)
+
+
+@pytest.mark.parametrize("C,H,W,bias", [(16, 16, 16, True), (32, 32, 32, True), (64, 8, 8, False)])
+def test_depthwise_reference_test_shapes(orc, C, H, W, bias):
+    """The reference test's depthwise cases and criterion (test_int8_special_conv.cu:71-141,
+    269-271: max |gpu - float ref| < 0.01), against the float64 reference."""
+    rng = np.random.default_rng(C)
+    x, w, ws, b = _dw_case(rng, 1, C, H, W, (3, 3), bias)
+    y = orc.depthwise_conv2d(x, w, ws, b, (1, 1)).astype(np.float64)
+    ref, _ = _dw_torch64(x, w, ws, b, (1, 1), (1, 1), (1, 1))
+    assert np.abs(y - ref).max() < 0.01
+
+
+def test_depthwise_closed_forms(orc):
+    # A 1x1 kernel is one rounded fp32 product, then the fp32 bias add and fp16 rounding.
+    rng = np.random.default_rng(5)
+    x, w, ws, b = _dw_case(rng, 2, 6, 5, 7, (1, 1))
+    y = orc.depthwise_conv2d(x, w, ws, b)
+    wf = w[:, 0, 0].astype(np.float32) * ws.astype(np.float32)
+    want = (x.astype(np.float32) * wf[None, :, None, None] + b.astype(np.float32)[None, :, None, None])
+    assert np.array_equal(y.view(np.uint16), want.astype(np.float16).view(np.uint16))
+    # Taps outside the image are skipped: with pad = k - 1 the corner output of a 2x2
+    # kernel sees only the image's corner pixel, times the kernel's opposite corner tap.
+    xs = np.ones((1, 1, 4, 4), np.float16)
+    wk = np.array([[[1, 2], [3, 4]]], np.int8)
+    y = orc.depthwise_conv2d(xs, wk, np.array([1.0], np.float16), None, (1, 1)).astype(np.float32)
+    assert y[0, 0, 0, 0] == 4 and y[0, 0, 0, 1] == 7 and y[0, 0, 1, 1] == 10 and y[0, 0, 4, 4] == 1
+
+
+def test_depthwise_accumulates_with_fma(orc):
+    """Each tap is one fused multiply-add into the running sum (nvcc contracts
+    `sum += inp * w` by default): with taps x*w and (-x)*w the exact sum is 0, an unfused
+    sum gives 0, and the fused one leaves the rounding error of fl(x*w), which is not 0."""
+    x = np.array([[[[1001.0, -1001.0]]]], np.float16)
+    wk = np.array([[[127, 127]]], np.int8)
+    ws = np.array([7.99], np.float16)
+    y = orc.depthwise_conv2d(x, wk, ws, None).astype(np.float64)
+    wf = np.float32(127) * np.float32(ws[0])
+    exact = np.float64(x[0, 0, 0, 0]) * np.float64(wf)
+    resid = np.float64(np.float32(exact)) - exact       # fl(x*w) - x*w, in exact arithmetic
+    assert resid != 0
+    assert y[0, 0, 0, 0] == np.float64(np.float16(resid))
+
+
+# ---- ConvTranspose2d k=2 s=2 (src/nn/int8_conv_transpose2d.cu) ----------------------
+
+def _ct_case(rng, N, C_in, H, W, C_out, bias=True):
+    x = rng.uniform(-1, 1, (N, C_in, H, W)).astype(np.float16)
+    w = rng.integers(-127, 128, (4 * C_out, C_in)).astype(np.int8)
+    ws = rng.uniform(0.005, 0.05, C_out).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, C_out).astype(np.float16) if bias else None
+    return x, w, ws, b
+
+
+def _ct_weight4(w_rep, C_in, C_out):
+    """Repacked rows (co*4 + kh*2 + kw, ci) back to the (C_in, C_out, 2, 2) ConvTranspose2d
+    weight (int8_conv_transpose2d.cuh:13-16)."""
+    return w_rep.reshape(C_out, 2, 2, C_in).transpose(3, 0, 1, 2)
+
+
+@pytest.mark.parametrize("N,C_in,H,W,C_out", [(1, 32, 6, 5, 8), (2, 7, 3, 4, 3), (1, 64, 4, 4, 16)])
+def test_conv_transpose_int32_stage_matches_torch(orc, N, C_in, H, W, C_out):
+    import torch
+    rng = np.random.default_rng(C_in + H)
+    x, w, ws, b = _ct_case(rng, N, C_in, H, W, C_out)
+    y, acc = orc.conv_transpose2d_k2s2(x, w, ws, b, with_acc=True)
+    # Per-pixel quantization through the (separately pinned) row quantizer.
+    rows = x.transpose(0, 2, 3, 1).reshape(-1, C_in)
+    q, s = orc.quantize_rows(rows)
+    qn = q.reshape(N, H, W, C_in).transpose(0, 3, 1, 2).astype(np.float64)
+    w4 = _ct_weight4(w, C_in, C_out).astype(np.float64)
+    ref = torch.nn.functional.conv_transpose2d(torch.from_numpy(qn), torch.from_numpy(w4), stride=2).numpy()
+    assert np.array_equal(acc, ref.astype(np.int32))
+    # FP16 output: float64 of the dequantized operands, within the two fp16 roundings.
+    sn = s.reshape(N, 1, H, W).astype(np.float64)
+    ref16 = torch.nn.functional.conv_transpose2d(torch.from_numpy(qn * sn),
+                                                 torch.from_numpy(w4 * ws.astype(np.float64)[None, :, None, None]),
+                                                 bias=torch.from_numpy(b.astype(np.float64)), stride=2).numpy()
+    # Two fp16 roundings: of the GEMM value g = y - bias, then of g + bias.
+    g = ref16 - b.astype(np.float64)[None, :, None, None]
+    bound = _ulp16(g) / 2 + _ulp16(ref16) / 2 + 2.0 ** -21 * np.abs(g) + 2.0 ** -25
+    assert np.all(np.abs(y.astype(np.float64) - ref16) <= bound)
+
+
+@pytest.mark.parametrize("C_in,H,W,C_out,bias", [(32, 16, 16, 64, True), (64, 8, 8, 32, True),
+                                                 (16, 32, 32, 16, False)])
+def test_conv_transpose_reference_test_shapes(orc, C_in, H, W, C_out, bias):
+    """The reference test's cases and criterion (test_int8_special_conv.cu:146-257, 275-279:
+    max |gpu - float ref| < 0.5 and mean < 0.1 against the unquantized float conv)."""
+    import torch
+    rng = np.random.default_rng(C_in * 7 + C_out)
+    x, w, ws, b = _ct_case(rng, 1, C_in, H, W, C_out, bias)
+    y = orc.conv_transpose2d_k2s2(x, w, ws, b).astype(np.float64)
+    w4 = _ct_weight4(w, C_in, C_out).astype(np.float64) * ws.astype(np.float64)[None, :, None, None]
+    ref = torch.nn.functional.conv_transpose2d(torch.from_numpy(x.astype(np.float64)), torch.from_numpy(w4),
+                                               bias=None if b is None else torch.from_numpy(b.astype(np.float64)),
+                                               stride=2).numpy()
+    d = np.abs(y - ref)
+    assert d.max() < 0.5 and d.mean() < 0.1
+
+
+def test_conv_transpose_bias_after_rounding(orc):
+    """The bias is added to the already-rounded FP16 GEMM value (the scatter step,
+    int8_conv_transpose2d.cu:99-101): output == half(half(acc * as * ws) + bias)."""
+    rng = np.random.default_rng(9)
+    x, w, ws, b = _ct_case(rng, 1, 16, 3, 3, 4)
+    y0 = orc.conv_transpose2d_k2s2(x, w, ws, None)
+    y1 = orc.conv_transpose2d_k2s2(x, w, ws, b)
+    want = (y0.astype(np.float32) + b.astype(np.float32)[None, :, None, None]).astype(np.float16)
+    assert np.array_equal(y1.view(np.uint16), want.view(np.uint16))
