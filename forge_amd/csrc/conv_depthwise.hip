@@ -87,18 +87,44 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(
         wf[t] = v;
         finite = __builtin_isfinite(v);
     }
-    // Input tile with zero padding outside the image: 64 consecutive columns per wave pass.
+    // Input tile with zero padding outside the image. Every load is issued before the first
+    // LDS write (fixed trip counts, guarded), so a wave has all of its rows in flight at once:
+    // the main 64 columns as one 128-byte row per wave instruction, and the at most 8 halo
+    // columns of 8 rows per instruction.
     const uint16_t* xp = x + static_cast<size_t>(plane) * H * W;
     const int rows = kDwTileH + kH - 1, cols = kDwTileW + kW - 1;
-    for (int r = t >> 6; r < rows; r += 4) {
-        const int hi = hi0 + r;
-        const bool rin = static_cast<unsigned>(hi) < static_cast<unsigned>(H);
-        for (int cl = t & 63; cl < cols; cl += 64) {
-            const int wi = wi0 + cl;
-            uint16_t v = 0;
-            if (rin && static_cast<unsigned>(wi) < static_cast<unsigned>(W)) v = xp[static_cast<size_t>(hi) * W + wi];
-            tile[r * kDwPitch + cl] = v;
-        }
+    constexpr int kMainIters = (kDwTileH + kDwMaxKH - 1 + 3) / 4;
+    constexpr int kHaloIters = ((kDwTileH + kDwMaxKH - 1) * 8 + 255) / 256;
+    const int lane = t & 63, wv = t >> 6;
+    uint16_t mv[kMainIters], hv[kHaloIters];
+#pragma unroll
+    for (int k = 0; k < kMainIters; k++) {
+        const int r = wv + 4 * k, hi = hi0 + r, wi = wi0 + lane;
+        uint16_t v = 0;
+        if (r < rows && static_cast<unsigned>(hi) < static_cast<unsigned>(H) &&
+            static_cast<unsigned>(wi) < static_cast<unsigned>(W))
+            v = xp[static_cast<size_t>(hi) * W + wi];
+        mv[k] = v;
+    }
+#pragma unroll
+    for (int k = 0; k < kHaloIters; k++) {
+        const int e = t + 256 * k, r = e >> 3, cl = kDwTileW + (e & 7);
+        const int hi = hi0 + r, wi = wi0 + cl;
+        uint16_t v = 0;
+        if (r < rows && cl < cols && static_cast<unsigned>(hi) < static_cast<unsigned>(H) &&
+            static_cast<unsigned>(wi) < static_cast<unsigned>(W))
+            v = xp[static_cast<size_t>(hi) * W + wi];
+        hv[k] = v;
+    }
+#pragma unroll
+    for (int k = 0; k < kMainIters; k++) {
+        const int r = wv + 4 * k;
+        if (r < rows) tile[r * kDwPitch + lane] = mv[k];
+    }
+#pragma unroll
+    for (int k = 0; k < kHaloIters; k++) {
+        const int e = t + 256 * k, r = e >> 3, cl = kDwTileW + (e & 7);
+        if (r < rows && cl < cols) tile[r * kDwPitch + cl] = hv[k];
     }
     const bool all_finite = __syncthreads_and(finite);
 

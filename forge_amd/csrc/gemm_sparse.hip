@@ -598,15 +598,31 @@ __device__ __forceinline__ void sp_store_tile(const v4i (&acc)[8][BMT / 32], con
             const int m = wm + 16 * j + r16;
             as[j] = ep.act_scale[m < M ? m : M - 1];
         }
+        // The wave's 128 w_scale / bias halves go through a wave-private LDS strip (two loads
+        // per lane, in flight together) instead of one memory latency per column group; the
+        // bias strip holds w_scale when there is no bias (ignored by dequant_gemm).
+        uint16_t* wsl = reinterpret_cast<uint16_t*>(lds + 4 * (BMT / 2) * kRowBytes) + wave * 256;
+        uint16_t* bl = wsl + 128;
+        {
+            const uint16_t* bsrc = has_bias ? ep.bias : ep.w_scale;
+            const int n0c = min(wn + lane, N - 1), n1c = min(wn + 64 + lane, N - 1);
+            const uint16_t w0 = ep.w_scale[n0c], w1 = ep.w_scale[n1c], b0 = bsrc[n0c], b1 = bsrc[n1c];
+            wsl[lane] = w0;
+            wsl[64 + lane] = w1;
+            bl[lane] = b0;
+            bl[64 + lane] = b1;
+        }
 #pragma unroll
         for (int i = 0; i < kTN; i++) {
+            const uint2 w2 = *reinterpret_cast<const uint2*>(wsl + 16 * i + 4 * q);
+            const uint2 b2 = *reinterpret_cast<const uint2*>(bl + 16 * i + 4 * q);
+            const uint32_t wr[4] = {w2.x & 0xFFFFu, w2.x >> 16, w2.y & 0xFFFFu, w2.y >> 16};
+            const uint32_t br[4] = {b2.x & 0xFFFFu, b2.x >> 16, b2.y & 0xFFFFu, b2.y >> 16};
             float ws[4], b[4];
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                int n = wn + 16 * i + 4 * q + t;
-                n = n < N ? n : N - 1;
-                ws[t] = h2f(ep.w_scale[n]);
-                b[t] = has_bias ? h2f(ep.bias[n]) : 0.0f;
+                ws[t] = h2f(static_cast<uint16_t>(wr[t]));
+                b[t] = h2f(static_cast<uint16_t>(br[t]));
             }
             const int u = 2 * i + (q >> 1), half = q & 1;
 #pragma unroll
@@ -638,7 +654,7 @@ __device__ __forceinline__ void sp_store_tile(const v4i (&acc)[8][BMT / 32], con
 
 template <int BMT, bool DEQUANT>
 constexpr int sp_dma_lds_bytes() {
-    constexpr int epi = DEQUANT ? 4 * (BMT / 2) * 256 : 4 * 16 * 512;
+    constexpr int epi = DEQUANT ? 4 * (BMT / 2) * 256 + 4 * 512 : 4 * 16 * 512;
     return SpDmaTile<BMT>::kLdsBytes > epi ? SpDmaTile<BMT>::kLdsBytes : epi;
 }
 

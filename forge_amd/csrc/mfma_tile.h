@@ -626,7 +626,8 @@ __device__ __forceinline__ void flush_up2x2(const int8_t* stage, const GemmEpilo
 // LDS bytes the epilogue needs: FP16 stages the whole wave tile, INT32 one 32-row strip.
 template <int BM, int BN, bool DEQUANT>
 constexpr int epilogue_lds_bytes() {
-    return DEQUANT ? BM * BN * 2 : 4 * 32 * (BN / 2) * 4;
+    // FP16: 4 wave tiles, then each wave's w_scale and bias strips (BN/2 halves each).
+    return DEQUANT ? BM * BN * 2 + 4 * BN * 2 : 4 * 32 * (BN / 2) * 4;
 }
 
 // Writes the wave's (BM/2) x (BN/2) tile through a wave-private LDS staging area: each lane
@@ -659,18 +660,48 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[BN / 64][BM / 64], 
             as[i] = ep.act_scale[m < M ? m : M - 1];
         }
         const bool has_bias = ep.bias != nullptr;
+        // The w_scale / bias halves of the wave's BN/2 columns are staged in a wave-private LDS
+        // strip first (one or two coalesced loads per lane, all in flight together), then read
+        // 4 columns at a time. Loading them per column group inside the loop below cost one
+        // memory latency per group (the FP16 epilogue of a K = 64 GEMM ran at a third of the
+        // INT32 one's rate); prefetching them into registers spilled the 256 x 256 tile.
+        // Without a bias the bias strip holds w_scale (in range, and ignored by dequant_gemm),
+        // so no load sits behind a branch; the upsample scatter has one scale per 4 columns.
+        uint16_t* wsl = reinterpret_cast<uint16_t*>(lds + BM * BN * 2) + wave * BN;
+        uint16_t* bl = wsl + BN / 2;
+        const uint16_t* bsrc = has_bias ? ep.bias : ep.w_scale;
+        {
+            constexpr int kIt = (BN / 2 + kWave - 1) / kWave;
+            uint16_t wv[kIt], bw[kIt];
+#pragma unroll
+            for (int k = 0; k < kIt; k++) {
+                const int n = min(wn + lane + kWave * k, N - 1);
+                wv[k] = ep.w_scale[ep.up_w ? n >> 2 : n];
+                bw[k] = bsrc[n];
+            }
+#pragma unroll
+            for (int k = 0; k < kIt; k++) {
+                const int c = lane + kWave * k;
+                if (c < BN / 2) {
+                    wsl[c] = wv[k];
+                    bl[c] = bw[k];
+                }
+            }
+        }
 #pragma unroll
         for (int j = 0; j < kTN; j++) {
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 const int nl = 32 * j + 8 * g + 4 * hi;     // first of this lane's 4 columns
+                const uint2 w2 = *reinterpret_cast<const uint2*>(wsl + nl);
+                const uint2 b2 = *reinterpret_cast<const uint2*>(bl + nl);
+                const uint32_t wr[4] = {w2.x & 0xFFFFu, w2.x >> 16, w2.y & 0xFFFFu, w2.y >> 16};
+                const uint32_t br[4] = {b2.x & 0xFFFFu, b2.x >> 16, b2.y & 0xFFFFu, b2.y >> 16};
                 float ws[4], b[4];
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
-                    int n = wn + nl + t;
-                    n = n < N ? n : N - 1;
-                    ws[t] = h2f(ep.w_scale[ep.up_w ? n >> 2 : n]);
-                    b[t] = has_bias ? h2f(ep.bias[n]) : 0.0f;
+                    ws[t] = h2f(static_cast<uint16_t>(wr[t]));
+                    b[t] = h2f(static_cast<uint16_t>(br[t]));
                 }
                 const int u = nl / kPer;                   // unit of 8 columns; half = hi
 #pragma unroll

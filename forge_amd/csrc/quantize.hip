@@ -154,10 +154,23 @@ __global__ __launch_bounds__(256) void quantize_pixels_nchw_kernel(
     const uint16_t* xi = x + static_cast<size_t>(img) * C * HW + p0;
     float amax = 0.0f;
     if (pl < np) {
-        for (int c = cg; c < C; c += 4) {
-            const uint16_t v = xi[static_cast<size_t>(c) * HW + pl];
-            amax = fmaxf(amax, fabsf(h2f(v)));
-            if constexpr (STASH) stash[pl * pitch + c] = v;
+        // kBatch channel loads in flight per lane before the first use.
+        constexpr int kBatch = 16;
+        for (int c0 = cg; c0 < C; c0 += 4 * kBatch) {
+            uint16_t v[kBatch];
+#pragma unroll
+            for (int j = 0; j < kBatch; j++) {
+                const int c = c0 + 4 * j;
+                v[j] = c < C ? xi[static_cast<size_t>(c) * HW + pl] : static_cast<uint16_t>(0);
+            }
+#pragma unroll
+            for (int j = 0; j < kBatch; j++) {
+                const int c = c0 + 4 * j;
+                if (c < C) {
+                    amax = fmaxf(amax, fabsf(h2f(v[j])));
+                    if constexpr (STASH) stash[pl * pitch + c] = v[j];
+                }
+            }
         }
     }
     red[cg][pl] = amax;
