@@ -63,6 +63,16 @@ __device__ __forceinline__ uint16_t dequant_gemm(int acc, float as, float ws, fl
     return f2h(has_bias ? __builtin_fmaf(a, s, b) : a * s);
 }
 
+// Workgroup id -> logical tile id such that each of the 8 XCDs (which receive workgroups
+// round-robin by id) runs one contiguous range of tiles: neighbouring tiles, which share
+// halo lines, then meet in the same L2. A bijection on [0, total) for any total.
+__device__ __forceinline__ int xcd_contiguous(int bid, int total) {
+    constexpr int kXcd = 8;
+    const int q = total / kXcd, r = total % kXcd;
+    const int x = bid % kXcd, i = bid / kXcd;
+    return x * q + min(x, r) + i;
+}
+
 // Wave-wide max over 64 lanes (every lane receives the result).
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -635,7 +635,7 @@ __device__ __forceinline__ void sp_store_tile(const v4i (&acc)[8][BMT / 32], con
                     make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
             }
         }
-        flush_rows<kU, 2, true>(stage, BMT / 2, ep, wm, wn);
+        flush_rows<kU, 2, true, false, BMT / 2>(stage, ep, wm, wn);
     } else {
         constexpr int kU = 32, kRowBytes = 512;              // 128 INT32 columns per staged row
         int8_t* strip = lds + wave * (16 * kRowBytes);
@@ -647,7 +647,7 @@ __device__ __forceinline__ void sp_store_tile(const v4i (&acc)[8][BMT / 32], con
                 *reinterpret_cast<int4*>(strip + r16 * kRowBytes + ((u ^ (r16 & (kU - 1))) << 4)) =
                     make_int4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
             }
-            flush_rows<kU, 4, false, true>(strip, 16, ep, wm + 16 * j, wn);
+            flush_rows<kU, 4, false, true, 16>(strip, ep, wm + 16 * j, wn);
         }
     }
 }

@@ -509,45 +509,63 @@ struct GemmEpilogue {
     const uint16_t* post_bias;
 };
 
-// Copies `rows` x kU 16-byte units of a wave-private staging area (rows of kRowBytes, unit u
-// of row r at slot u ^ (r % kU)) to the output with coalesced 16-byte row stores. NT: non-
-// temporal stores (used for INT32 outputs, which are large and seldom re-read soon: measured
-// 2.5 us faster at 4096^2; FP16 outputs keep cached stores for the next layer's quantize).
-template <int kU, int kEsz, bool DEQUANT, bool NT = false>
-__device__ __forceinline__ void flush_rows(const int8_t* stage, int rows, const GemmEpilogue& ep, int row0,
-                                           int col0) {
+// Copies kRows x kU 16-byte units of a wave-private staging area (rows of kRowBytes, unit u
+// of row r at slot u ^ (r % kU)) to the output with coalesced 16-byte row stores. The units
+// go in batches of kB per lane: all kB LDS reads are issued before the first store, so the
+// LDS latency is paid once per batch rather than once per unit (a loop of read -> wait ->
+// store left the epilogue latency-bound). NT: non-temporal stores (used for INT32 outputs,
+// which are large and seldom re-read soon: measured 2.5 us faster at 4096^2; FP16 outputs
+// keep cached stores for the next layer's quantize).
+template <int kU, int kEsz, bool DEQUANT, bool NT = false, int kRows>
+__device__ __forceinline__ void flush_rows(const int8_t* stage, const GemmEpilogue& ep, int row0, int col0) {
     constexpr int kPer = 16 / kEsz;
     constexpr int kRowBytes = kU * 16;
+    constexpr int kUnits = kRows * kU;
+    static_assert(kUnits % kWave == 0, "staged units must fill whole wave passes");
+    constexpr int kIters = kUnits / kWave;
+    constexpr int kB = kIters < 8 ? kIters : 8;
+    static_assert(kIters % kB == 0, "batch must divide the passes");
     const int lane = threadIdx.x & (kWave - 1);
     const int M = ep.M, N = ep.N;
-    for (int idx = lane; idx < rows * kU; idx += kWave) {
-        const int r = idx / kU, u = idx % kU;
-        const int4 v = *reinterpret_cast<const int4*>(stage + r * kRowBytes + ((u ^ (r & (kU - 1))) << 4));
-        const int row = row0 + r;
-        const int col = col0 + u * kPer;
-        if (row >= M || col >= N) continue;
-        const size_t o = static_cast<size_t>(row) * N + col;
-        if (ep.vec_out && col + kPer <= N) {
-            if constexpr (NT) {
-                const v4i w = v4i{v.x, v.y, v.z, v.w};
-                if constexpr (DEQUANT) __builtin_nontemporal_store(w, reinterpret_cast<v4i*>(ep.c16 + o));
-                else __builtin_nontemporal_store(w, reinterpret_cast<v4i*>(ep.c32 + o));
-            } else {
-                if constexpr (DEQUANT) *reinterpret_cast<int4*>(ep.c16 + o) = v;
-                else *reinterpret_cast<int4*>(ep.c32 + o) = v;
-            }
-        } else {
-            // Ragged or unaligned rows: element stores (constant register indices).
-            const int n_ok = N - col;
-            const uint32_t w[4] = {static_cast<uint32_t>(v.x), static_cast<uint32_t>(v.y),
-                                   static_cast<uint32_t>(v.z), static_cast<uint32_t>(v.w)};
+#pragma unroll 1
+    for (int it = 0; it < kIters; it += kB) {
+        int4 v[kB];
 #pragma unroll
-            for (int t = 0; t < kPer; t++) {
-                if (t >= n_ok) break;
-                if constexpr (DEQUANT)
-                    ep.c16[o + t] = static_cast<uint16_t>(w[t >> 1] >> (16 * (t & 1)));
-                else
-                    ep.c32[o + t] = static_cast<int32_t>(w[t]);
+        for (int b = 0; b < kB; b++) {
+            const int idx = lane + (it + b) * kWave;
+            const int r = idx / kU, u = idx % kU;
+            v[b] = *reinterpret_cast<const int4*>(stage + r * kRowBytes + ((u ^ (r & (kU - 1))) << 4));
+        }
+#pragma unroll
+        for (int b = 0; b < kB; b++) {
+            const int idx = lane + (it + b) * kWave;
+            const int r = idx / kU, u = idx % kU;
+            const int row = row0 + r;
+            const int col = col0 + u * kPer;
+            if (row >= M || col >= N) continue;
+            const size_t o = static_cast<size_t>(row) * N + col;
+            if (ep.vec_out && col + kPer <= N) {
+                if constexpr (NT) {
+                    const v4i w = v4i{v[b].x, v[b].y, v[b].z, v[b].w};
+                    if constexpr (DEQUANT) __builtin_nontemporal_store(w, reinterpret_cast<v4i*>(ep.c16 + o));
+                    else __builtin_nontemporal_store(w, reinterpret_cast<v4i*>(ep.c32 + o));
+                } else {
+                    if constexpr (DEQUANT) *reinterpret_cast<int4*>(ep.c16 + o) = v[b];
+                    else *reinterpret_cast<int4*>(ep.c32 + o) = v[b];
+                }
+            } else {
+                // Ragged or unaligned rows: element stores (constant register indices).
+                const int n_ok = N - col;
+                const uint32_t w[4] = {static_cast<uint32_t>(v[b].x), static_cast<uint32_t>(v[b].y),
+                                       static_cast<uint32_t>(v[b].z), static_cast<uint32_t>(v[b].w)};
+#pragma unroll
+                for (int t = 0; t < kPer; t++) {
+                    if (t >= n_ok) break;
+                    if constexpr (DEQUANT)
+                        ep.c16[o + t] = static_cast<uint16_t>(w[t >> 1] >> (16 * (t & 1)));
+                    else
+                        ep.c32[o + t] = static_cast<int32_t>(w[t]);
+                }
             }
         }
     }
@@ -565,8 +583,10 @@ __device__ __forceinline__ uint32_t add_bias_pair(uint32_t d, float b) {
 // and the two kw values of a pixel are adjacent in the output row 2h + kh. vec_out: groups
 // of 4 pixels (one image row, since W % 4 == 0) become one 16-byte store of 8 halves, and
 // each lane keeps one group across its loop, so the pixel coordinates are computed once.
+// pbias: the wave's LDS strip of post_bias[co] per wave-local column.
 template <int kU, int kRows>
-__device__ __forceinline__ void flush_up2x2(const int8_t* stage, const GemmEpilogue& ep, int row0, int col0) {
+__device__ __forceinline__ void flush_up2x2(const int8_t* stage, const uint16_t* pbias, const GemmEpilogue& ep,
+                                            int row0, int col0) {
     constexpr int kRowBytes = kU * 16;
     constexpr int kPairs = kU * 4;                   // (co, kh) column pairs in the wave tile
     const int lane = threadIdx.x & (kWave - 1);
@@ -587,21 +607,34 @@ __device__ __forceinline__ void flush_up2x2(const int8_t* stage, const GemmEpilo
         if (m >= M) return;                          // M % 4 == 0: a group is all in or all out
         const int img = m / HW, p = m - img * HW, h = p / W, w = p - h * W;
         uint16_t* base = ep.c16 + static_cast<size_t>(img) * Co * plane + 2 * h * W2 + 2 * w;
-        for (int j = lane / kQuads; j < kPairs; j += kWave / kQuads) {
-            const int cw = 2 * j, n = col0 + cw;
-            if (n >= N) break;
-            const int co = n >> 2, kh = (n >> 1) & 1;
-            uint32_t d[4];
+        // Column pairs j = lane / kQuads + k * (kWave / kQuads), in batches of kB whose LDS
+        // words are all read before the first store.
+        constexpr int kStep = kWave / kQuads, kIters = kPairs / kStep;
+        constexpr int kB = kIters < 4 ? kIters : 4;
+        static_assert(kPairs % kStep == 0 && kIters % kB == 0, "pairs must split evenly");
+#pragma unroll 1
+        for (int k0 = 0; k0 < kIters; k0 += kB) {
+            uint32_t d[kB][4];
 #pragma unroll
-            for (int t = 0; t < 4; t++) d[t] = word(4 * g + t, cw);
-            if (has_bias) {
-                const float b = h2f(ep.post_bias[co]);
+            for (int b = 0; b < kB; b++) {
+                const int cw = 2 * (lane / kQuads + (k0 + b) * kStep);
 #pragma unroll
-                for (int t = 0; t < 4; t++) d[t] = add_bias_pair(d[t], b);
+                for (int t = 0; t < 4; t++) d[b][t] = word(4 * g + t, cw);
             }
-            *reinterpret_cast<int4*>(base + co * plane + kh * W2) =
-                make_int4(static_cast<int>(d[0]), static_cast<int>(d[1]), static_cast<int>(d[2]),
-                          static_cast<int>(d[3]));
+#pragma unroll
+            for (int b = 0; b < kB; b++) {
+                const int cw = 2 * (lane / kQuads + (k0 + b) * kStep), n = col0 + cw;
+                if (n >= N) continue;
+                const int co = n >> 2, kh = (n >> 1) & 1;
+                if (has_bias) {
+                    const float bf = h2f(pbias[cw]);
+#pragma unroll
+                    for (int t = 0; t < 4; t++) d[b][t] = add_bias_pair(d[b][t], bf);
+                }
+                *reinterpret_cast<int4*>(base + co * plane + kh * W2) =
+                    make_int4(static_cast<int>(d[b][0]), static_cast<int>(d[b][1]), static_cast<int>(d[b][2]),
+                              static_cast<int>(d[b][3]));
+            }
         }
     } else {
         for (int r = lane; r < kRows; r += kWave) {
@@ -614,7 +647,7 @@ __device__ __forceinline__ void flush_up2x2(const int8_t* stage, const GemmEpilo
                 if (n >= N) break;
                 const int co = n >> 2, kh = (n >> 1) & 1;
                 uint32_t d = word(r, cw);
-                if (has_bias) d = add_bias_pair(d, h2f(ep.post_bias[co]));
+                if (has_bias) d = add_bias_pair(d, h2f(pbias[cw]));
                 uint16_t* o = base + co * plane + kh * W2;
                 o[0] = static_cast<uint16_t>(d & 0xFFFFu);
                 o[1] = static_cast<uint16_t>(d >> 16);
@@ -673,11 +706,14 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[BN / 64][BM / 64], 
         {
             constexpr int kIt = (BN / 2 + kWave - 1) / kWave;
             uint16_t wv[kIt], bw[kIt];
+            // The upsample scatter's bias strip holds post_bias[co] per column instead (its
+            // GEMM value has no bias); without a post_bias it reads w_scale (ignored).
+            const uint16_t* psrc = ep.post_bias ? ep.post_bias : ep.w_scale;
 #pragma unroll
             for (int k = 0; k < kIt; k++) {
                 const int n = min(wn + lane + kWave * k, N - 1);
                 wv[k] = ep.w_scale[ep.up_w ? n >> 2 : n];
-                bw[k] = bsrc[n];
+                bw[k] = ep.up_w ? psrc[n >> 2] : bsrc[n];
             }
 #pragma unroll
             for (int k = 0; k < kIt; k++) {
@@ -717,8 +753,8 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[BN / 64][BM / 64], 
                 }
             }
         }
-        if (ep.up_w) flush_up2x2<kU, BM / 2>(stage, ep, wm, wn);
-        else flush_rows<kU, kEsz, true>(stage, BM / 2, ep, wm, wn);
+        if (ep.up_w) flush_up2x2<kU, BM / 2>(stage, bl, ep, wm, wn);
+        else flush_rows<kU, kEsz, true, false, BM / 2>(stage, ep, wm, wn);
     } else {
         int8_t* strip = lds + wave * (32 * kRowBytes);
 #pragma unroll
@@ -732,7 +768,7 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[BN / 64][BM / 64], 
                         make_int4(acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3]);
                 }
             }
-            flush_rows<kU, kEsz, false, true>(strip, 32, ep, wm + 32 * i, wn);
+            flush_rows<kU, kEsz, false, true, 32>(strip, ep, wm + 32 * i, wn);
         }
     }
 }

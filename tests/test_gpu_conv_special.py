@@ -4,11 +4,12 @@ Every output is compared bit-for-bit with the oracle (oracle/forge_oracle.c), wh
 src/nn/int8_depthwise_conv2d.cu:25-103 and src/nn/int8_conv_transpose2d.cu:70-191 and is
 pinned against torch float64 convolutions in tests/test_oracle.py. The reference test's own
 cases (tests/test_int8_special_conv.cu:266-279) are included with its float criterion.
-Branches covered: the depthwise LDS tile kernel (vector and ragged stores, zero-padding and
-the masked loop for non-finite taps) and the direct kernel (strides, dilations, wide
-kernels); the transposed conv's pixel quantizer (4-byte and byte rows, LDS stash and
-re-read), the three GEMM engines under the scatter epilogue (16-byte groups and element
-stores), image chunking, and the configs' full-size shape."""
+Branches covered: the depthwise rolling-window kernel (every kernel size and padding it
+takes, several strips and column waves, ragged and unaligned stores, non-finite taps), the
+LDS tile kernel (the other stride-1 shapes; its masked loop for non-finite taps) and the
+direct kernel (strides, dilations, wide kernels); the transposed conv's pixel quantizer
+(4-byte and byte rows, LDS stash and re-read), the three GEMM engines under the scatter
+epilogue (16-byte groups and element stores), image chunking, and the full-size shapes."""
 import numpy as np
 import pytest
 
@@ -51,6 +52,14 @@ DW_CASES = [
     (1, 4, 25, 26, 3, 3, (2, 2), (1, 1), (2, 2), True),      # direct kernel: dilation
     (1, 2, 20, 30, 3, 11, (1, 5), (1, 1), (1, 1), True),     # direct kernel: kW > 9
     (1, 1, 1, 1, 1, 1, (0, 0), (1, 1), (1, 1), True),
+    # rolling-window kernel (W % 8 == 0, square 1/3/5/7, column pad (k-1)/2 or 0)
+    (2, 3, 40, 64, 7, 7, (3, 3), (1, 1), (1, 1), True),
+    (1, 2, 21, 32, 7, 7, (0, 0), (1, 1), (1, 1), True),     # valid conv, Wo % 8 != 0
+    (1, 5, 33, 48, 5, 5, (1, 0), (1, 1), (1, 1), False),    # row pad != column pad
+    (3, 4, 17, 16, 1, 1, (0, 0), (1, 1), (1, 1), True),
+    (1, 2, 100, 1024, 3, 3, (1, 1), (1, 1), (1, 1), True),  # 3 column waves, many strips
+    (1, 3, 9, 24, 3, 3, (2, 0), (1, 1), (1, 1), True),      # row pad 2, column pad 0
+    (1, 2, 5, 8, 5, 5, (2, 2), (1, 1), (1, 1), True),       # kernel taller than the image
 ]
 
 
@@ -87,6 +96,19 @@ def test_depthwise_nonfinite_tap_skips_padding(dev, orc):
     ws[2] = np.float16(np.inf)
     want = orc.depthwise_conv2d(x, w, ws, b, (1, 1))
     say("depthwise non-finite taps")
+    y = to_host(ops.int8_depthwise_conv2d_forward(to_dev(x, dev), to_dev(w, dev), to_dev(ws, dev), to_dev(b, dev),
+                                                  3, 3, (1, 1)))
+    assert _bits_equal(y, want)
+
+
+def test_depthwise_nonfinite_tap_tile_kernel(dev, orc):
+    """As above through the LDS tile kernel (W % 8 != 0): its masked loop."""
+    from forge_amd import ops
+    rng = np.random.default_rng(78)
+    x, w, ws, b = _dw_inputs(rng, 1, 3, 19, 26, 3, 3, True)
+    ws[0] = np.float16(-np.inf)
+    want = orc.depthwise_conv2d(x, w, ws, b, (1, 1))
+    say("depthwise non-finite taps, tile kernel")
     y = to_host(ops.int8_depthwise_conv2d_forward(to_dev(x, dev), to_dev(w, dev), to_dev(ws, dev), to_dev(b, dev),
                                                   3, 3, (1, 1)))
     assert _bits_equal(y, want)
