@@ -52,8 +52,26 @@ inline bool aligned(const void* p, size_t a) {
 __device__ __forceinline__ float h2f(uint16_t h) {
     return __half2float(__ushort_as_half(h));
 }
+// The empty asm makes f an opaque, already-rounded fp32 register value: without it the
+// backend may fuse the multiply or add that produced f into the conversion
+// (v_fma_mixlo_f16), which rounds a*b (+c) to fp16 once -- measured to differ from the
+// reference's fp32-then-fp16 rounding when the fp32 result is an fp16 tie.
 __device__ __forceinline__ uint16_t f2h(float f) {
+    asm("" : "+v"(f));
     return __half_as_ushort(__float2half_rn(f));
+}
+
+// Per-row activation quantization (src/quant/quantize.cu:49-56, 112-126): the row scale from
+// its absmax, and one value with the reciprocal scale, rounded to nearest even and clamped.
+__device__ __forceinline__ float row_scale(float amax) {
+    return fmaxf(amax, 1e-8f) / 127.0f;
+}
+
+__device__ __forceinline__ int quant1(float x, float inv) {
+    const float r = __builtin_rintf(x * inv);
+    // NaN -> 0 (as a float->int conversion of NaN gives on both vendors), then clamp.
+    int q = (r == r) ? static_cast<int>(fminf(fmaxf(r, -128.0f), 127.0f)) : 0;
+    return q;
 }
 
 // GEMM dequant epilogue: half(fma((float)acc, as*ws, bias)), or acc*(as*ws) without bias.

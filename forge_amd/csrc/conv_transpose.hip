@@ -4,7 +4,10 @@
 // pixel owns one 2x2 output block, so the layer is a GEMM of the per-pixel quantized input
 // rows (H*W, C_in) with the repacked weights (4*C_out, C_in), row co*4 + kh*2 + kw, followed
 // by a scatter to NCHW. The reference runs transpose -> quantize -> GEMM to an FP16 buffer
-// -> scatter + bias, one image at a time. Here:
+// -> scatter + bias, one image at a time. Here, for C_in in {32, 64, 128, 256} and
+// H*W % 8 == 0, convt_fused_kernel does all of it in one pass per 64-pixel tile (described at
+// the kernel): input read once, INT8 activations kept in LDS, output written once, one launch
+// for all images, no workspace traffic. Every other shape takes two kernels:
 //   1. quantize_pixels_nchw reads the NCHW image once and writes the INT8 pixel rows and
 //      their scales (no FP16 transpose buffer);
 //   2. the dense tile engine runs the GEMM with the upsample-scatter epilogue: each wave's
@@ -12,9 +15,10 @@
 //      output is) gets the bias added in fp32, is rounded again, and is stored straight into
 //      the NCHW output as 16-byte runs of 4 pixels x (kw = 0, 1) -- the (M, 4*C_out) FP16
 //      intermediate is never written.
-// Images are processed in chunks as large as the caller's workspace allows (its size is the
-// reference's formula, of which one image needs only the INT8 rows and scales), so small
-// images do not cost two launches each. Every per-pixel result is independent of the chunk.
+//    Images are processed in chunks as large as the caller's workspace allows (its size is
+//    the reference's formula, of which one image needs only the INT8 rows and scales), so
+//    small images do not cost two launches each.
+// Every per-pixel result is independent of the path and the chunking.
 #include "common.h"
 #include "gemm_dense.h"
 #include "mfma_tile.h"
@@ -24,6 +28,159 @@
 namespace forge_amd {
 
 static size_t up256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+// Single-pass kernel for C_in = 32 * KC (KC = 1, 2, 4, 8), H*W % 8 == 0: one workgroup takes
+// 64 consecutive pixels of one image and writes their whole (C_out, 2x2) output, so the INT8
+// activations never leave the chip and the input is read once.
+//   1. Thread t loads pixels 8*(t%8) .. +8 of channels t/8 + 32k as 16-byte rows (KC loads
+//      in flight), takes the per-pixel absmax over its channels, then over the wave's 8
+//      channel groups (lane shuffles) and the 4 waves (LDS): the row arithmetic of
+//      quantize_rows on each pixel's C_in values.
+//   2. The quantized pixels form the A tile in LDS (64 x C_in bytes, 16-byte chunks swizzled
+//      by row so the MFMA row reads spread over the banks).
+//   3. Work items (m-block i of 32 pixels, n-block j of 32 GEMM columns) go round-robin to the
+//      4 waves; B fragments are the weight rows, read from L2 straight into registers; K is
+//      KC steps of v_mfma_i32_32x32x32_i8.
+//   4. A lane's accumulators are one pixel x 4 consecutive columns n = co*4 + (kh, kw): the
+//      2x2 output block of one channel, so the dequant (act_scale * w_scale[co], no bias,
+//      rounded to FP16), the bias (added in fp32 and rounded again) and two 4-byte stores
+//      (rows 2h and 2h + 1) happen in registers; adjacent lanes are adjacent pixels, so each
+//      store instruction writes 128-byte runs.
+template <int KC>
+__global__ __launch_bounds__(256) void convt_fused_kernel(
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ w, const uint16_t* __restrict__ w_scale,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int HW, int W, int C_out, int tiles)
+{
+    constexpr int C = 32 * KC;
+    constexpr int kNch = C / 16;
+    static_assert((kNch & (kNch - 1)) == 0, "row swizzle needs a power-of-two chunk count");
+    __shared__ __align__(16) int8_t As[64 * C];
+    __shared__ float red[4][64];
+    __shared__ float ascale[64];
+    __shared__ float sinv[64];
+    const int t = threadIdx.x, lane = t & (kWave - 1), wave = t >> 6;
+    const int img = blockIdx.x / tiles;
+    const int p0 = (blockIdx.x - img * tiles) * 64;
+    const int np = min(64, HW - p0);                 // a multiple of 8
+
+    // 1. loads and per-pixel absmax
+    const int po = t & 7, cg = t >> 3;
+    const bool pin = 8 * po < np;
+    const uint16_t* xi = x + static_cast<size_t>(img) * C * HW + p0 + 8 * po;
+    uint4 v[KC];
+#pragma unroll
+    for (int k = 0; k < KC; k++)
+        v[k] = pin ? *reinterpret_cast<const uint4*>(xi + static_cast<size_t>(cg + 32 * k) * HW)
+                   : make_uint4(0u, 0u, 0u, 0u);
+    float m[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) m[e] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KC; k++) {
+        const uint32_t u[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            m[e] = fmaxf(m[e], fabsf(h2f(static_cast<uint16_t>((e & 1) ? (u[e >> 1] >> 16) : (u[e >> 1] & 0xFFFFu)))));
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+#pragma unroll
+        for (int off = 8; off < kWave; off <<= 1) m[e] = fmaxf(m[e], __shfl_xor(m[e], off, kWave));
+    if (lane < 8) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) red[wave][8 * po + e] = m[e];
+    }
+    __syncthreads();
+    if (t < 64) {
+        const float a = fmaxf(fmaxf(red[0][t], red[1][t]), fmaxf(red[2][t], red[3][t]));
+        const float scale = row_scale(a);
+        ascale[t] = scale;
+        sinv[t] = 1.0f / scale;
+    }
+    __syncthreads();
+
+    // 2. quantize into the A tile: As[p][c] at chunk (c / 16) ^ (p % kNch)
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const int p = 8 * po + e;
+        const float inv = sinv[p];
+#pragma unroll
+        for (int k = 0; k < KC; k++) {
+            const int c = cg + 32 * k;
+            const uint32_t word = (e & 1) ? ((&v[k].x)[e >> 1] >> 16) : ((&v[k].x)[e >> 1] & 0xFFFFu);
+            As[p * C + ((((c >> 4) ^ (p & (kNch - 1)))) << 4) + (c & 15)] =
+                static_cast<int8_t>(quant1(h2f(static_cast<uint16_t>(word)), inv));
+        }
+    }
+    __syncthreads();
+
+    // 3./4. MFMA items and the in-register scatter
+    const int N = 4 * C_out;
+    const int items = 2 * ((N + 31) / 32);
+    const int l31 = lane & 31, hi = lane >> 5;
+    const bool has_bias = bias != nullptr;
+    const size_t plane = 4 * static_cast<size_t>(HW);
+    const size_t W2 = 2 * static_cast<size_t>(W);
+    for (int it = wave; it < items; it += 4) {
+        const int i = it & 1, j = it >> 1;
+        const int n = 32 * j + l31;
+        v4i fb[KC];
+#pragma unroll
+        for (int ks = 0; ks < KC; ks++)
+            fb[ks] = n < N ? *reinterpret_cast<const v4i*>(w + static_cast<size_t>(n) * C + 16 * (2 * ks + hi))
+                           : v4i{0, 0, 0, 0};
+        float wsv[4], bv[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int co = min(8 * j + 2 * g + hi, C_out - 1);
+            wsv[g] = h2f(w_scale[co]);
+            bv[g] = has_bias ? h2f(bias[co]) : 0.0f;
+        }
+        v16i acc;
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[e] = 0;
+        const int row = 32 * i + l31;
+#pragma unroll
+        for (int ks = 0; ks < KC; ks++) {
+            const int c = 2 * ks + hi;
+            const v4i fa = *reinterpret_cast<const v4i*>(As + row * C + ((c ^ (row & (kNch - 1))) << 4));
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[ks], fa, acc, 0, 0, 0);
+        }
+        if (row < np) {
+            const int p = p0 + row, h = p / W, wc = p - h * W;
+            const float as = ascale[row];
+            uint16_t* ybase = y + static_cast<size_t>(img) * C_out * plane + 2 * h * W2 + 2 * wc;
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int co = 8 * j + 2 * g + hi;     // columns 4co .. 4co + 3
+                if (co >= C_out) continue;
+                uint32_t hv[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    uint16_t r = dequant_gemm(acc[4 * g + q], as, wsv[g], 0.0f, false);
+                    if (has_bias) r = f2h(h2f(r) + bv[g]);
+                    hv[q] = r;
+                }
+                uint16_t* o = ybase + co * plane;
+                *reinterpret_cast<uint32_t*>(o) = hv[0] | (hv[1] << 16);        // kh = 0, kw = 0, 1
+                *reinterpret_cast<uint32_t*>(o + W2) = hv[2] | (hv[3] << 16);   // kh = 1
+            }
+        }
+    }
+}
+
+template <int KC>
+static int launch_convt_fused(const uint16_t* input, const int8_t* weight, const uint16_t* w_scale,
+                              const uint16_t* bias, uint16_t* output, int N, int HW, int W, int C_out,
+                              hipStream_t s)
+{
+    const int tiles = divup(HW, 64);
+    const long long blocks = static_cast<long long>(N) * tiles;
+    if (blocks > 0x7FFFFFFFLL) return FORGE_EINVAL;
+    convt_fused_kernel<KC><<<static_cast<unsigned>(blocks), 256, 0, s>>>(input, weight, w_scale, bias, output, HW, W,
+                                                                        C_out, tiles);
+    return launch_status();
+}
 
 }  // namespace forge_amd
 
@@ -46,12 +203,22 @@ extern "C" int forge_int8_conv_transpose2d_k2s2_forward(const uint16_t* input, c
     if (!input || !weight || !w_scale || !output || !workspace) return FORGE_EINVAL;
     const long long HW = static_cast<long long>(H) * W;
     if (HW > 0x7FFFFFFFLL || 4LL * C_out > 0x7FFFFFFFLL) return FORGE_EINVAL;
+    hipStream_t s = as_stream(stream);
+    if (HW % 8 == 0 && aligned(input, 16) && aligned(weight, 16) && aligned(output, 4)) {
+        const int hw = static_cast<int>(HW);
+        switch (C_in) {
+            case 32:  return launch_convt_fused<1>(input, weight, w_scale, bias, output, N, hw, W, C_out, s);
+            case 64:  return launch_convt_fused<2>(input, weight, w_scale, bias, output, N, hw, W, C_out, s);
+            case 128: return launch_convt_fused<4>(input, weight, w_scale, bias, output, N, hw, W, C_out, s);
+            case 256: return launch_convt_fused<8>(input, weight, w_scale, bias, output, N, hw, W, C_out, s);
+            default: break;
+        }
+    }
     const size_t per_image = up256(static_cast<size_t>(HW) * C_in) + up256(static_cast<size_t>(HW) * 4);
     const size_t ws_bytes = forge_int8_conv_transpose2d_k2s2_workspace_size(C_in, H, W, C_out);
     long long chunk = static_cast<long long>(ws_bytes / per_image);
     chunk = std::max(1LL, std::min<long long>(chunk, N));
     chunk = std::min<long long>(chunk, 0x7FFFFFFFLL / HW);       // GEMM rows stay in int range
-    hipStream_t s = as_stream(stream);
     const int Ng = 4 * C_out;
     const size_t in_img = static_cast<size_t>(C_in) * HW, out_img = static_cast<size_t>(Ng) * HW;
     for (long long n0 = 0; n0 < N; n0 += chunk) {

@@ -631,9 +631,9 @@ __device__ __forceinline__ void flush_up2x2(const int8_t* stage, const uint16_t*
 #pragma unroll
                     for (int t = 0; t < 4; t++) d[b][t] = add_bias_pair(d[b][t], bf);
                 }
-                *reinterpret_cast<int4*>(base + co * plane + kh * W2) =
-                    make_int4(static_cast<int>(d[b][0]), static_cast<int>(d[b][1]), static_cast<int>(d[b][2]),
-                              static_cast<int>(d[b][3]));
+                __builtin_nontemporal_store(v4i{static_cast<int>(d[b][0]), static_cast<int>(d[b][1]),
+                                                static_cast<int>(d[b][2]), static_cast<int>(d[b][3])},
+                                            reinterpret_cast<v4i*>(base + co * plane + kh * W2));
             }
         }
     } else {
@@ -754,7 +754,7 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[BN / 64][BM / 64], 
             }
         }
         if (ep.up_w) flush_up2x2<kU, BM / 2>(stage, bl, ep, wm, wn);
-        else flush_rows<kU, kEsz, true, false, BM / 2>(stage, ep, wm, wn);
+        else flush_rows<kU, kEsz, true, true, BM / 2>(stage, ep, wm, wn);
     } else {
         int8_t* strip = lds + wave * (32 * kRowBytes);
 #pragma unroll

@@ -18,17 +18,6 @@
 
 namespace forge_amd {
 
-__device__ __forceinline__ float row_scale(float amax) {
-    return fmaxf(amax, 1e-8f) / 127.0f;
-}
-
-__device__ __forceinline__ int quant1(float x, float inv) {
-    const float r = __builtin_rintf(x * inv);
-    // NaN -> 0 (as a float->int conversion of NaN gives on both vendors), then clamp.
-    int q = (r == r) ? static_cast<int>(fminf(fmaxf(r, -128.0f), 127.0f)) : 0;
-    return q;
-}
-
 // 8 halves (one uint4) -> 8 int8 packed into a uint2.
 __device__ __forceinline__ uint2 quant8(uint4 v, float inv) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};

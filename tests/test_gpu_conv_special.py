@@ -7,9 +7,11 @@ cases (tests/test_int8_special_conv.cu:266-279) are included with its float crit
 Branches covered: the depthwise rolling-window kernel (every kernel size and padding it
 takes, several strips and column waves, ragged and unaligned stores, non-finite taps), the
 LDS tile kernel (the other stride-1 shapes; its masked loop for non-finite taps) and the
-direct kernel (strides, dilations, wide kernels); the transposed conv's pixel quantizer
-(4-byte and byte rows, LDS stash and re-read), the three GEMM engines under the scatter
-epilogue (16-byte groups and element stores), image chunking, and the full-size shapes."""
+direct kernel (strides, dilations, wide kernels); the transposed conv's fused single-pass
+kernel (partial pixel tiles and column blocks, rows that span image rows) and its two-kernel
+path: the pixel quantizer (4-byte and byte rows, LDS stash and re-read), the three GEMM
+engines under the scatter epilogue (16-byte groups and element stores), image chunking; and
+the full-size shapes."""
 import numpy as np
 import pytest
 
@@ -153,14 +155,21 @@ def _ct_inputs(rng, N, C_in, H, W, C_out, bias):
 
 CT_CASES = [
     # N, C_in, H, W, C_out, bias
-    (1, 32, 16, 16, 64, True),      # reference test cases
+    (1, 32, 16, 16, 64, True),      # reference test cases (the first two take the fused kernel)
     (1, 64, 8, 8, 32, True),
     (1, 16, 32, 32, 16, False),
+    # fused single-pass kernel: C_in in {32, 64, 128, 256}, H*W % 8 == 0
+    (1, 128, 32, 64, 64, True),
+    (2, 256, 24, 36, 96, False),
+    (2, 64, 6, 12, 5, True),        # partial pixel tile, C_out % 8 != 0 (partial column block)
+    (1, 32, 3, 8, 33, True),        # 5 column blocks over 4 waves
+    (1, 128, 8, 3, 16, True),       # odd W: a 32-pixel block spans image rows
+    # two-kernel path: pixel quantizer + GEMM with the scatter epilogue
     (3, 24, 7, 5, 10, True),        # W % 4 != 0: element stores; chunked images
     (2, 13, 6, 8, 5, True),         # C_in % 4 != 0: byte rows, byte-gather GEMM
     (1, 640, 4, 8, 8, True),        # C_in > 512: the quantizer re-reads x
-    (1, 128, 32, 64, 64, True),     # C_in % 128 == 0: DMA engine
-    (2, 256, 24, 36, 96, False),    # DMA engine, 256-row tiles
+    (1, 384, 16, 16, 40, True),     # C_in % 128 == 0: DMA engine
+    (2, 192, 24, 36, 96, False),    # register-staged engine
     (1, 48, 1, 1, 7, True),         # one pixel
     (5, 8, 3, 4, 3, True),          # many small images in one chunk
 ]
