@@ -18,7 +18,10 @@ what the same counters read for a device copy of known size in the same runs.
 extra: configs[2] (2:4 sparse vs dense at 4096x11008x4096), configs[3] (decode
 M = 1/4/16, N = K = 8192, dense and 2:4, HBM GB/s with 6 rotating weight copies so the
 256 MB MALL cannot hold them; calls captured into a HIP graph and replayed so host launch
-overhead is not timed) and configs[4] (INT8 NHWC 3x3 conv, INT32 and dequant outputs).
+overhead is not timed), configs[4] (INT8 NHWC 3x3 conv, INT32 and dequant outputs), and
+the rest of the INT8 conv family on NCHW FP16 maps: depthwise 3x3 (1, 64, 540, 960) and
+ConvTranspose2d k2s2 (1, 64, 270, 480) -> (1, 32, 540, 960), as time and HBM GB/s of
+input + output bytes.
 """
 from __future__ import annotations
 
@@ -249,6 +252,35 @@ def bench_extra(dev):
     out["c5_conv_s32_us"] = t32 * 1e3
     out["c5_conv_dequant_tops"] = ops_c / t16 / 1e9
     out["c5_conv_dequant_us"] = t16 * 1e3
+    del xc, wc, o32, o16
+    torch.cuda.empty_cache()
+
+    # The rest of the INT8 conv family (NCHW FP16 in and out), HBM-bound:
+    # depthwise 3x3, pad 1: (1, 64, 540, 960) -> same shape; bytes = input + output;
+    # ConvTranspose2d k2s2: (1, 64, 270, 480) -> (1, 32, 540, 960); bytes = input + output + weights.
+    xd = (torch.rand((1, 64, 540, 960), generator=g, device=dev) * 2 - 1).half()
+    wd = torch.randint(-127, 128, (64, 9), generator=g, device=dev, dtype=torch.int8)
+    wsd = (torch.rand((64,), generator=g, device=dev) * 0.045 + 0.005).half()
+    bd = (torch.rand((64,), generator=g, device=dev) - 0.5).half()
+    yd = torch.empty_like(xd)
+    dw = lambda: ops.int8_depthwise_conv2d_forward(xd, wd, wsd, bd, 3, 3, (1, 1), out=yd)
+    xt = (torch.rand((1, 64, 270, 480), generator=g, device=dev) * 2 - 1).half()
+    wt = torch.randint(-127, 128, (4 * 32, 64), generator=g, device=dev, dtype=torch.int8)
+    wst = (torch.rand((32,), generator=g, device=dev) * 0.045 + 0.005).half()
+    bt = (torch.rand((32,), generator=g, device=dev) - 0.5).half()
+    yt = torch.empty((1, 32, 540, 960), dtype=torch.float16, device=dev)
+    wsp = torch.empty((ops.int8_conv_transpose2d_k2s2_workspace_size(64, 270, 480, 32),), dtype=torch.uint8,
+                      device=dev)
+    ct = lambda: ops.int8_conv_transpose2d_k2s2_forward(xt, wt, wst, bt, workspace=wsp, out=yt)
+    for _ in range(3):
+        dw()
+        ct()
+    t_dw = events_time_ms(dw, 20)
+    t_ct = events_time_ms(ct, 20)
+    out["f2_depthwise_us"] = t_dw * 1e3
+    out["f2_depthwise_GBs"] = (xd.numel() * 2 + yd.numel() * 2) / t_dw / 1e6
+    out["f2_convT_us"] = t_ct * 1e3
+    out["f2_convT_GBs"] = (xt.numel() * 2 + yt.numel() * 2 + wt.numel()) / t_ct / 1e6
     return out
 
 

@@ -513,9 +513,9 @@ struct GemmEpilogue {
 // of row r at slot u ^ (r % kU)) to the output with coalesced 16-byte row stores. The units
 // go in batches of kB per lane: all kB LDS reads are issued before the first store, so the
 // LDS latency is paid once per batch rather than once per unit (a loop of read -> wait ->
-// store left the epilogue latency-bound). NT: non-temporal stores (used for INT32 outputs,
-// which are large and seldom re-read soon: measured 2.5 us faster at 4096^2; FP16 outputs
-// keep cached stores for the next layer's quantize).
+// store left the epilogue latency-bound). NT: non-temporal stores, used for both output
+// types (measured: INT32 4096^2 2.5 us faster; FP16 4096^2 0.8 us and M = 129,600 x 128,
+// K = 64 2 us faster than cached stores).
 template <int kU, int kEsz, bool DEQUANT, bool NT = false, int kRows>
 __device__ __forceinline__ void flush_rows(const int8_t* stage, const GemmEpilogue& ep, int row0, int col0) {
     constexpr int kPer = 16 / kEsz;
