@@ -21,7 +21,8 @@ M = 1/4/16, N = K = 8192, dense and 2:4, HBM GB/s with 6 rotating weight copies 
 overhead is not timed), configs[4] (INT8 NHWC 3x3 conv, INT32 and dequant outputs), and
 the rest of the INT8 conv family on NCHW FP16 maps: depthwise 3x3 (1, 64, 540, 960) and
 ConvTranspose2d k2s2 (1, 64, 270, 480) -> (1, 32, 540, 960), as time and HBM GB/s of
-input + output bytes.
+input + output bytes; and SparseLinear's weight preparation at 11008 x 4096 fp32, one pass
+against the reference's separate quantize / prune+compress / pack steps.
 """
 from __future__ import annotations
 
@@ -281,6 +282,32 @@ def bench_extra(dev):
     out["f2_depthwise_GBs"] = (xd.numel() * 2 + yd.numel() * 2) / t_dw / 1e6
     out["f2_convT_us"] = t_ct * 1e3
     out["f2_convT_GBs"] = (xt.numel() * 2 + yt.numel() * 2 + wt.numel()) / t_ct / 1e6
+    del xd, yd, xt, yt, wsp
+    torch.cuda.empty_cache()
+
+    # Weight preparation for SparseLinear at configs[2]'s weight (11008 x 4096, fp32): the one
+    # pass (quantize + prune + compress + gfx950 pack) against the reference's sequence of
+    # separate steps (quantize rows, prune_compress_24 through a raw-nibble buffer, pack).
+    N, K = 11008, 4096
+    wf = torch.randn((N, K), generator=g, device=dev) * 0.02
+    qw = torch.empty((N, K), dtype=torch.int8, device=dev)
+    qs = torch.empty((N,), dtype=torch.float16, device=dev)
+    cp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+    rw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+    mt = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+    one = lambda: ops.prepare_sparse_weight(wf)
+    def steps():
+        ops.quantize_weight_rows(wf, qw, qs)
+        ops.prune_compress_24(qw, cp, rw, N, K)
+        ops.pack_metadata(rw, mt, N, K)
+    for _ in range(3):
+        one()
+        steps()
+    t_one = events_time_ms(one, 10)
+    t_steps = events_time_ms(steps, 10)
+    out["f4_prep_sparse_us"] = t_one * 1e3
+    out["f4_prep_sparse_GBs"] = (N * K * 4 + N * K // 2 + N * K // 8 + N * 2) / t_one / 1e6
+    out["f4_prep_steps_us"] = t_steps * 1e3
     return out
 
 

@@ -44,6 +44,8 @@ SIGNATURES = {
     "forge_int8_conv2d_forward": (_I, [_P, _P, _P, _P, _P] + [_I] * 13 + [_P, _P]),
     "forge_int8_conv2d_nhwc_s32": (_I, [_P, _P, _P] + [_I] * 13 + [_P]),
     "forge_int8_conv2d_nhwc_dequant": (_I, [_P, _P, _P, _P, _P, _P] + [_I] * 13 + [_P]),
+    "forge_quantize_weight_rows": (_I, [_P, _I, _P, _P, _I, _I, _P]),
+    "forge_prepare_sparse_weight": (_I, [_P, _I, _P, _P, _P, _I, _I, _P]),
     "forge_int8_conv_transpose2d_k2s2_workspace_size": (ctypes.c_size_t, [_I] * 4),
     "forge_int8_conv_transpose2d_k2s2_forward": (_I, [_P] * 5 + [_I] * 5 + [_P, _P]),
     "forge_int8_depthwise_conv2d_forward": (_I, [_P] * 5 + [_I] * 12 + [_P]),

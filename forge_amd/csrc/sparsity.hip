@@ -90,6 +90,116 @@ __global__ __launch_bounds__(256) void unpack_metadata_kernel(
     }
 }
 
+// ---- weight preparation ------------------------------------------------------------
+// python/forge/nn/linear.py:168-173 and :231-249 quantize a weight matrix with torch float32
+// ops (scale = clamp(amax|w|, 1e-8) / 127, q = clamp(round(w / scale), -127, 127), scale
+// stored as FP16), then SparseLinear launches prune_compress and pack_metadata through a raw
+// nibble buffer. Here one workgroup per weight row does all of it: the row absmax (first read),
+// then per 32-value chunk (second read, from L2) the IEEE division, round-half-even and clamp,
+// the 2:4 prune of its 8 groups (prune4, the reference's tie rule), one 16-byte store of the
+// compressed bytes and one index word at its gfx950 position. No dense INT8 or raw-nibble
+// intermediate exists. The dense variant (QuantizedLinear) writes the INT8 row instead.
+
+template <bool F16>
+__device__ __forceinline__ float wload(const void* w, size_t i) {
+    if constexpr (F16) return h2f(static_cast<const uint16_t*>(w)[i]);
+    else return static_cast<const float*>(w)[i];
+}
+
+// 32 consecutive values from element offset off (a multiple of 32; 16-byte aligned base).
+template <bool F16>
+__device__ __forceinline__ void wload32(const void* w, size_t off, float (&v)[32]) {
+    if constexpr (F16) {
+        const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(w) + off);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint4 u = p[j];
+            const uint32_t ws[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                v[8 * j + 2 * e] = h2f(static_cast<uint16_t>(ws[e] & 0xFFFFu));
+                v[8 * j + 2 * e + 1] = h2f(static_cast<uint16_t>(ws[e] >> 16));
+            }
+        }
+    } else {
+        const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(w) + off);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float4 f = p[j];
+            v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+        }
+    }
+}
+
+__device__ __forceinline__ int8_t quant_weight(float x, float scale) {
+    const float r = fminf(fmaxf(__builtin_rintf(x / scale), -127.0f), 127.0f);
+    return static_cast<int8_t>(static_cast<int>(r));
+}
+
+// Row absmax over the workgroup (256 threads), the reference's scale, and its FP16 copy.
+__device__ __forceinline__ float block_row_scale(float amax, uint16_t* w_scale, int n) {
+    __shared__ float red[4];
+    amax = wave_max(amax);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float scale = row_scale(amax);
+    if (threadIdx.x == 0) w_scale[n] = f2h(scale);
+    return scale;
+}
+
+template <bool F16>
+__global__ __launch_bounds__(256) void prepare_sparse_weight_kernel(
+    const void* __restrict__ w, int8_t* __restrict__ comp, uint32_t* __restrict__ meta,
+    uint16_t* __restrict__ w_scale, int N, int K)
+{
+    const int n = blockIdx.x, t = threadIdx.x;
+    const int cpr = K / 32;
+    const size_t row = static_cast<size_t>(n) * K;
+    float amax = 0.0f;
+    for (int c = t; c < cpr; c += 256) {
+        float v[32];
+        wload32<F16>(w, row + 32 * static_cast<size_t>(c), v);
+#pragma unroll
+        for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+    }
+    const float scale = block_row_scale(amax, w_scale, n);
+    for (int c = t; c < cpr; c += 256) {
+        float v[32];
+        wload32<F16>(w, row + 32 * static_cast<size_t>(c), v);
+        uint32_t cw[4] = {0u, 0u, 0u, 0u};
+        uint32_t word = 0;
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            int8_t q[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) q[i] = quant_weight(v[4 * g + i], scale);
+            int8_t c0, c1;
+            uint8_t nib;
+            prune4(q, c0, c1, nib);
+            const uint32_t pair = static_cast<uint32_t>(static_cast<uint8_t>(c0)) |
+                                  (static_cast<uint32_t>(static_cast<uint8_t>(c1)) << 8);
+            cw[g >> 1] |= pair << (16 * (g & 1));
+            word |= static_cast<uint32_t>(nib) << (4 * g);
+        }
+        *reinterpret_cast<uint4*>(comp + static_cast<size_t>(n) * (K / 2) + 16 * static_cast<size_t>(c)) =
+            make_uint4(cw[0], cw[1], cw[2], cw[3]);
+        meta[meta_pos(n, c, N, cpr)] = word;
+    }
+}
+
+template <bool F16>
+__global__ __launch_bounds__(256) void quantize_weight_rows_kernel(
+    const void* __restrict__ w, int8_t* __restrict__ q, uint16_t* __restrict__ w_scale, int K)
+{
+    const int n = blockIdx.x, t = threadIdx.x;
+    const size_t row = static_cast<size_t>(n) * K;
+    float amax = 0.0f;
+    for (int k = t; k < K; k += 256) amax = fmaxf(amax, fabsf(wload<F16>(w, row + k)));
+    const float scale = block_row_scale(amax, w_scale, n);
+    for (int k = t; k < K; k += 256) q[row + k] = quant_weight(wload<F16>(w, row + k), scale);
+}
+
 }  // namespace forge_amd
 
 namespace forge { namespace sparsity {
@@ -169,5 +279,29 @@ extern "C" int forge_unpack_metadata(const uint32_t* meta_packed, uint8_t* meta_
     const long long total = static_cast<long long>(N) * (K / 32);
     const int blocks = static_cast<int>(std::min<long long>(divupll(total, 256), 16384));
     unpack_metadata_kernel<<<blocks, 256, 0, as_stream(stream)>>>(meta_packed, meta_raw, N, K);
+    return launch_status();
+}
+
+extern "C" int forge_quantize_weight_rows(const void* w, int w_fp16, int8_t* w_int8, uint16_t* w_scale, int N, int K,
+                                          void* stream)
+{
+    if (N <= 0 || K <= 0) return FORGE_OK;
+    if (!w || !w_int8 || !w_scale) return FORGE_EINVAL;
+    hipStream_t s = as_stream(stream);
+    if (w_fp16) quantize_weight_rows_kernel<true><<<N, 256, 0, s>>>(w, w_int8, w_scale, K);
+    else        quantize_weight_rows_kernel<false><<<N, 256, 0, s>>>(w, w_int8, w_scale, K);
+    return launch_status();
+}
+
+extern "C" int forge_prepare_sparse_weight(const void* w, int w_fp16, int8_t* W_comp, uint32_t* w_meta,
+                                           uint16_t* w_scale, int N, int K, void* stream)
+{
+    if (N <= 0 || K <= 0) return FORGE_OK;
+    if (!w || !W_comp || !w_meta || !w_scale || K % 32 != 0 || !aligned(w, 16) || !aligned(W_comp, 16) ||
+        !aligned(w_meta, 4))
+        return FORGE_EINVAL;
+    hipStream_t s = as_stream(stream);
+    if (w_fp16) prepare_sparse_weight_kernel<true><<<N, 256, 0, s>>>(w, W_comp, w_meta, w_scale, N, K);
+    else        prepare_sparse_weight_kernel<false><<<N, 256, 0, s>>>(w, W_comp, w_meta, w_scale, N, K);
     return launch_status();
 }

@@ -21,14 +21,16 @@ from torch import nn
 from . import ops
 
 
-def _weight_to_int8(weight_fp: torch.Tensor):
-    """Per-output-row symmetric weight quantization (linear.py:168-173, :235-238):
-    scale = max(amax|w|, 1e-8) / 127, w_int8 = clamp(round(w / scale), -127, 127) (round half
-    to even), scale stored as FP16."""
-    w = weight_fp.to(torch.float32)
-    scale = w.abs().amax(dim=1).clamp(min=1e-8) / 127.0
-    q = torch.round(w / scale.unsqueeze(1)).clamp(-127, 127).to(torch.int8)
-    return q, scale.to(torch.float16)
+def _prep_device(module_tensor: torch.Tensor) -> torch.device:
+    """Weight preparation runs on the module's device, or cuda:0 for a CPU module."""
+    return module_tensor.device if module_tensor.is_cuda else torch.device("cuda", 0)
+
+
+def _as_weight(weight_fp: torch.Tensor, dev: torch.device) -> torch.Tensor:
+    """The reference converts any float weight to float32 (linear.py:169, :234); fp16 and fp32
+    go to the device as they are (the kernel widens fp16 exactly), other dtypes as float32."""
+    w = weight_fp if weight_fp.dtype in (torch.float16, torch.float32) else weight_fp.to(torch.float32)
+    return w.to(dev).contiguous()
 
 
 class _Int8LinearFn(torch.autograd.Function):
@@ -82,7 +84,10 @@ class QuantizedLinear(nn.Module):
 
     @torch.no_grad()
     def quantize_weight(self, weight_fp: torch.Tensor) -> None:
-        q, scale = _weight_to_int8(weight_fp)
+        """Per-output-row symmetric quantization (linear.py:167-173) on the device:
+        scale = max(amax|w|, 1e-8) / 127, w_int8 = clamp(round(w / scale), -127, 127) (round half
+        to even, IEEE division), scale stored as FP16."""
+        q, scale = ops.quantize_weight_rows(_as_weight(weight_fp, _prep_device(self.w_int8)))
         self.w_int8.copy_(q)
         self.w_scale.data.copy_(scale)
 
@@ -136,17 +141,10 @@ class SparseLinear(nn.Module):
 
     @torch.no_grad()
     def from_dense_weight(self, weight_fp: torch.Tensor) -> None:
-        """Quantize per row, prune 2:4 (the lower-magnitude pair of each group of 4), compress
-        and pack the index words, on the module's device (or cuda:0 for a CPU module)."""
-        q, scale = _weight_to_int8(weight_fp)
-        N, K = q.shape
-        dev = self.W_comp.device if self.W_comp.is_cuda else torch.device("cuda", 0)
-        qd = q.to(dev).contiguous()
-        comp = torch.empty(N, K // 2, dtype=torch.int8, device=dev)
-        raw = torch.empty(N * K // 4, dtype=torch.uint8, device=dev)
-        meta = torch.empty(N, K // 32, dtype=torch.int32, device=dev)
-        ops.prune_compress_24(qd, comp, raw, N, K)
-        ops.pack_metadata(raw, meta, N, K)
+        """linear.py:231-249 in one device pass (forge_prepare_sparse_weight): quantize per row
+        as QuantizedLinear does, prune 2:4 (the lower-magnitude pair of each group of 4),
+        compress, and write the index words in the gfx950 order."""
+        comp, meta, scale = ops.prepare_sparse_weight(_as_weight(weight_fp, _prep_device(self.W_comp)))
         self.W_comp.copy_(comp)
         self.w_meta.copy_(meta)
         self.w_scale.data.copy_(scale)

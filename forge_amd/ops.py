@@ -372,3 +372,41 @@ def int8_depthwise_conv2d_forward(input: torch.Tensor, weight: torch.Tensor, w_s
     _call("forge_int8_depthwise_conv2d_forward", _p(input), _p(weight), _p(w_scale), _p(bias), _p(out), N, C, H, W,
           kH, kW, pad[0], pad[1], stride[0], stride[1], dil[0], dil[1], _stream())
     return out
+
+
+# ---- weight preparation ------------------------------------------------------------
+
+def _weight_arg(w: torch.Tensor):
+    if w.dtype not in (torch.float32, torch.float16):
+        raise TypeError(f"weight must be float32 or float16, got {w.dtype}")
+    if not w.is_cuda or not w.is_contiguous() or w.dim() != 2:
+        raise ValueError("weight must be a contiguous 2-D device tensor")
+    return 1 if w.dtype == torch.float16 else 0
+
+
+def quantize_weight_rows(w: torch.Tensor, w_int8: Optional[torch.Tensor] = None,
+                         w_scale: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """QuantizedLinear.quantize_weight (linear.py:168-173) on the device: (N, K) fp32/fp16 ->
+    (w_int8 (N, K) int8, w_scale (N,) fp16)."""
+    f16 = _weight_arg(w)
+    N, K = w.shape
+    if w_int8 is None:
+        w_int8 = torch.empty((N, K), dtype=torch.int8, device=w.device)
+    if w_scale is None:
+        w_scale = torch.empty((N,), dtype=torch.float16, device=w.device)
+    _need(w_int8, torch.int8, "w_int8", N * K)
+    _need(w_scale, torch.float16, "w_scale", N)
+    _call("forge_quantize_weight_rows", _p(w), f16, _p(w_int8), _p(w_scale), N, K, _stream())
+    return w_int8, w_scale
+
+
+def prepare_sparse_weight(w: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """SparseLinear.from_dense_weight (linear.py:231-249) in one device pass: (N, K) fp32/fp16 ->
+    (W_comp (N, K/2) int8, w_meta (N, K/32) int32 in the gfx950 order, w_scale (N,) fp16)."""
+    f16 = _weight_arg(w)
+    N, K = w.shape
+    comp = torch.empty((N, K // 2), dtype=torch.int8, device=w.device)
+    meta = torch.empty((N, K // 32), dtype=torch.int32, device=w.device)
+    scale = torch.empty((N,), dtype=torch.float16, device=w.device)
+    _call("forge_prepare_sparse_weight", _p(w), f16, _p(comp), _p(meta), _p(scale), N, K, _stream())
+    return comp, meta, scale

@@ -170,6 +170,24 @@ int forge_sparse_int8_linear(const uint16_t* x, const int8_t* W_comp, const uint
 int forge_splitk_reduce(const float* workspace, const uint16_t* bias, uint16_t* out,
                         int M, int N_out, void* stream);
 
+/* ---- weight preparation ------------------------------------------------------------- */
+
+/* Extension: the reference quantizes weights with torch float32 ops in Python
+ * (python/forge/nn/linear.py:168-173, QuantizedLinear.quantize_weight); this is that
+ * computation as one device pass: per row scale = max(amax|w|, 1e-8) / 127 (fp32),
+ * w_int8 = clamp(round_half_even(w / scale), -127, 127), w_scale = fp16(scale).
+ * w: (N, K) row-major fp32, or fp16 when w_fp16 != 0 (widened exactly, as .to(float32) does). */
+int forge_quantize_weight_rows(const void* w, int w_fp16, int8_t* w_int8, uint16_t* w_scale,
+                               int N, int K, void* stream);
+
+/* Extension: SparseLinear.from_dense_weight (python/forge/nn/linear.py:231-249) in one device
+ * pass: the quantization above, then 2:4 prune + compress (forge_prune_compress_24's rule) and
+ * the index words in the gfx950 layout (forge_pack_metadata's), with no dense INT8 or raw-nibble
+ * buffer. W_comp (N, K/2) int8, w_meta (N*K/32) uint32, w_scale (N) fp16.
+ * K % 32 == 0; w and W_comp 16-byte aligned. */
+int forge_prepare_sparse_weight(const void* w, int w_fp16, int8_t* W_comp, uint32_t* w_meta,
+                                uint16_t* w_scale, int N, int K, void* stream);
+
 /* ---- INT8 conv2d ------------------------------------------------------------------- */
 
 /* Replaces forge::nn::int8_conv2d_workspace_size (include/forge/nn/int8_conv2d.cuh:23-29). */

@@ -323,6 +323,32 @@ void orc_conv2d_nhwc_s32(const int8_t* x, const int8_t* w, int32_t* out,
 }
 
 /* ------------------------------------------------------------------------- */
+/* Per-row symmetric weight quantization, python/forge/nn/linear.py:168-173    */
+/* and :235-238 (torch float32 ops): scale = clamp(amax|w|, min=1e-8) / 127,   */
+/* q = clamp(round(w / scale), -127, 127) with IEEE division and round half    */
+/* to even, stored scale = scale.to(float16) (RNE). w is fp32 (the reference   */
+/* converts any input to float32 first). Finite weights only: torch's amax and */
+/* clamp propagate NaN and its float->int8 conversion of NaN is unspecified.   */
+/* ------------------------------------------------------------------------- */
+
+void orc_quantize_weight_rows(const float* w, int8_t* q, uint16_t* scale16, float* scale32, int N, int K)
+{
+    for (int n = 0; n < N; n++) {
+        const float* row = w + (size_t)n * K;
+        float amax = 0.0f;
+        for (int k = 0; k < K; k++) amax = fmaxf(amax, fabsf(row[k]));
+        const float scale = fmaxf(amax, 1e-8f) / 127.0f;
+        for (int k = 0; k < K; k++) {
+            float r = rintf(row[k] / scale);
+            r = fminf(fmaxf(r, -127.0f), 127.0f);
+            q[(size_t)n * K + k] = (int8_t)r;
+        }
+        if (scale16) scale16[n] = orc_f32_to_f16(scale);
+        if (scale32) scale32[n] = scale;
+    }
+}
+
+/* ------------------------------------------------------------------------- */
 /* INT8 depthwise conv2d, NCHW FP16 in and out                               */
 /* src/nn/int8_depthwise_conv2d.cu:25-70: per output, taps in (kh, kw) order, */
 /* out-of-image taps skipped, w = (float)q * scale (one rounded product),     */

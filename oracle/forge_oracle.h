@@ -24,6 +24,9 @@
  *   orc_sparse_gemm_s32               dense GEMM of the decompressed weights == dense GEMM of the
  *                                     pruned weights (numpy)
  *   orc_conv2d_nhwc_s32               torch.nn.functional.conv2d in float64 (exact for these ints)
+ *   orc_quantize_weight_rows          the reference's own torch float32 expression run on the CPU
+ *                                     (bit-identical), closed forms (|q| max 127 at the absmax,
+ *                                     zero row, the -127 clamp)
  *   orc_depthwise_conv2d              torch conv2d (groups = C) in float64 on the dequantized weights
  *                                     (<= 1 fp16 ulp + fp32 sum error); 1x1 kernels as one rounded
  *                                     product; the reference test's three shapes at its tolerance
@@ -72,6 +75,7 @@ void orc_conv2d_nhwc_s32(const int8_t* x, const int8_t* w, int32_t* out,
                          int N, int H, int W, int C, int Co, int kH, int kW,
                          int padH, int padW, int strideH, int strideW, int dilH, int dilW);
 
+void orc_quantize_weight_rows(const float* w, int8_t* q, uint16_t* scale16, float* scale32, int N, int K);
 void orc_depthwise_conv2d(const uint16_t* in, const int8_t* w, const uint16_t* w_scale,
                           const uint16_t* bias, uint16_t* out, int N, int C, int H, int W,
                           int kH, int kW, int padH, int padW, int strideH, int strideW,

@@ -57,6 +57,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_conv_out_size.restype = _I
     L.orc_conv2d_nhwc_s32.argtypes = [_P, _P, _P] + [_I] * 13
     L.orc_depthwise_conv2d.argtypes = [_P] * 5 + [_I] * 12
+    L.orc_quantize_weight_rows.argtypes = [_P] * 4 + [_I] * 2
     L.orc_conv_transpose2d_k2s2.argtypes = [_P] * 6 + [_I] * 5
     L.orc_mt19937_seed.argtypes = [_P, ctypes.c_uint32]
     L.orc_mt19937_next.argtypes = [_P]
@@ -197,6 +198,28 @@ def conv2d_nhwc_s32(x, w, pad=(0, 0), stride=(1, 1), dil=(1, 1)):
     lib().orc_conv2d_nhwc_s32(_p(x), _p(w), _p(out), N, H, W, C, Co, kH, kW,
                               pad[0], pad[1], stride[0], stride[1], dil[0], dil[1])
     return out
+
+
+def quantize_weight_rows(w):
+    """w (N, K) float (converted to fp32 as the reference does) -> (q int8 (N, K),
+    scale fp16 (N,), scale fp32 (N,))."""
+    w = np.ascontiguousarray(w, np.float32)
+    N, K = w.shape
+    q = np.empty((N, K), np.int8)
+    s16 = np.empty(N, np.uint16)
+    s32 = np.empty(N, np.float32)
+    lib().orc_quantize_weight_rows(_p(w), _p(q), _p(s16), _p(s32), N, K)
+    return q, s16.view(np.float16), s32
+
+
+def prepare_sparse_weight(w):
+    """SparseLinear.from_dense_weight (linear.py:231-249): quantize rows, prune 2:4, compress,
+    pack the index words in the gfx950 layout. -> (W_comp (N, K/2) int8, w_meta (N*K/32,)
+    uint32, w_scale fp16 (N,))."""
+    q, s16, _ = quantize_weight_rows(w)
+    N, K = q.shape
+    comp, raw = prune_compress_24(q)
+    return comp, pack_metadata_gfx950(raw, N, K), s16
 
 
 def depthwise_conv2d(x16, w, w_scale16, bias16=None, pad=(0, 0), stride=(1, 1), dil=(1, 1)):

@@ -32,7 +32,8 @@ def test_header_declares_the_path():
               "forge_sparse_int8_gemm_plan", "forge_prune_compress_24", "forge_pack_metadata",
               "forge_splitk_reduce", "forge_int8_conv2d_forward", "forge_int8_conv2d_workspace_size",
               "forge_int8_conv_transpose2d_k2s2_forward", "forge_int8_conv_transpose2d_k2s2_workspace_size",
-              "forge_int8_depthwise_conv2d_forward"]:
+              "forge_int8_depthwise_conv2d_forward", "forge_quantize_weight_rows",
+              "forge_prepare_sparse_weight"]:
         assert s in syms
 
 
@@ -102,6 +103,14 @@ def test_conv_workspace_size(lib):
     up = lambda b: (b + 255) // 256 * 256
     assert n == up(M * K * 2) + up(M * K) + up(M * 4) + up(M * 16 * 2)
     assert n >= M * K * 2 + M * K + M * 4 + M * 16 * 2     # at least the reference's size
+
+
+def test_weight_prep_argument_checks(lib):
+    fake = ctypes.c_void_p(4096)   # never dereferenced: validation fails first
+    assert lib.forge_prepare_sparse_weight(fake, 0, fake, fake, fake, 4, 48, None) == -1      # K % 32
+    assert lib.forge_prepare_sparse_weight(ctypes.c_void_p(4100), 0, fake, fake, fake, 4, 64, None) == -1
+    assert lib.forge_quantize_weight_rows(fake, 0, None, fake, 4, 64, None) == -1
+    assert lib.forge_quantize_weight_rows(None, 0, None, None, 0, 64, None) == 0
 
 
 def test_conv_transpose_workspace_size(lib):

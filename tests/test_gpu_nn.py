@@ -14,9 +14,11 @@ pytestmark = pytest.mark.gpu
 
 
 def _np_weight_quant(w32):
-    scale = np.maximum(np.abs(w32).max(axis=1), np.float32(1e-8)) / np.float32(127.0)
-    q = np.clip(np.rint(w32 / scale[:, None]), -127, 127).astype(np.int8)
-    return q, scale.astype(np.float16)
+    """The oracle's restatement of linear.py:168-173 (pinned to the reference's torch
+    expression in test_oracle.py)."""
+    from oracle import oracle
+    q, s16, _ = oracle.quantize_weight_rows(w32)
+    return q, s16
 
 
 @pytest.mark.parametrize("M,K,N,bias", [(7, 256, 96, True), (64, 1024, 320, False), (300, 512, 200, True)])

@@ -429,3 +429,58 @@ def test_conv_transpose_bias_after_rounding(orc):
     y1 = orc.conv_transpose2d_k2s2(x, w, ws, b)
     want = (y0.astype(np.float32) + b.astype(np.float32)[None, :, None, None]).astype(np.float16)
     assert np.array_equal(y1.view(np.uint16), want.view(np.uint16))
+
+
+# ---- weight quantization (python/forge/nn/linear.py:168-173, :235-238) --------------
+
+def _torch_weight_quant(w):
+    """The reference's own expression (linear.py:168-173), run by torch on the CPU."""
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(w)).to(torch.float32)
+    scale = t.abs().amax(dim=1).clamp(min=1e-8) / 127.0
+    q = (t / scale.unsqueeze(1)).round().clamp(-127, 127).to(torch.int8)
+    return q.numpy(), scale.to(torch.float16).numpy(), scale.numpy()
+
+
+@pytest.mark.parametrize("N,K,dist", [(64, 256, "normal"), (33, 100, "uniform"), (8, 4096, "outlier"),
+                                      (5, 7, "normal")])
+def test_weight_quant_matches_reference_expression(orc, N, K, dist):
+    rng = np.random.default_rng(N + K)
+    if dist == "normal":
+        w = rng.standard_normal((N, K)).astype(np.float32) * 0.02
+    elif dist == "uniform":
+        w = rng.uniform(-3, 3, (N, K)).astype(np.float32)
+    else:
+        w = rng.standard_normal((N, K)).astype(np.float32)
+        w[:, rng.choice(K, 4, replace=False)] *= 50
+    q, s16, s32 = orc.quantize_weight_rows(w)
+    tq, ts16, ts32 = _torch_weight_quant(w)
+    assert np.array_equal(q, tq)
+    assert np.array_equal(s16.view(np.uint16), ts16.view(np.uint16))
+    assert np.array_equal(s32.view(np.uint32), ts32.view(np.uint32))
+
+
+def test_weight_quant_closed_forms(orc):
+    # the absmax element maps to +-127; a zero row gets scale 1e-8/127 and q = 0; half-way
+    # quotients round to even (w = 2.5 * scale with scale = 1 -> 2).
+    w = np.array([[0.5, -1.0, 0.25, 0.0], [0, 0, 0, 0], [127.0, 2.5, -3.5, 0.5]], np.float32)
+    q, s16, s32 = orc.quantize_weight_rows(w)
+    assert q[0, 1] == -127 and q[0, 0] == 64 and q[0, 2] == 32       # 63.5 -> 64, 31.75 -> 32
+    assert s32[1] == np.float32(np.float32(1e-8) / np.float32(127)) and not q[1].any()
+    assert s32[2] == 1.0 and list(q[2]) == [127, 2, -4, 0]           # RNE: 2.5 -> 2, -3.5 -> -4, 0.5 -> 0
+
+
+def test_sparse_weight_prep_is_the_composition(orc):
+    """prepare_sparse_weight == quantize rows, then the (separately pinned) prune + gfx950 pack;
+    decompressing gives the 2:4-pruned quantized weights."""
+    rng = np.random.default_rng(11)
+    w = rng.standard_normal((48, 256)).astype(np.float32)
+    comp, meta, s16 = orc.prepare_sparse_weight(w)
+    q, s16b, _ = orc.quantize_weight_rows(w)
+    assert np.array_equal(s16.view(np.uint16), s16b.view(np.uint16))
+    raw = orc.unpack_metadata_gfx950(meta, 48, 256)
+    d = orc.decompress_24(comp, raw, 48, 256).reshape(48, 64, 4)
+    qg = q.reshape(48, 64, 4)
+    kept = d != 0
+    assert np.all(kept.sum(axis=2) <= 2)
+    assert np.array_equal(d[kept], qg[kept])
