@@ -309,10 +309,11 @@ __global__ __launch_bounds__(256) void depthwise_rows_kernel(
                 for (int j = 0; j < 8; j++) h[j] = f2h(has_bias ? acc[0][j] + bv : acc[0][j]);
                 uint16_t* dst = yp + static_cast<size_t>(o) * Wo + wo0;
                 if (vec_out && wo0 + 8 <= Wo) {
-                    *reinterpret_cast<uint4*>(dst) = make_uint4(h[0] | (static_cast<uint32_t>(h[1]) << 16),
-                                                                h[2] | (static_cast<uint32_t>(h[3]) << 16),
-                                                                h[4] | (static_cast<uint32_t>(h[5]) << 16),
-                                                                h[6] | (static_cast<uint32_t>(h[7]) << 16));
+                    const v4i o4 = v4i{static_cast<int>(h[0] | (static_cast<uint32_t>(h[1]) << 16)),
+                                       static_cast<int>(h[2] | (static_cast<uint32_t>(h[3]) << 16)),
+                                       static_cast<int>(h[4] | (static_cast<uint32_t>(h[5]) << 16)),
+                                       static_cast<int>(h[6] | (static_cast<uint32_t>(h[7]) << 16))};
+                    __builtin_nontemporal_store(o4, reinterpret_cast<v4i*>(dst));
                 } else {
 #pragma unroll
                     for (int j = 0; j < 8; j++)
