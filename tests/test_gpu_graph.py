@@ -128,3 +128,26 @@ def test_graph_conv_special(dev):
              lambda: ops.int8_depthwise_conv2d_forward(x, w, ws, b, 3, 3, (1, 1), (2, 2), out=y2),
              lambda: ops.int8_conv_transpose2d_k2s2_forward(x, wt, wts, bt, workspace=wsp, out=y3)]
     _replay_check(dev, calls, [y1, y2, y3])
+
+
+def test_graph_weight_prep(dev):
+    """The one-pass sparse weight preparation and the dense weight quantizer."""
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(25)
+    w = to_dev((rng.standard_normal((96, 512)) * 0.05).astype(np.float32), dev)
+    comp = torch.empty((96, 256), dtype=torch.int8, device=dev)
+    meta = torch.empty((96, 16), dtype=torch.int32, device=dev)
+    sc = torch.empty((96,), dtype=torch.float16, device=dev)
+    q = torch.empty((96, 512), dtype=torch.int8, device=dev)
+    qs = torch.empty((96,), dtype=torch.float16, device=dev)
+
+    def prep():
+        c, m, s = ops.prepare_sparse_weight(w)
+        comp.copy_(c)
+        meta.copy_(m)
+        sc.copy_(s)
+
+    say("graph weight prep")
+    calls = [prep, lambda: ops.quantize_weight_rows(w, q, qs)]
+    _replay_check(dev, calls, [comp, meta, sc, q, qs])
