@@ -18,6 +18,7 @@
 #include "forge_oracle.h"
 
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 #include <time.h>
@@ -471,6 +472,51 @@ uint32_t orc_mt19937_next(orc_mt19937_t* s)
 /* CPU baseline timing: the host INT32 loop plus the dequant epilogue over a  */
 /* slice of rows, single-threaded. Returns seconds.                           */
 /* ------------------------------------------------------------------------- */
+
+/* The same work split over output rows on `threads` POSIX threads (the multi-core CPU
+ * baseline: each thread runs the INT32 loop and the epilogue on a contiguous row range). */
+typedef struct {
+    const int8_t *A, *B;
+    const float* act_scale;
+    const uint16_t *w_scale, *bias;
+    uint16_t* out;
+    int32_t* acc;
+    int r0, r1, K, N;
+} orc_rows_job;
+
+static void* orc_rows_worker(void* p)
+{
+    const orc_rows_job* j = (const orc_rows_job*)p;
+    if (j->r1 > j->r0) {
+        orc_gemm_s32_rows(j->A, j->B, j->acc, j->r0, j->r1, j->K, j->N);
+        orc_dequant_epilogue(j->acc + (size_t)j->r0 * j->N, j->act_scale + j->r0, j->w_scale, j->bias,
+                             j->out + (size_t)j->r0 * j->N, j->r1 - j->r0, j->N);
+    }
+    return NULL;
+}
+
+double orc_time_gemm_dequant_rows_mt(const int8_t* A, const int8_t* B, const float* act_scale,
+                                     const uint16_t* w_scale, const uint16_t* bias, uint16_t* out,
+                                     int rows, int K, int N, int threads)
+{
+    if (threads < 1) threads = 1;
+    if (threads > 256) threads = 256;
+    struct timespec t0, t1;
+    int32_t* acc = (int32_t*)malloc((size_t)rows * N * sizeof(int32_t));
+    pthread_t tid[256];
+    orc_rows_job jobs[256];
+    clock_gettime(CLOCK_MONOTONIC, &t0);
+    for (int t = 0; t < threads; t++) {
+        const orc_rows_job j = {A, B, act_scale, w_scale, bias, out, acc,
+                                (int)((long long)rows * t / threads), (int)((long long)rows * (t + 1) / threads), K, N};
+        jobs[t] = j;
+        pthread_create(&tid[t], NULL, orc_rows_worker, &jobs[t]);
+    }
+    for (int t = 0; t < threads; t++) pthread_join(tid[t], NULL);
+    clock_gettime(CLOCK_MONOTONIC, &t1);
+    free(acc);
+    return (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
+}
 
 double orc_time_gemm_dequant_rows(const int8_t* A, const int8_t* B, const float* act_scale,
                                   const uint16_t* w_scale, const uint16_t* bias, uint16_t* out,

@@ -88,6 +88,9 @@ typedef struct { uint32_t mt[624]; int idx; } orc_mt19937_t;
 void     orc_mt19937_seed(orc_mt19937_t* s, uint32_t seed);
 uint32_t orc_mt19937_next(orc_mt19937_t* s);
 
+double orc_time_gemm_dequant_rows_mt(const int8_t* A, const int8_t* B, const float* act_scale,
+                                     const uint16_t* w_scale, const uint16_t* bias, uint16_t* out,
+                                     int rows, int K, int N, int threads);
 double orc_time_gemm_dequant_rows(const int8_t* A, const int8_t* B, const float* act_scale,
                                   const uint16_t* w_scale, const uint16_t* bias, uint16_t* out,
                                   int rows, int K, int N);

@@ -64,6 +64,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_mt19937_next.restype = ctypes.c_uint32
     L.orc_time_gemm_dequant_rows.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I]
     L.orc_time_gemm_dequant_rows.restype = ctypes.c_double
+    L.orc_time_gemm_dequant_rows_mt.argtypes = [_P] * 6 + [_I] * 4
+    L.orc_time_gemm_dequant_rows_mt.restype = ctypes.c_double
 
 
 def _p(a):
@@ -261,6 +263,20 @@ def mt19937(seed: int, count: int) -> np.ndarray:
     L.orc_mt19937_seed(ctypes.addressof(state), seed)
     return np.array([L.orc_mt19937_next(ctypes.addressof(state)) for _ in range(count)],
                     dtype=np.uint32)
+
+
+def time_gemm_dequant_rows_mt(A, B, act_scale, w_scale16, bias16, rows, threads):
+    """time_gemm_dequant_rows split over output rows on `threads` POSIX threads."""
+    A = np.ascontiguousarray(A, np.int8)
+    B = np.ascontiguousarray(B, np.int8)
+    K = A.shape[1]
+    N = B.shape[0]
+    as_ = np.ascontiguousarray(act_scale, np.float32)
+    ws = _u16(w_scale16)
+    b = None if bias16 is None else _u16(bias16)
+    out = np.empty((rows, N), np.uint16)
+    secs = lib().orc_time_gemm_dequant_rows_mt(_p(A), _p(B), _p(as_), _p(ws), _p(b), _p(out), rows, K, N, threads)
+    return secs, out.view(np.float16)
 
 
 def time_gemm_dequant_rows(A, B, act_scale, w_scale16, bias16, rows):
