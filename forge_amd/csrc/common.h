@@ -74,6 +74,97 @@ __device__ __forceinline__ int quant1(float x, float inv) {
     return q;
 }
 
+// 8 halves (one uint4) -> 8 int8 packed into a uint2.
+__device__ __forceinline__ uint2 quant8(uint4 v, float inv) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t out[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int q0 = quant1(h2f(static_cast<uint16_t>(w[j] & 0xFFFFu)), inv);
+        const int q1 = quant1(h2f(static_cast<uint16_t>(w[j] >> 16)), inv);
+        out[j >> 1] |= ((static_cast<uint32_t>(q0) & 0xFFu) << (16 * (j & 1))) |
+                       ((static_cast<uint32_t>(q1) & 0xFFu) << (16 * (j & 1) + 8));
+    }
+    return make_uint2(out[0], out[1]);
+}
+
+__device__ __forceinline__ float absmax8(uint4 v, float m) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        m = fmaxf(m, fabsf(h2f(static_cast<uint16_t>(w[j] & 0xFFFFu))));
+        m = fmaxf(m, fabsf(h2f(static_cast<uint16_t>(w[j] >> 16))));
+    }
+    return m;
+}
+
+// ---- row quantization on fp16 bit patterns (the same results as absmax8/quant8) -------
+// With the sign bit cleared, fp16 bit patterns order exactly as their magnitudes (zero,
+// subnormals, normals, inf), so the row absmax is a packed u16 maximum, one v_pk_max_u16 per
+// two values. NaN patterns (above 0x7C00) sort above inf; a row whose maximum is one holds a
+// NaN and takes the fp32 maximum instead, which skips NaN as fmaxf does.
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+    typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(us2, a),
+                                                                  __builtin_bit_cast(us2, b)));
+}
+__device__ __forceinline__ uint32_t absbits8(uint4 v, uint32_t m) {
+    m = pk_max_u16(m, v.x & 0x7FFF7FFFu);
+    m = pk_max_u16(m, v.y & 0x7FFF7FFFu);
+    m = pk_max_u16(m, v.z & 0x7FFF7FFFu);
+    return pk_max_u16(m, v.w & 0x7FFF7FFFu);
+}
+// Two rows' packed maxima (lo, hi halves each) -> (max of row a, max of row b).
+__device__ __forceinline__ uint32_t pk_rows2(uint32_t a, uint32_t b) {
+    return pk_max_u16(__builtin_amdgcn_perm(b, a, 0x05040100u), __builtin_amdgcn_perm(b, a, 0x07060302u));
+}
+// Wave-wide packed u16 maximum by DPP (no LDS traffic): quad swaps and row rotations give
+// every lane its 16-lane row's maximum, row_bcast:15/31 fold the four rows into lane 63, whose
+// value is returned to all lanes. Needs all 64 lanes active.
+__device__ __forceinline__ uint32_t wave_max_pk_u16(uint32_t v) {
+    const int x = static_cast<int>(v);
+    v = pk_max_u16(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false)));
+    int y = static_cast<int>(v);
+    v = pk_max_u16(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(y, y, 0x4E, 0xF, 0xF, false)));
+    y = static_cast<int>(v);
+    v = pk_max_u16(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(y, y, 0x124, 0xF, 0xF, false)));
+    y = static_cast<int>(v);
+    v = pk_max_u16(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(y, y, 0x128, 0xF, 0xF, false)));
+    y = static_cast<int>(v);
+    v = pk_max_u16(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(y, y, 0x142, 0xA, 0xF, false)));
+    y = static_cast<int>(v);
+    v = pk_max_u16(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(y, y, 0x143, 0xC, 0xF, false)));
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+constexpr uint32_t kHalfInfBits = 0x7C00u;
+
+// One value of a row quantized with inv = 1 / row_scale(absmax of that row), as the byte of
+// clamp(rne(x * inv), -128, 127). |x| <= absmax bounds |x * inv| by 127 plus a few ulp, so the
+// clamp acts only on NaN (x NaN, or an inf row's inf * 0): fl(x * inv) + 1.5 * 2^23 rounds
+// the product to an integer held in the low mantissa bits (round to nearest even, as rintf,
+// for |v| < 2^22), whose low byte is the two's complement int8; a NaN's low byte is 0 (fp16
+// NaN payloads land 13 bits up; the default NaN is 0x7FC00000). The asm keeps the product
+// rounded on its own (a fused multiply-add would round once).
+__device__ __forceinline__ uint32_t qrow_bits(uint16_t h, float inv) {
+    float p = h2f(h) * inv;
+    asm("" : "+v"(p));
+    return __float_as_uint(p + 12582912.0f);
+}
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+    return __builtin_amdgcn_perm(b1, b0, 0x0C0C0400u) | __builtin_amdgcn_perm(b3, b2, 0x04000C0Cu);
+}
+// 8 halves of a row -> 8 int8, equal to quant8(v, inv) when inv comes from the row's absmax.
+__device__ __forceinline__ uint2 quant8_row(uint4 v, float inv) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t b[8];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        b[2 * j] = qrow_bits(static_cast<uint16_t>(w[j] & 0xFFFFu), inv);
+        b[2 * j + 1] = qrow_bits(static_cast<uint16_t>(w[j] >> 16), inv);
+    }
+    return make_uint2(pack_low_bytes(b[0], b[1], b[2], b[3]), pack_low_bytes(b[4], b[5], b[6], b[7]));
+}
+
 // GEMM dequant epilogue: half(fma((float)acc, as*ws, bias)), or acc*(as*ws) without bias.
 __device__ __forceinline__ uint16_t dequant_gemm(int acc, float as, float ws, float b, bool has_bias) {
     const float s = as * ws;

@@ -6,113 +6,112 @@
 //   q[m,k]   = clamp(rne(x[m,k] * (1.0f / scale[m])), -128, 127)
 //
 // MI355X design: the main kernel gives each row to one 256-thread workgroup (short rows at
-// large M: one wavefront per row, 4 rows per workgroup). A lane holds
-// VPT 16-byte vectors of its row in VGPRs, so x is read from HBM once; the row absmax is a
-// 64-lane butterfly per wave plus a 4-entry LDS max, then each lane writes 8 int8 per
-// vector. The exported two-pass kernel (any K, any alignment, any
-// block size) reduces through LDS; both compute the same max (exact) and the same
-// IEEE-rounded arithmetic, so their outputs are bit-identical.
+// large M: one wavefront per row, 4 rows per workgroup). A lane holds VPT 16-byte vectors of
+// its row in VGPRs, so x is read from HBM once; the row absmax is a packed u16 maximum of the
+// fp16 magnitude bit patterns reduced across the wave by DPP (plus a 4-entry LDS max), with
+// the fp32 maximum for a row that holds a NaN; then each lane writes 8 int8 per vector. The
+// exported two-pass kernel (any K, any alignment, any block size) reduces through LDS in
+// fp32. All compute the same max (exact) and the same IEEE-rounded arithmetic, so their
+// outputs are bit-identical.
 #include "common.h"
 #include "forge/quant/quantize.h"
 #include "forge/quant/dequantize.h"
 
 namespace forge_amd {
 
-// 8 halves (one uint4) -> 8 int8 packed into a uint2.
-__device__ __forceinline__ uint2 quant8(uint4 v, float inv) {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    uint32_t out[2] = {0u, 0u};
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int q0 = quant1(h2f(static_cast<uint16_t>(w[j] & 0xFFFFu)), inv);
-        const int q1 = quant1(h2f(static_cast<uint16_t>(w[j] >> 16)), inv);
-        out[j >> 1] |= ((static_cast<uint32_t>(q0) & 0xFFu) << (16 * (j & 1))) |
-                       ((static_cast<uint32_t>(q1) & 0xFFu) << (16 * (j & 1) + 8));
-    }
-    return make_uint2(out[0], out[1]);
-}
-
-__device__ __forceinline__ float absmax8(uint4 v, float m) {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        m = fmaxf(m, fabsf(h2f(static_cast<uint16_t>(w[j] & 0xFFFFu))));
-        m = fmaxf(m, fabsf(h2f(static_cast<uint16_t>(w[j] >> 16))));
-    }
-    return m;
-}
-
 // One 256-thread workgroup per row; K % 8 == 0, K <= VPT * 2048, x 16-byte and q 8-byte
 // aligned. Thread t holds 16-byte vectors t, t + 256, ... of its row in VGPRs (x is read
-// once), the row absmax is a 64-lane butterfly per wave then a 4-entry LDS max, and every
-// lane writes 8 int8 per vector. Spreading a row over 4 waves keeps decode-size calls (a
-// handful of rows) from serialising one wave's loads.
+// once) and every lane writes 8 int8 per vector. Spreading a row over 4 waves keeps
+// decode-size calls (a handful of rows) from serialising one wave's loads.
+//
+// All of a lane's loads are issued before any is used, unconditionally: a lane past the row
+// end re-reads the row's last vector, which cannot change a maximum (a load inside
+// `if (idx < nvec)` next to its use compiled to load -> wait -> use, one memory latency per
+// vector). The absmax runs on fp16 bit patterns (absbits8: one packed u16 max per two values,
+// DPP across the wave, 4 entries through LDS); a row holding a NaN takes the fp32 maximum,
+// which skips NaN as fmaxf does. Values are quantized by quant8_row, bit-equal to quant8
+// for a row's own scale.
 template <int VPT>
 __global__ __launch_bounds__(256) void quantize_rows_block_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scales, int K)
 {
+    __shared__ uint32_t wbits[4];
     __shared__ float wmax[4];
     const int row = blockIdx.x;
-    const int t = threadIdx.x;
+    const int t = threadIdx.x, lane = t & (kWave - 1), wave = t / kWave;
     const int nvec = K >> 3;
     const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<size_t>(row) * K);
     uint2* dst = reinterpret_cast<uint2*>(q + static_cast<size_t>(row) * K);
     uint4 v[VPT];
-    float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < VPT; i++) {
-        const int idx = t + i * 256;
-        if (idx < nvec) {
-            v[i] = src[idx];
-            amax = absmax8(v[i], amax);
-        }
-    }
-    amax = wave_max(amax);
-    if ((t & (kWave - 1)) == 0) wmax[t / kWave] = amax;
+    for (int i = 0; i < VPT; i++) v[i] = src[min(t + i * 256, nvec - 1)];
+    uint32_t m = 0u;
+#pragma unroll
+    for (int i = 0; i < VPT; i++) m = absbits8(v[i], m);
+    m = wave_max_pk_u16(pk_max_u16(m, m >> 16)) & 0xFFFFu;
+    if (lane == 0) wbits[wave] = m;
     __syncthreads();
-    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const uint32_t bits = max(max(wbits[0], wbits[1]), max(wbits[2], wbits[3]));
+    float amax;
+    if (bits > kHalfInfBits) {               // the row holds a NaN (uniform over the workgroup)
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < VPT; i++) a = absmax8(v[i], a);
+        a = wave_max(a);
+        if (lane == 0) wmax[wave] = a;
+        __syncthreads();
+        amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    } else {
+        amax = h2f(static_cast<uint16_t>(bits));
+    }
     const float scale = row_scale(amax);
     const float inv = 1.0f / scale;
     if (t == 0) scales[row] = scale;
 #pragma unroll
     for (int i = 0; i < VPT; i++) {
         const int idx = t + i * 256;
-        if (idx < nvec) dst[idx] = quant8(v[i], inv);
+        if (idx < nvec) dst[idx] = quant8_row(v[i], inv);
     }
 }
 
 // Short rows (K <= 2048) at large M: one wavefront per row, 4 rows per workgroup, so a
 // workgroup moves 4 rows and the grid is M/4 workgroups instead of M tiny ones (at
 // M = 147,456, K = 1280 the per-row workgroups ran at 3.6 TB/s). Lane t holds vectors t, t + 64,
-// ... of its row; the absmax is a 64-lane butterfly. Same arithmetic as the kernels above.
+// ... of its row; loads, absmax and quantization as in the kernel above, the absmax reduced
+// within the wave by DPP.
 template <int VPT>
 __global__ __launch_bounds__(256) void quantize_rows_wave_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ q, float* __restrict__ scales, int M, int K)
 {
     const int lane = threadIdx.x & (kWave - 1);
     const int row = blockIdx.x * 4 + static_cast<int>(threadIdx.x / kWave);
-    if (row >= M) return;
+    if (row >= M) return;                    // whole waves leave: the DPP reduction sees 64 lanes
     const int nvec = K >> 3;
     const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<size_t>(row) * K);
     uint2* dst = reinterpret_cast<uint2*>(q + static_cast<size_t>(row) * K);
     uint4 v[VPT];
-    float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < VPT; i++) {
-        const int idx = lane + i * kWave;
-        if (idx < nvec) {
-            v[i] = src[idx];
-            amax = absmax8(v[i], amax);
-        }
+    for (int i = 0; i < VPT; i++) v[i] = src[min(lane + i * kWave, nvec - 1)];
+    uint32_t m = 0u;
+#pragma unroll
+    for (int i = 0; i < VPT; i++) m = absbits8(v[i], m);
+    const uint32_t bits = wave_max_pk_u16(pk_max_u16(m, m >> 16)) & 0xFFFFu;
+    float amax;
+    if (bits > kHalfInfBits) {               // the row holds a NaN (uniform over the wave)
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < VPT; i++) a = absmax8(v[i], a);
+        amax = wave_max(a);
+    } else {
+        amax = h2f(static_cast<uint16_t>(bits));
     }
-    amax = wave_max(amax);
     const float scale = row_scale(amax);
     const float inv = 1.0f / scale;
     if (lane == 0) scales[row] = scale;
 #pragma unroll
     for (int i = 0; i < VPT; i++) {
         const int idx = lane + i * kWave;
-        if (idx < nvec) dst[idx] = quant8(v[i], inv);
+        if (idx < nvec) dst[idx] = quant8_row(v[i], inv);
     }
 }
 

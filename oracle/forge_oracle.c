@@ -85,7 +85,13 @@ void orc_quantize_rows(const uint16_t* x, int8_t* q, float* scales, int M, int K
     for (int m = 0; m < M; m++) {
         const uint16_t* row = x + (size_t)m * K;
         float amax = 0.0f;
-        for (int k = 0; k < K; k++) amax = fmaxf(amax, fabsf(orc_f16_to_f32(row[k])));
+        /* quantize.cu: amax = fmaxf(amax, fabsf(x)), run on the GPU, whose max returns the
+         * other operand for a NaN of either kind. C's fmaxf returns NaN when an operand is a
+         * signalling NaN (glibc follows IEEE 754-2008 maxNum), so the skip is written out. */
+        for (int k = 0; k < K; k++) {
+            const float a = fabsf(orc_f16_to_f32(row[k]));
+            if (a > amax) amax = a;
+        }
         const float scale = fmaxf(amax, 1e-8f) / 127.0f;          /* quantize.cu:49,112 */
         const float inv = 1.0f / scale;                            /* quantize.cu:51,114 */
         scales[m] = scale;

@@ -46,3 +46,35 @@ def poison(t, byte: int):
     """Fills a device tensor's bytes with a garbage pattern (the reference tests use 0x7B/0x5A)."""
     import torch
     t.view(torch.uint8).fill_(byte)
+
+
+def special_fp16_rows(rng, M, K, inf=True):
+    """fp16 rows for the quantizers' edge cases (bit patterns): NaNs with various payloads
+    (quiet, the signalling pattern, negative, all ones) among normal values, a row of NaNs, a
+    NaN where the row's largest magnitude would be, a row of subnormals with +-0, a row of
+    -0, exact ties after scaling (absmax 127 makes the scale 1: 2.5 -> 2, 3.5 -> 4, ...), the
+    fp16 maximum, and optionally +inf and -inf rows (scale inf, every value quantized to 0).
+    Special rows sit at the start and at the end of the matrix."""
+    x = (rng.standard_normal((M, K), dtype=np.float32)).astype(np.float16).view(np.uint16).copy()
+    nan_bits = np.array([0x7E00, 0x7C01, 0xFE00, 0x7D55, 0xFFFF], np.uint16)
+
+    def r(i):
+        return i % M if i >= 0 else (M + i) % M
+
+    n = min(K, 7)
+    x[r(0), rng.choice(K, n, replace=False)] = rng.choice(nan_bits, n)
+    x[r(1)] = rng.choice(np.array([0x0001, 0x8001, 0x03FF, 0x83FF, 0x0200, 0x8000, 0x0000], np.uint16), K)
+    x[r(2)] = 0x8000
+    ties = np.array([127.0, 2.5, 3.5, -2.5, 0.5, -0.5, 1.5, -126.5], np.float16).view(np.uint16)
+    x[r(3)] = 0
+    x[r(3), :min(K, 8)] = ties[:min(K, 8)]
+    x[r(4)] = np.float16(65504).view(np.uint16)
+    x[r(4), ::3] = np.float16(-65504).view(np.uint16)
+    big = int(np.argmax(np.abs(x[r(5)].view(np.float16).astype(np.float32))))
+    x[r(5), big] = 0x7E00
+    x[r(-1)] = 0x7E00
+    x[r(-2), rng.choice(K, n, replace=False)] = rng.choice(nan_bits, n)
+    if inf:
+        x[r(6), K // 2] = 0x7C00
+        x[r(-3), 0] = 0xFC00
+    return x.view(np.float16)

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 from conftest import golden
-from helpers import fp16_normal, poison, say, to_dev, to_host, ulp_diff16
+from helpers import fp16_normal, poison, say, special_fp16_rows, to_dev, to_host, ulp_diff16
 
 pytestmark = pytest.mark.gpu
 
@@ -78,6 +78,30 @@ def test_quantize_outlier_rows_and_ties(dev, orc):
     say("quantize outliers/ties")
     q, s = ops.fused_quantize_activation(to_dev(x, dev), M, K)
     assert np.array_equal(to_host(q), qr) and np.array_equal(to_host(s), sr)
+
+
+# Shapes reaching each kernel: block kernel VPT 1 / 2 / 8, wave kernel VPT 1 / 2 / 4 (ragged
+# last workgroup at 2050 rows), and the scalar kernel (K % 8 != 0).
+SPECIAL_CASES = [(9, 1024), (16, 4096), (4, 16384), (2050, 8), (2048, 1000), (2051, 2048), (6, 1003)]
+
+
+@pytest.mark.parametrize("M,K", SPECIAL_CASES)
+def test_quantize_special_values(dev, orc, M, K):
+    """NaN payloads, a NaN at the largest magnitude, NaN-only rows, subnormals, +-0, ties after
+    scaling, the fp16 maximum and +-inf rows: INT8 and scales bit-exact against the oracle
+    (which follows the reference's fmaxf, skipping NaN, and its NaN -> 0 conversion), for the
+    main kernels and the exported two-pass kernel."""
+    from forge_amd import ops
+    rng = np.random.default_rng(M * 7 + K)
+    x = special_fp16_rows(rng, M, K)
+    qr, sr = orc.quantize_rows(x)
+    say(f"quantize special values M={M} K={K}")
+    q, s = ops.fused_quantize_activation(to_dev(x, dev), M, K)
+    assert np.array_equal(to_host(s).view(np.uint32), sr.view(np.uint32))
+    assert np.array_equal(to_host(q), qr)
+    q2, s2 = ops.fused_quantize_activation_twopass(to_dev(x, dev), M, K, 256)
+    assert np.array_equal(to_host(s2).view(np.uint32), sr.view(np.uint32))
+    assert np.array_equal(to_host(q2), qr)
 
 
 def test_dequant_golden(dev, orc):

@@ -99,6 +99,30 @@ def test_quantize_matches_numpy_float32(orc):
     assert np.array_equal(s, sc) and np.array_equal(q, qr)
 
 
+def test_quantize_special_values_match_numpy(orc):
+    """NaN of every kind (quiet, signalling pattern, negative, payloads) is skipped by the
+    absmax, as the reference's GPU fmaxf does, and quantizes to 0; a NaN-only row has amax 0;
+    an inf row has scale inf and quantizes everything to 0 (x * 0, or inf * 0 = NaN -> 0);
+    subnormals, -0, ties and the fp16 maximum follow the float32 formula. Checked against
+    numpy's nanmax and float32 arithmetic, element by element."""
+    from helpers import special_fp16_rows
+    rng = np.random.default_rng(11)
+    for M, K in [(9, 64), (12, 1003), (16, 4096)]:
+        x = special_fp16_rows(rng, M, K)
+        q, s = orc.quantize_rows(x)
+        xf = x.astype(np.float32)
+        with np.errstate(invalid="ignore"):
+            a = np.abs(xf)
+            amax = np.where(np.isnan(a).all(axis=1), np.float32(0), np.nanmax(np.where(np.isnan(a), -1, a), axis=1))
+            sc = (np.maximum(amax.astype(np.float32), np.float32(1e-8)) / np.float32(127)).astype(np.float32)
+            inv = (np.float32(1) / sc).astype(np.float32)
+            v = np.rint((xf * inv[:, None]).astype(np.float32))
+        qr = np.where(np.isnan(v), 0, np.clip(np.nan_to_num(v, nan=0.0), -128, 127)).astype(np.int8)
+        assert np.array_equal(s.view(np.uint32), sc.view(np.uint32))
+        assert np.array_equal(q, qr)
+        assert np.isinf(s).any() and not q[np.isinf(s)].any()
+
+
 # ---- dequant ----------------------------------------------------------------------
 
 def _ulp_diff(a16, b16):
