@@ -32,6 +32,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 namespace forge_amd {
 
@@ -839,6 +840,373 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
     return sparse_launch(pt, p, s);
 }
 
+// ---- fused quantize + sparse linear (the reference's FQ path) ------------------------
+// src/gemm/int8_sparse.cu:250-335 (and :1022-1033): for narrow layers at large M the int8
+// copy of the activations costs a DRAM round trip (write M*K, read it back) that the fused
+// path avoids by quantizing each block of token rows on the chip. MI355X form: a persistent
+// 512-thread workgroup (2 waves per SIMD) with a double-buffered LDS token tile of BT rows:
+//   - producer waves 4..7 quantize tile t+1 (BT/4 rows each) into one buffer -- K/128 slabs
+//     of BT rows x 128 bytes in the two-pass engine's conflict-free B layout (sp_b_off) --
+//     and its row scales. kFqRowsInFlight rows form a batch whose 16-byte loads issue
+//     together, before the previous batch is quantized; the last batch of a tile fetches the
+//     first batch of the next, across the barrier. Row absmax on fp16 bit patterns (one
+//     packed u16 max per two values, DPP across the wave, two rows per reduction), values by
+//     quant8_row: the arithmetic of quantize_rows.
+//   - consumer waves 0..3 run tile t from the other buffer: each owns NBW consecutive 16-row
+//     weight blocks per pass, streams their compressed bytes and index words straight from
+//     L2 into registers (kFqAhead K steps ahead, in the SMFMAC lane layout), reads the
+//     step's 16-token B fragments from LDS once for all NBW blocks
+//     (v_smfmac_i32_16x16x128_i8, A = weights), and writes each lane's 4 consecutive outputs
+//     of one token row as one 8-byte store with the GEMM dequant epilogue (w_scale and bias
+//     staged in LDS once).
+// The two kinds of waves run separate loops with one LDS-only barrier per tile (so the
+// producer's prefetch stays in flight across it). A producer's quantize (VALU) and a
+// consumer's SMFMACs share every SIMD. The scratch buffers and the split-K workspace are not
+// touched (as in the reference). Every output equals the two-pass path's bits: same
+// quantization, exact INT32 sums, same epilogue. Measured at 147,456 x 1280 -> 320: 210 us
+// (two-pass 229); the consumer side bounds it -- weight-fragment loads (16 half cache lines
+// per instruction) and LDS reads with one consumer wave per SIMD keep the matrix core ~11 %
+// busy.
+constexpr int kFqMaxK = 2048;
+constexpr int kFqRowsInFlight = 4;   // token rows per producer wave whose loads are in flight together
+constexpr int kFqAhead = 3;          // K steps of weight fragments in flight per consumer wave
+constexpr int kFqLds = 160 * 1024;
+
+template <int NBW, int BT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void sparse_fq_kernel(
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ W_comp, const uint32_t* __restrict__ meta,
+    const uint16_t* __restrict__ w_scale, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
+    int M, int K, int N, int tiles)
+{
+    constexpr int kTB = BT / 16;                 // 16-token blocks per tile
+    constexpr int kRowsPerProducer = BT / 4;
+    static_assert(BT % 16 == 0 && kRowsPerProducer % kFqRowsInFlight == 0 && kFqRowsInFlight % 2 == 0,
+                  "tile rows must split evenly");
+    constexpr int kSlab = BT * kSpBRow;
+    extern __shared__ __align__(16) int8_t lds[];
+    const int tileBytes = BT * K;
+    float* sscale = reinterpret_cast<float*>(lds + 2 * tileBytes);          // [2][BT]
+    uint16_t* sws = reinterpret_cast<uint16_t*>(sscale + 2 * BT);          // N
+    uint16_t* sbias = sws + N;                                              // N
+    const int t = threadIdx.x, lane = t & (kWave - 1), wave = t >> 6;
+    const int KS = K / kSpStep, Kc = K / 2, cpr = K / 32, NB = N / 16;
+    const bool has_bias = bias != nullptr;
+    const int nvec = K / 8;
+    for (int n = t; n < N; n += 512) {
+        sws[n] = w_scale[n];
+        sbias[n] = has_bias ? bias[n] : static_cast<uint16_t>(0);
+    }
+
+    // Producer: rows pw*BT/4 .. +BT/4 of `tile` into buffer `buf`, kFqRowsInFlight rows per
+    // batch, the next batch's loads issued before this one is used. Loads are unconditional:
+    // lanes past the row end re-read its last vector (one coalesced request; a repeated value
+    // leaves the maximum unchanged), since a load inside `if (idx < nvec)` together with its
+    // use compiled to load -> wait -> use, one memory latency per vector.
+    constexpr int kR = kFqRowsInFlight;
+    constexpr int kBatches = kRowsPerProducer / kR;
+    auto load_batch = [&](int ln, int m0, int r0, uint4 (&v)[kR][4]) {
+#pragma unroll
+        for (int u = 0; u < kR; u++) {
+            const int row = min(m0 + r0 + u, M - 1);
+            const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<size_t>(row) * K);
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[u][i] = src[min(ln + kWave * i, nvec - 1)];
+        }
+    };
+    auto quantize_batch = [&](int ln, int r0, const uint4 (&v)[kR][4], int8_t* Xs, float* sc) {
+        uint32_t mb[kR];
+#pragma unroll
+        for (int u = 0; u < kR; u++) {
+            mb[u] = 0u;
+#pragma unroll
+            for (int i = 0; i < 4; i++) mb[u] = absbits8(v[u][i], mb[u]);
+        }
+        uint32_t abits[kR];
+#pragma unroll
+        for (int u = 0; u < kR; u += 2) {
+            const uint32_t r2 = wave_max_pk_u16(pk_rows2(mb[u], mb[u + 1]));
+            abits[u] = r2 & 0xFFFFu;
+            abits[u + 1] = r2 >> 16;
+        }
+#pragma unroll
+        for (int u = 0; u < kR; u++) {
+            float amax;
+            if (abits[u] > kHalfInfBits) {       // the row holds a NaN: fp32 max skipping it
+                float a = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; i++) a = absmax8(v[u][i], a);
+                amax = wave_max(a);
+            } else {
+                amax = h2f(static_cast<uint16_t>(abits[u]));
+            }
+            const int r = r0 + u;
+            const float scale = row_scale(amax);
+            const float inv = 1.0f / scale;
+            if (ln == 0) sc[r] = scale;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int idx = ln + kWave * i;
+                if (idx < nvec) {
+                    const int k = 8 * idx;
+                    *reinterpret_cast<uint2*>(Xs + (k >> 7) * kSlab + sp_b_off(r, (k >> 4) & 7) + (k & 8)) =
+                        quant8_row(v[u][i], inv);
+                }
+            }
+        }
+    };
+    // Producer tile: the first batch of `tile` is in v[E] on entry (loaded during the previous
+    // tile); the last batch's successor load fetches the first batch of tile `after` (a valid
+    // tile in any case) into v[(E + kBatches) & 1], so every batch's loads, a tile's first
+    // included, are in flight while the batch before it is quantized.
+    auto quantize_tile = [&](auto E, int tile, int buf, int after, int ln, int rp, uint4 (&v)[2][kR][4]) {
+        constexpr int e = decltype(E)::value;
+        asm volatile("" : "+v"(ln));             // re-made opaque per tile: nothing lane-derived is hoisted
+        int8_t* Xs = lds + buf * tileBytes;
+        float* sc = sscale + buf * BT;
+        const int m0 = tile * BT;
+#pragma unroll
+        for (int bt = 0; bt < kBatches; bt++) {
+            const int cur = (bt + e) & 1;
+            if (bt + 1 < kBatches) load_batch(ln, m0, rp + (bt + 1) * kR, v[cur ^ 1]);
+            else load_batch(ln, min(after, tiles - 1) * BT, rp, v[cur ^ 1]);
+            quantize_batch(ln, rp + bt * kR, v[cur], Xs, sc);
+        }
+    };
+
+    // Consumer wave cw: every output of `tile` from buffer `buf`. Workgroups walk K from
+    // different starting steps (integer sums do not depend on the order), so the CUs reading
+    // the same weight rows at the same time spread over different addresses.
+    auto compute_tile = [&](int tile, int buf, int cw) {
+        int ln = lane;                           // opaque, as in the producer
+        asm volatile("" : "+v"(ln));
+        const int r16 = ln & 15, g = ln >> 4;
+        const int8_t* Xs = lds + buf * tileBytes;
+        const float* sc = sscale + buf * BT;
+        const int m0 = tile * BT;
+        const int rot = (blockIdx.x + tile) % KS;
+        for (int p0 = 0; p0 < NB; p0 += 4 * NBW) {
+            const int wb0 = p0 + cw * NBW;
+            if (wb0 >= NB) continue;
+            v4i acc[NBW][kTB];
+#pragma unroll
+            for (int i = 0; i < NBW; i++)
+#pragma unroll
+                for (int j = 0; j < kTB; j++) acc[i][j] = v4i{0, 0, 0, 0};
+            v4i fa[kFqAhead][NBW];
+            int fi[kFqAhead][NBW];
+            // Blocks past NB (a ragged last pass) re-read block NB-1; their accumulators are never
+            // stored. (Zeroing the fragment instead put a use right behind each load, which made
+            // the compiler wait for the whole prefetch ring at once.)
+            auto aload = [&](int s, v4i (&a)[NBW], int (&ix)[NBW]) {
+                const int sr = s + rot < KS ? s + rot : s + rot - KS;
+#pragma unroll
+                for (int i = 0; i < NBW; i++) {
+                    const int b = min(wb0 + i, NB - 1);
+                    a[i] = *reinterpret_cast<const v4i*>(W_comp + static_cast<size_t>(16 * b + r16) * Kc +
+                                                         kSpARow * sr + 16 * g);
+                    ix[i] = static_cast<int>(meta[static_cast<size_t>(b) * cpr * 16 + (4 * sr + g) * 16 + r16]);
+                }
+            };
+            // One K step: the step's kTB token fragments are read from LDS together, so their
+            // latency overlaps the first block's SMFMACs instead of preceding each block's.
+            auto step = [&](int s, const v4i (&a)[NBW], const int (&ix)[NBW]) {
+                const int8_t* slab = Xs + (s + rot < KS ? s + rot : s + rot - KS) * kSlab;
+                v8i fb[kTB];
+#pragma unroll
+                for (int j = 0; j < kTB; j++) {
+                    const int r = 16 * j + r16;
+                    const v4i b0 = *reinterpret_cast<const v4i*>(slab + sp_b_off(r, g));
+                    const v4i b1 = *reinterpret_cast<const v4i*>(slab + sp_b_off(r, g + 4));
+                    fb[j] = v8i{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+                }
+#pragma unroll
+                for (int j = 0; j < kTB; j++)
+#pragma unroll
+                    for (int i = 0; i < NBW; i++)
+                        acc[i][j] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a[i], fb[j], acc[i][j], ix[i], 0, 0);
+            };
+            // The fragment ring: kFqAhead K steps in flight. The main loop is branch-free (every
+            // step loads its successor), so the compiler's wait before a step counts only that
+            // step's loads; loads under a condition made it wait for the whole ring. Steps past
+            // KS in the prologue re-read step KS-1 and go unused.
+#pragma unroll
+            for (int d = 0; d < kFqAhead; d++) aload(min(d, KS - 1), fa[d], fi[d]);
+            int s0 = 0;
+            for (; s0 + 2 * kFqAhead <= KS; s0 += kFqAhead) {
+#pragma unroll
+                for (int d = 0; d < kFqAhead; d++) {
+                    step(s0 + d, fa[d], fi[d]);
+                    aload(s0 + d + kFqAhead, fa[d], fi[d]);
+                }
+            }
+#pragma unroll
+            for (int d = 0; d < kFqAhead; d++) {         // fewer than 2 * kFqAhead steps remain
+                if (s0 + d < KS) {
+                    step(s0 + d, fa[d], fi[d]);
+                    if (s0 + d + kFqAhead < KS) aload(s0 + d + kFqAhead, fa[d], fi[d]);
+                }
+            }
+#pragma unroll
+            for (int d = 0; d < kFqAhead; d++)
+                if (s0 + kFqAhead + d < KS) step(s0 + kFqAhead + d, fa[d], fi[d]);
+            // epilogue: lane holds C[16 blk + 4 g + e][16 j + r16]
+#pragma unroll
+            for (int i = 0; i < NBW; i++) {
+                const int blk = wb0 + i;
+                if (blk >= NB) continue;
+                const int n = 16 * blk + 4 * g;
+                float ws[4], bv[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    ws[e] = h2f(sws[n + e]);
+                    bv[e] = h2f(sbias[n + e]);
+                }
+#pragma unroll
+                for (int j = 0; j < kTB; j++) {
+                    const int m = m0 + 16 * j + r16;
+                    if (m >= M) continue;
+                    const float as = sc[16 * j + r16];
+                    uint16_t h[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) h[e] = dequant_gemm(acc[i][j][e], as, ws[e], bv[e], has_bias);
+                    *reinterpret_cast<uint2*>(out + static_cast<size_t>(m) * N + n) =
+                        make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+                }
+            }
+        }
+    };
+
+    // Producer and consumer waves run separate tile loops with the same number of barriers
+    // (one before the first tile, one after each tile), so each side's registers and hoisted
+    // addresses stay its own. The barrier waits for LDS traffic only: the producer's prefetch
+    // loads stay in flight across it.
+    auto barrier = [] {
+        __builtin_amdgcn_s_waitcnt(0xC07F);      // lgkmcnt(0)
+        lds_barrier();
+    };
+    const int grid = static_cast<int>(gridDim.x);
+    int tile = blockIdx.x;
+    if (wave >= 4) {
+        const int rp = (wave - 4) * kRowsPerProducer;
+        // The lane id passes through an opaque copy at every tile, so the per-lane load and LDS
+        // store offsets are derived per tile rather than hoisted out of the loop as
+        // 4 x kRowsPerProducer live registers.
+        int ln = lane;
+        uint4 v[2][kR][4];
+        // Tile i of this workgroup uses buffer i & 1 and enters with parity (i * kBatches) & 1;
+        // the loop is unrolled by two so both are compile-time.
+        using P0 = std::integral_constant<int, 0>;
+        using P1 = std::integral_constant<int, kBatches & 1>;
+        load_batch(ln, tile * BT, rp, v[0]);
+        quantize_tile(P0{}, tile, 0, tile + grid, ln, rp, v);
+        barrier();
+        while (tile < tiles) {
+            int next = tile + grid;
+            if (next < tiles) quantize_tile(P1{}, next, 1, next + grid, ln, rp, v);
+            barrier();
+            tile = next;
+            if (tile >= tiles) break;
+            next = tile + grid;
+            if (next < tiles) quantize_tile(P0{}, next, 0, next + grid, ln, rp, v);
+            barrier();
+            tile = next;
+        }
+    } else {
+        barrier();
+        for (int it = 0; tile < tiles; it++, tile += grid) {
+            compute_tile(tile, it & 1, wave);
+            barrier();                           // buffer it&1 is free, buffer (it+1)&1 is complete
+        }
+    }
+}
+
+// Token rows per tile: the tallest of 64 / 48 / 32 whose two buffers and the scale strips fit.
+static int fq_bt(int K, int N) {
+    for (int bt : {64, 48, 32}) {
+        const size_t need = 2 * static_cast<size_t>(bt) * K + 2 * bt * sizeof(float) + 4 * static_cast<size_t>(N);
+        if (need <= static_cast<size_t>(kFqLds)) return bt;
+    }
+    return 0;
+}
+
+static size_t fq_lds_bytes(int K, int N, int bt) {
+    return 2 * static_cast<size_t>(bt) * K + 2 * bt * sizeof(float) + 4 * static_cast<size_t>(N);
+}
+
+// Whether the fused kernel applies: K a multiple of the 128-deep step and at most kFqMaxK, a
+// token tile that fits twice in LDS, 16-byte aligned activations and weights, 8-byte aligned
+// output.
+static bool fq_fits(const void* x, const void* W_comp, const void* out, int K, int N) {
+    return K % kSpStep == 0 && K <= kFqMaxK && fq_bt(K, N) > 0 && aligned(x, 16) && aligned(W_comp, 16) &&
+           aligned(out, 8);
+}
+
+// Automatic path choice (the role of the reference's sp_use_fused, int8_sparse.cu:926-938).
+// The two-pass path writes an INT8 copy of x and reads it back (2*M*K extra DRAM bytes once
+// x and its copy, 3*M*K, outgrow the 256 MB MALL); the fused kernel instead re-streams
+// W_comp + index words (N*K*5/8 bytes) from L2 for every tile of token rows and is bound by
+// its consumer waves, whose work grows with N. Measured on MI355X (fused vs two-pass, us):
+// fused wins at M = 147,456 for 1280->320 (210 vs 229), 1280->160 (146 vs 177), 1536->384 (240
+// vs 255), 2048->256 (244 vs 260), 1024->128 (123 vs 134), at 1280->320 for M = 98,304 (122 vs
+// 127) and 262,144 (322 vs 365); two-pass wins for N >= 512 (1280->640: 269 vs 285), for
+// K = 640 (95 vs 108), when N fills the two-pass engine's 256-row weight tiles at K < 2048
+// (1024->256: 144 vs 170), and while 3*M*K stays near the MALL (M = 65,536, 1280->320: 80 vs
+// 90). 1280->480 is even (226 vs 228).
+static bool fq_pays(int M, int K, int N) {
+    if (K % kSpStep != 0 || K > kFqMaxK || fq_bt(K, N) == 0) return false;
+    if (3.0 * M * K < 300e6) return false;
+    if (N > 480 || K < 1024) return false;
+    return N % 256 != 0 || K >= 2048;
+}
+
+template <int NBW, int BT>
+static int launch_fq(const uint16_t* x, const int8_t* W_comp, const uint32_t* meta, const uint16_t* w_scale,
+                     const uint16_t* bias, uint16_t* out, int M, int K, int N, hipStream_t s)
+{
+    const size_t lds = fq_lds_bytes(K, N, BT);
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&sparse_fq_kernel<NBW, BT>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kFqLds);
+    if (attr != hipSuccess) return static_cast<int>(attr);
+    int st = FORGE_OK;
+    const int cu = device_info(&st).cu_count;
+    if (st != FORGE_OK) return st;
+    const int tiles = divup(M, BT);
+    const int grid = std::min(tiles, cu);     // one 8-wave workgroup per CU
+    sparse_fq_kernel<NBW, BT><<<grid, 512, lds, s>>>(x, W_comp, meta, w_scale, bias, out, M, K, N, tiles);
+    return launch_status();
+}
+
+template <int BT>
+static int launch_fq_bt(const uint16_t* x, const int8_t* W_comp, const uint32_t* meta, const uint16_t* w_scale,
+                        const uint16_t* bias, uint16_t* out, int M, int K, int N, hipStream_t s)
+{
+    // Weight blocks per consumer wave per pass: all of N in one pass up to kMax blocks per wave,
+    // several passes of kMax beyond. kMax keeps the accumulators (NBW x BT/16 blocks) and the
+    // fragment ring within the 256 registers of a wave at 2 waves per SIMD (no spills).
+    constexpr int kMax = BT == 64 ? 4 : (BT == 48 ? 5 : 6);
+    const int per_wave = divup(N / 16, 4);
+    if (per_wave <= 1) return launch_fq<1, BT>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+    if (per_wave <= 2) return launch_fq<2, BT>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+    if (per_wave <= 3) return launch_fq<3, BT>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+    if (per_wave <= 4 || kMax == 4) return launch_fq<4, BT>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+    if constexpr (kMax >= 5) {
+        if (per_wave <= 5 || kMax == 5) return launch_fq<5, BT>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+    }
+    if constexpr (kMax >= 6) return launch_fq<6, BT>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+    return FORGE_EINVAL;
+}
+
+static int launch_sparse_fq(const uint16_t* x, const int8_t* W_comp, const uint32_t* meta, const uint16_t* w_scale,
+                            const uint16_t* bias, uint16_t* out, int M, int K, int N, hipStream_t s)
+{
+    switch (fq_bt(K, N)) {
+        case 64: return launch_fq_bt<64>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+        case 48: return launch_fq_bt<48>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+        case 32: return launch_fq_bt<32>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+        default: return FORGE_EINVAL;
+    }
+}
+
 }  // namespace forge_amd
 
 using namespace forge_amd;
@@ -877,9 +1245,8 @@ extern "C" int forge_sparse_int8_gemm_s32(const int8_t* W_comp, const int8_t* x,
 // built yet; the automatic choice therefore never selects it.
 extern "C" int forge_sparse_int8_linear_fused(int M, int K, int N_out, int* out_flag)
 {
-    (void)M; (void)K; (void)N_out;
     if (!out_flag) return FORGE_EINVAL;
-    *out_flag = 0;
+    *out_flag = (M > 0 && N_out > 0 && N_out % 16 == 0 && fq_pays(M, K, N_out)) ? 1 : 0;
     return FORGE_OK;
 }
 
@@ -888,11 +1255,16 @@ extern "C" int forge_sparse_int8_linear(const uint16_t* x, const int8_t* W_comp,
                                         int M, int K, int N_out, int8_t* scratch_q, float* scratch_scale,
                                         float* splitk_workspace, int split_k, void* stream, int path)
 {
-    (void)path;   // every path computes the same bits; the two-pass path serves them all
     if (M <= 0 || K <= 0 || N_out <= 0) return FORGE_OK;
     if (!x || !W_comp || !w_meta || !w_scale || !out || !scratch_q || !scratch_scale) return FORGE_EINVAL;
     if (K % 64 != 0 || N_out % 16 != 0) return FORGE_EINVAL;
     hipStream_t s = as_stream(stream);
+    // int8_sparse.cu:1022-1033: the fused kernel when forced (path 1) or, on auto (-1) with no
+    // split-K asked for, when it pays; it needs its shape and alignment, else two-pass. Every
+    // path gives the same bits.
+    if (fq_fits(x, W_comp, out, K, N_out) &&
+        (path == 1 || (path == -1 && split_k <= 1 && fq_pays(M, K, N_out))))
+        return launch_sparse_fq(x, W_comp, w_meta, w_scale, bias, out, M, K, N_out, s);
     int st = launch_quantize(x, scratch_q, scratch_scale, M, K, s);
     if (st != FORGE_OK) return st;
     return sparse_gemm(W_comp, scratch_q, w_meta, scratch_scale, w_scale, bias, out, nullptr, M, K, N_out,

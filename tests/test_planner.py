@@ -54,3 +54,29 @@ def test_out_of_range_tile_means_auto(plan):
 def test_headline_plan_is_unsplit(plan):
     # 4096 x 11008 x 4096 has 1376 128x128 tiles: splitting cannot pay
     assert plan(4096, 4096, 11008, 0, True)[1] == 1
+
+
+# The automatic fused/two-pass choice of the sparse linear (the role of the reference's
+# sp_use_fused, src/gemm/int8_sparse.cu:926-938), host-only: the MI355X rule follows
+# measured timings of both paths, not the RTX-4090 model.
+FUSED_CHOICE = [
+    ((147456, 1280, 320), True),     # the reference's example layer (int8_sparse.cuh:82)
+    ((147456, 1280, 160), True), ((147456, 1536, 384), True), ((147456, 2048, 256), True),
+    ((147456, 1024, 128), True), ((98304, 1280, 320), True), ((262144, 1280, 320), True),
+    ((4096, 1280, 320), False),      # small M: the INT8 copy stays on chip
+    ((65536, 1280, 320), False),     # 3*M*K near the 256 MB MALL
+    ((147456, 1024, 256), False),    # N fills the two-pass engine's 256-row tiles
+    ((147456, 640, 160), False),     # short K
+    ((147456, 1280, 640), False),    # wide N
+    ((147456, 2176, 256), False),    # K beyond the fused kernel's 2048
+    ((147456, 1280, 328), False),    # N not a multiple of 16
+]
+
+
+@pytest.mark.parametrize("shape,fused", FUSED_CHOICE)
+def test_sparse_linear_auto_path_choice(shape, fused):
+    import forge_amd
+    lib = forge_amd.load()
+    f = ctypes.c_int(-1)
+    assert lib.forge_sparse_int8_linear_fused(*shape, ctypes.byref(f)) == 0
+    assert f.value == (1 if fused else 0)
