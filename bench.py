@@ -314,6 +314,35 @@ def bench_extra(dev):
     out["f4_prep_sparse_us"] = t_one * 1e3
     out["f4_prep_sparse_GBs"] = (N * K * 4 + N * K // 2 + N * K // 8 + N * 2) / t_one / 1e6
     out["f4_prep_steps_us"] = t_steps * 1e3
+    del wf, qw, qs, cp, rw, mt
+    torch.cuda.empty_cache()
+
+    # The reference's fused-quantize example layer (int8_sparse.cuh:82): sparse_int8_linear
+    # 1280 -> 320 at M = 147,456, FP16 in/out, on the fused path (path 1) and on the two-pass
+    # path (path 0); algorithmic bytes of the fused path = x + out + compressed weights + index
+    # words + w_scale and bias.
+    M, K, N = 147456, 1280, 320
+    W = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+    comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+    raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+    meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+    ops.prune_compress_24(W, comp, raw, N, K)
+    ops.pack_metadata(raw, meta, N, K)
+    xs = torch.randn((M, K), generator=g, device=dev).half()
+    ws = (torch.rand((N,), generator=g, device=dev) * 9e-3 + 1e-3).half()
+    bs = (torch.randn((N,), generator=g, device=dev) * 0.1).half()
+    sq = torch.empty((M, K), dtype=torch.int8, device=dev)
+    ss = torch.empty((M,), dtype=torch.float32, device=dev)
+    fq = lambda: ops.sparse_int8_linear(xs, comp, meta, ws, bs, sq, ss, None, 1, 1)
+    tp = lambda: ops.sparse_int8_linear(xs, comp, meta, ws, bs, sq, ss, None, 1, 0)
+    for _ in range(3):
+        fq()
+        tp()
+    t_fq = events_time_ms(fq, 10)
+    t_tp = events_time_ms(tp, 10)
+    out["f1_fq_us"] = t_fq * 1e3
+    out["f1_twopass_us"] = t_tp * 1e3
+    out["f1_fq_GBs"] = (2 * M * K + 2 * M * N + N * K // 2 + N * K // 8 + 4 * N) / t_fq / 1e6
     return out
 
 
