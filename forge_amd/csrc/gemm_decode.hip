@@ -15,7 +15,8 @@
 //
 // Sparse, up to 8 tokens (decode_sparse_reg_kernel): the dense kernel's structure on 256-deep
 // segments of compressed rows, with a K permutation that keeps the SMFMAC operands consistent
-// (described at the kernel).
+// (described at the kernel). The same kernel serves 16 < M <= 64 tokens of the sparse GEMM with
+// TB = 2 or 4 token blocks per weight fragment (launch_skinny_tb).
 //
 // Sparse, 9-16 tokens (decode_sparse_kernel): a 512-thread workgroup owns 32 weight rows and all of K; its 8
 // wavefronts split K into 128-deep stages, each wave streaming its slice of the compressed
@@ -247,6 +248,56 @@ __device__ __forceinline__ void swap8_rows(v4i own0, v4i own1, bool hi, v4i& h0,
     h1 = hi ? own1 : y;
 }
 
+// Epilogue of the register kernels with several token blocks: red holds each wave's INT32
+// partials, block (b, tb) of wave w at ((w * RB + b) * TB + tb) * 64 + lane; lane l holds
+// rows n0 + 16 b + 4 (l / 16) + e of token 16 tb + l % 16. Waves take the RB x TB blocks in
+// turn, sum the WV partials exactly and store each lane's 4 consecutive outputs of one token
+// row together (8-byte FP16 or 16-byte INT32 stores when the rows allow it).
+template <bool DEQUANT, int RB, int TB, int WV>
+__device__ __forceinline__ void decode_epilogue_blocks(const v4i* red, const GemmEpilogue& ep, int n0, int wave,
+                                                       int lane)
+{
+    const int M = ep.M, N = ep.N;
+    const int r16 = lane & 15, g = lane >> 4;
+    for (int q = wave; q < RB * TB; q += WV) {
+        const int b = q / TB, tb = q - b * TB;
+        v4i sum = red[(b * TB + tb) * kWave + lane];
+#pragma unroll
+        for (int w = 1; w < WV; w++) sum += red[((w * RB + b) * TB + tb) * kWave + lane];
+        const int m = 16 * tb + r16;
+        const int nb = n0 + 16 * b + 4 * g;
+        if (m >= M || nb >= N) continue;
+        const size_t o = static_cast<size_t>(m) * N + nb;
+        const bool whole = ep.vec_out && nb + 4 <= N;
+        if constexpr (DEQUANT) {
+            const float as = ep.act_scale[m];
+            uint16_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int n = nb + e < N ? nb + e : N - 1;
+                const float bv = ep.bias ? h2f(ep.bias[n]) : 0.0f;
+                h[e] = dequant_gemm(sum[e], as, h2f(ep.w_scale[n]), bv, ep.bias != nullptr);
+            }
+            if (whole) {
+                *reinterpret_cast<uint2*>(ep.c16 + o) =
+                    make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (nb + e < N) ep.c16[o + e] = h[e];
+            }
+        } else {
+            if (whole) {
+                *reinterpret_cast<int4*>(ep.c32 + o) = make_int4(sum[0], sum[1], sum[2], sum[3]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (nb + e < N) ep.c32[o + e] = sum[e];
+            }
+        }
+    }
+}
+
 template <bool DEQUANT, int S, int RB, int WV, int AH>
 __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void decode_dense_kernel(
     const int8_t* __restrict__ W, const int8_t* __restrict__ X, GemmEpilogue ep, int K)
@@ -369,12 +420,12 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
 // for the instruction's K range [32 G, +32) of its 128-deep step. Whole 4-groups move, so the
 // index nibbles stay valid: the lane's index word is the packed word of 32-K chunk
 // 8 seg + 2 G + h, and the token operand is gathered with the same permutation.
-template <bool DEQUANT, int S, int RB, int WV, int AH>
+template <bool DEQUANT, int S, int RB, int WV, int AH, int TB = 1>
 __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void decode_sparse_reg_kernel(
     const int8_t* __restrict__ W, const uint32_t* __restrict__ meta, const int8_t* __restrict__ X,
     GemmEpilogue ep, int K)
 {
-    __shared__ v4i red[WV * RB * kWave];
+    __shared__ v4i red[WV * RB * TB * kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int n0 = blockIdx.x * 16 * RB;
@@ -408,12 +459,18 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
             pi[b][h] = base + (c >> 2) * 64 + 16 * (c & 3);
         }
     }
-    // Tokens: row r16 (clamped; rows >= M are zeroed). Step h reads the segment's dense bytes
-    // [64 (g >> 1) + 32 h + 16 (g & 1), +16) and the same + 128.
-    const bool tok = r16 < M;
-    const int8_t* px = X + static_cast<size_t>(tok ? r16 : M - 1) * K + 64 * (g >> 1) + 16 * (g & 1);
+    // Tokens of block tb: row 16 tb + r16 (clamped; rows >= M are zeroed). Step h reads the
+    // segment's dense bytes [64 (g >> 1) + 32 h + 16 (g & 1), +16) and the same + 128.
+    bool tok[TB];
+    const int8_t* px[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++) {
+        const int r = 16 * tb + r16;
+        tok[tb] = r < M;
+        px[tb] = X + static_cast<size_t>(tok[tb] ? r : M - 1) * K + 64 * (g >> 1) + 16 * (g & 1);
+    }
 
-    struct Stage { v4i w[RB][2], x[4]; int ix[RB][2]; };
+    struct Stage { v4i w[RB][2], x[TB][4]; int ix[RB][2]; };
     auto load = [&](int t, Stage& f) {
         const int sg = s0 + (t < ns ? t : ns - 1);
 #pragma unroll
@@ -424,30 +481,38 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
             for (int h = 0; h < 2; h++) f.ix[b][h] = static_cast<int>(ld_stream<uint32_t>(pi[b][h] + sg * 128));
         }
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            f.x[2 * h] = *reinterpret_cast<const v4i*>(px + sg * 256 + 32 * h);
-            f.x[2 * h + 1] = *reinterpret_cast<const v4i*>(px + sg * 256 + 32 * h + 128);
-        }
+        for (int tb = 0; tb < TB; tb++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                f.x[tb][2 * h] = *reinterpret_cast<const v4i*>(px[tb] + sg * 256 + 32 * h);
+                f.x[tb][2 * h + 1] = *reinterpret_cast<const v4i*>(px[tb] + sg * 256 + 32 * h + 128);
+            }
     };
 
-    v4i acc[RB];
+    v4i acc[RB][TB];
 #pragma unroll
-    for (int b = 0; b < RB; b++) acc[b] = v4i{0, 0, 0, 0};
+    for (int b = 0; b < RB; b++)
+#pragma unroll
+        for (int tb = 0; tb < TB; tb++) acc[b][tb] = v4i{0, 0, 0, 0};
     auto compute = [&](Stage& f, bool real) {
-        const bool live = tok && real;
-        v8i xb[2];
+        v4i a[RB][2];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const v4i lo = live ? f.x[2 * h] : v4i{0, 0, 0, 0};
-            const v4i hi4 = live ? f.x[2 * h + 1] : v4i{0, 0, 0, 0};
-            xb[h] = __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
-        }
+        for (int b = 0; b < RB; b++) swap8_rows(f.w[b][0], f.w[b][1], hi, a[b][0], a[b][1]);
 #pragma unroll
-        for (int b = 0; b < RB; b++) {
-            v4i a0, a1;
-            swap8_rows(f.w[b][0], f.w[b][1], hi, a0, a1);
-            acc[b] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a0, xb[0], acc[b], f.ix[b][0], 0, 0);
-            acc[b] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a1, xb[1], acc[b], f.ix[b][1], 0, 0);
+        for (int tb = 0; tb < TB; tb++) {
+            const bool live = tok[tb] && real;
+            v8i xb[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const v4i lo = live ? f.x[tb][2 * h] : v4i{0, 0, 0, 0};
+                const v4i hi4 = live ? f.x[tb][2 * h + 1] : v4i{0, 0, 0, 0};
+                xb[h] = __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+#pragma unroll
+            for (int b = 0; b < RB; b++) {
+                acc[b][tb] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a[b][0], xb[0], acc[b][tb], f.ix[b][0], 0, 0);
+                acc[b][tb] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a[b][1], xb[1], acc[b][tb], f.ix[b][1], 0, 0);
+            }
         }
     };
 
@@ -464,9 +529,13 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
     }
 
 #pragma unroll
-    for (int b = 0; b < RB; b++) red[(wave * RB + b) * kWave + lane] = acc[b];
+    for (int b = 0; b < RB; b++)
+#pragma unroll
+        for (int tb = 0; tb < TB; tb++) red[((wave * RB + b) * TB + tb) * kWave + lane] = acc[b][tb];
     __syncthreads();
-    if (wave < RB) {
+    if constexpr (TB > 1) {
+        decode_epilogue_blocks<DEQUANT, RB, TB, WV>(red, ep, n0, wave, lane);
+    } else if (wave < RB) {
         const int b = wave;
         v4i sum = red[b * kWave + lane];
 #pragma unroll
@@ -534,6 +603,64 @@ static int launch_decode_sparse(const int8_t* W, const uint32_t* meta, const int
     else FORGE_DEC_SPARSE(8);
 #undef FORGE_DEC_SPARSE
     return launch_status();
+}
+
+// Sparse with several token blocks (16 < M <= 64): the register kernel with each weight
+// fragment and index word reused for TB = 2 or 4 token blocks. Each wave's segment count is
+// padded to the next value of {1, 2, 3, 4, 6, 8}. Workgroups own 32 weight rows when that still
+// gives half the chip's CUs one each, else 16 (each workgroup reads the whole token block, so
+// fewer, taller workgroups read less). Measured on the reference benchmark's M = 64 shapes:
+// 1536x6144 14.7 -> 7.1 us, 6144x1536 33.9 -> 15.1 us against the register-staged tile engine.
+// (The dense GEMM keeps its tile engine at these M: the same structure measured slower there.)
+constexpr int kSkinnyTbAheadSparse = 2;
+
+static int pad_stages(int per)
+{
+    static const int kSparse[] = {1, 2, 3, 4, 6, 8};
+    for (int c : kSparse)
+        if (per <= c) return c;
+    return -1;
+}
+
+template <bool DEQUANT, int RB, int TB>
+static int launch_tb_sparse(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep, int K,
+                            hipStream_t s)
+{
+    constexpr int WV = kDecDenseWaves, AH = kSkinnyTbAheadSparse;
+    const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
+    const int S = pad_stages(divup(K / 256, WV));
+#define FORGE_TB_SPARSE(SS) \
+    decode_sparse_reg_kernel<DEQUANT, SS, RB, WV, AH, TB><<<grid, WV * kWave, 0, s>>>(W, meta, X, ep, K)
+    switch (S) {
+    case 1: FORGE_TB_SPARSE(1); break;
+    case 2: FORGE_TB_SPARSE(2); break;
+    case 3: FORGE_TB_SPARSE(3); break;
+    case 4: FORGE_TB_SPARSE(4); break;
+    case 6: FORGE_TB_SPARSE(6); break;
+    case 8: FORGE_TB_SPARSE(8); break;
+    default: return FORGE_EINVAL;
+    }
+#undef FORGE_TB_SPARSE
+    return launch_status();
+}
+
+bool skinny_tb_supported(int M, int K)
+{
+    return M > kDecodeMaxM && M <= kSkinnyTbMaxM && K <= kDecodeMaxK && K % 256 == 0;
+}
+
+int launch_skinny_tb(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep, int K, int cu,
+                     hipStream_t s)
+{
+    if (!skinny_tb_supported(ep.M, K)) return FORGE_EINVAL;
+    const bool tall = 2 * divup(ep.N, 32) >= cu;
+    const bool dq = ep.c16 != nullptr;
+    if (ep.M <= 32) {
+        if (tall) return dq ? launch_tb_sparse<true, 2, 2>(W, meta, X, ep, K, s) : launch_tb_sparse<false, 2, 2>(W, meta, X, ep, K, s);
+        return dq ? launch_tb_sparse<true, 1, 2>(W, meta, X, ep, K, s) : launch_tb_sparse<false, 1, 2>(W, meta, X, ep, K, s);
+    }
+    if (tall) return dq ? launch_tb_sparse<true, 2, 4>(W, meta, X, ep, K, s) : launch_tb_sparse<false, 2, 4>(W, meta, X, ep, K, s);
+    return dq ? launch_tb_sparse<true, 1, 4>(W, meta, X, ep, K, s) : launch_tb_sparse<false, 1, 4>(W, meta, X, ep, K, s);
 }
 
 bool decode_supported(int M, int K) { return M <= kDecodeMaxM && K % 128 == 0 && K <= kDecodeMaxK; }

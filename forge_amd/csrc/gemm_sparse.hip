@@ -777,6 +777,22 @@ static int cu_count_or_default() {
     return (st == FORGE_OK && d.cu_count > 0) ? d.cu_count : default_cu_count();
 }
 
+// Unsplit DMA engine choice for M > 128: 256 weight rows x 256 tokens (sparse_dma32) or x 128
+// tokens (sparse_dma<128>). Both stream about the same bytes per CU per microsecond on MI355X,
+// so a 128-deep stage costs in proportion to its bytes (52 KB: ~1.16 us; 36 KB: ~0.80 us) and
+// the wider tile wins only where its tile waves are not much emptier: measured, 1536x6144 at
+// M = 1024 (96 vs 192 tiles) 20.0 vs 15.6 us, 6144x1536 at M = 4096 55.7 vs 43.4 us, while
+// configs[2] (688 vs 1376 tiles) runs 1.4x faster on the wide tile. Fixed cost per tile wave:
+// ring fill and the epilogue.
+static bool sparse_prefer_wide(int M, int N, int K, int cu)
+{
+    const long long tn = divup(N, 256);
+    const double steps = static_cast<double>(divup(K, kSpStep));
+    const double w256 = static_cast<double>(divupll(tn * divup(M, 256), cu));
+    const double w128 = static_cast<double>(divupll(tn * divup(M, 128), cu));
+    return w256 * (1.16 * steps + 4.0) <= w128 * (0.80 * steps + 3.0);
+}
+
 int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, const float* act_scale,
                 const uint16_t* w_scale, const uint16_t* bias, uint16_t* out16, int32_t* out32, int M,
                 int K, int N, int32_t* ws, int split_k, int tile, hipStream_t s)
@@ -795,6 +811,13 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
         void* o = out16 ? static_cast<void*>(out16) : static_cast<void*>(out32);
         GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N, aligned(o, 16) ? 1 : 0};
         return launch_decode(W_comp, meta, x, ep, K, true, s);
+    }
+    // 16 < M <= 64 in automatic mode: the same weight-streaming kernel with several token blocks
+    // (a forced tile or split runs the engine it names).
+    if (skinny_tb_supported(M, K) && tile == FORGE_SPARSE_TILE_AUTO && split_k <= 1) {
+        void* o = out16 ? static_cast<void*>(out16) : static_cast<void*>(out32);
+        GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N, aligned(o, 16) ? 1 : 0};
+        return launch_skinny_tb(W_comp, meta, x, ep, K, cu_count_or_default(), s);
     }
     int pt = 1, ps = 1;
     sparse_plan_cost(M, K, N, out32 ? 1 : split_k, out32 ? false : ws != nullptr, tile,
@@ -825,7 +848,7 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
         (tile == FORGE_SPARSE_TILE_AUTO || tile == FORGE_SPARSE_TILE_256x128)) {
         void* o = out16 ? static_cast<void*>(out16) : static_cast<void*>(out32);
         GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N, aligned(o, 16) ? 1 : 0};
-        const bool wide = tile == FORGE_SPARSE_TILE_AUTO && M > 128;
+        const bool wide = tile == FORGE_SPARSE_TILE_AUTO && M > 128 && sparse_prefer_wide(M, N, K, cu_count_or_default());
         if (wide)
             return out16 ? launch_sparse_dma32<true>(W_comp, x, meta, ep, K, s)
                          : launch_sparse_dma32<false>(W_comp, x, meta, ep, K, s);
@@ -1241,8 +1264,8 @@ extern "C" int forge_sparse_int8_gemm_s32(const int8_t* W_comp, const int8_t* x,
                        -1, as_stream(stream));
 }
 
-// The fused quantize + GEMM path (reference int8_sparse.cu:258-335, K <= 1280) is not
-// built yet; the automatic choice therefore never selects it.
+// Whether the automatic path of sparse_int8_linear takes the fused quantize + GEMM kernel at
+// this shape (reference sp_use_fused, int8_sparse.cu:926-938; MI355X chooser fq_pays).
 extern "C" int forge_sparse_int8_linear_fused(int M, int K, int N_out, int* out_flag)
 {
     if (!out_flag) return FORGE_EINVAL;

@@ -1,5 +1,6 @@
 """GPU parity: decode-shape GEMMs (M <= 16 tokens) on the weight-streaming decode kernel,
-dense and 2:4 sparse, against the oracle.
+dense and 2:4 sparse, against the oracle; and 16 < M <= 64 on the same kernels with several
+16-token blocks per weight fragment.
 
 Bar: INT32 bit-exact; FP16 bit-exact to the oracle's epilogue. Shapes exercise the kernel's
 K split over 8 wavefronts (K = 128: one wave works; K = 1152: 9 stages, uneven slices and
@@ -101,3 +102,78 @@ def test_config4_full_size_sampled(dev, orc, M):
     say(f"config4 sparse {M}x8192x8192")
     ys = to_host(ops.sparse_int8_linear(xd, comp, meta, wsd, bd, sq, ss)).view(np.uint16)
     assert np.array_equal(ys[:, cols], ref_s)
+
+
+# 16 < M <= 64: two (M <= 32) or four token blocks, partial last block; K covering every padded
+# per-wave stage count (idle waves at small K, padding stages at 640 / 1152 / 5120); N ragged,
+# odd (element stores), and >= 4096 (32-row workgroups instead of 16).
+TB_DENSE = [(17, 128, 48), (32, 384, 200), (33, 640, 201), (48, 1152, 96), (64, 1536, 4160),
+            (40, 5120, 64), (64, 8192, 32), (25, 2048, 4112)]
+TB_SPARSE = [(17, 256, 48), (32, 768, 208), (33, 1280, 16), (48, 2048, 96), (64, 1536, 4160),
+             (40, 5120, 64), (64, 8192, 32), (25, 3072, 4112), (64, 6144, 1536)]
+
+
+def _check_cols(N):
+    return np.arange(N) if N <= 512 else np.unique(np.r_[0:40, N // 2 - 20:N // 2 + 20, N - 40:N])
+
+
+@pytest.mark.parametrize("M,K,N", TB_DENSE)
+def test_token_blocks_dense(dev, orc, M, K, N):
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(M * 13 + K + N)
+    A = int8_uniform(rng, (M, K))
+    B = int8_uniform(rng, (N, K))
+    act = rng.uniform(0.001, 0.05, M).astype(np.float32)
+    ws = rng.uniform(0.001, 0.05, N).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
+    cols = _check_cols(N)
+    acc = orc.gemm_s32(A, B[cols])
+    say(f"token-block dense M={M} K={K} N={N}")
+    Ad, Bd = to_dev(A, dev), to_dev(B, dev)
+    C = torch.empty((M, N), dtype=torch.int32, device=dev)
+    poison(C, 0x7B)
+    C1 = to_host(ops.int8_gemm_s32(Ad, Bd, out=C))
+    assert np.array_equal(C1[:, cols], acc)
+    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    poison(Y, 0x7B)
+    ops.int8_gemm_dequant(Ad, Bd, to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev), out=Y)
+    ref = orc.dequant_epilogue(acc, act, ws[cols], b[cols]).view(np.uint16)
+    assert np.array_equal(to_host(Y).view(np.uint16)[:, cols], ref)
+    # repeat run: identical bits
+    assert np.array_equal(to_host(ops.int8_gemm_s32(Ad, Bd, out=C)), C1)
+
+
+@pytest.mark.parametrize("M,K,N", TB_SPARSE)
+def test_token_blocks_sparse(dev, orc, M, K, N):
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(M * 7 + K * 5 + N)
+    W = int8_uniform(rng, (N, K))
+    x = int8_uniform(rng, (M, K))
+    act = rng.uniform(0.001, 0.05, M).astype(np.float32)
+    ws = rng.uniform(0.001, 0.05, N).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
+    cols = _check_cols(N)
+    cr, mr = orc.prune_compress_24(W)
+    Wp = orc.decompress_24(cr, mr, N, K)
+    acc = orc.gemm_s32(x, Wp[cols])
+    comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+    raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+    meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+    ops.prune_compress_24(to_dev(W, dev), comp, raw, N, K)
+    ops.pack_metadata(raw, meta, N, K)
+    say(f"token-block sparse M={M} K={K} N={N}")
+    xd = to_dev(x, dev)
+    C = torch.empty((M, N), dtype=torch.int32, device=dev)
+    poison(C, 0x7B)
+    assert np.array_equal(to_host(ops.sparse_int8_gemm_s32(comp, xd, meta, out=C))[:, cols], acc)
+    ref = orc.dequant_epilogue(acc, act, ws[cols], b[cols]).view(np.uint16)
+    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    wsp = torch.empty((M, N), dtype=torch.float32, device=dev)
+    # automatic plan (the token-block kernel) and a forced split (the split-K engine): same bits
+    for split in (0, 1, 2):
+        poison(Y, 0x7B)
+        ops.sparse_int8_gemm(comp, xd, meta, to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev),
+                             splitk_workspace=wsp, split_k=split, out=Y)
+        assert np.array_equal(to_host(Y).view(np.uint16)[:, cols], ref)
