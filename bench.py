@@ -23,7 +23,9 @@ overhead is not timed), configs[4] (INT8 NHWC 3x3 conv, INT32 and dequant output
 the rest of the INT8 conv family on NCHW FP16 maps: depthwise 3x3 (1, 64, 540, 960) and
 ConvTranspose2d k2s2 (1, 64, 270, 480) -> (1, 32, 540, 960), as time and HBM GB/s of
 input + output bytes; and SparseLinear's weight preparation at 11008 x 4096 fp32, one pass
-against the reference's separate quantize / prune+compress / pack steps.
+against the reference's separate quantize / prune+compress / pack steps; and
+extra.reference_sweep: the reference's own sparse benchmark (bench_int8_sparse.cu shapes and
+protocol) with the dense path beside it.
 """
 from __future__ import annotations
 
@@ -122,6 +124,105 @@ def graph_time_ms(calls, replays: int = 20) -> float:
     e.record()
     e.synchronize()
     return s.elapsed_time(e) / (replays * len(calls))
+
+
+def graph_median_ms(fn, min_sample_ms: float = 0.2, warmup: int = 50, reps: int = 100) -> float:
+    """The reference benchmark's protocol (benchmarks/bench_int8_sparse.cu:41-85): fn is
+    captured n times into one graph so that a replay takes >= min_sample_ms, replays are
+    warmed up, then each of `reps` replays is bracketed by events; the per-call time is the
+    median replay / n. Inputs stay resident (L2/MALL), as in the reference."""
+    import math
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(10):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(20):
+        fn()
+    e.record()
+    e.synchronize()
+    n = max(1, math.ceil(min_sample_ms / max(s.elapsed_time(e) / 20, 1e-3)))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(n):
+            fn()
+    for _ in range(warmup):
+        graph.replay()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in evs:
+        a.record()
+        graph.replay()
+        b.record()
+    torch.cuda.synchronize()
+    ts = sorted(a.elapsed_time(b) for a, b in evs)
+    return ts[len(ts) // 2] / n
+
+
+def bench_reference_sweep(dev):
+    """The reference's own sparse benchmark (benchmarks/bench_int8_sparse.cu:113-114, 235-236):
+    sparse_int8_gemm with the dequant epilogue, automatic plan and a split-K workspace, on
+    K x N in {1536x6144, 6144x1536, 1280x5120, 5120x1280} x M in {64, 1024, 4096, 8192}, the
+    dense int8_gemm_dequant beside it; and sparse_int8_linear (FP16 in) at its narrow-N layer
+    shapes, two-pass / fused / automatic. Microseconds per call."""
+    import torch
+    from forge_amd import ops
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    gemm, layers, best = {}, {}, 0.0
+    for K, N in ((1536, 6144), (6144, 1536), (1280, 5120), (5120, 1280)):
+        W = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+        comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+        raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+        meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+        ops.prune_compress_24(W, comp, raw, N, K)
+        ops.pack_metadata(raw, meta, N, K)
+        ws = (torch.rand((N,), generator=g, device=dev) * 0.01 + 0.001).half()
+        b = (torch.rand((N,), generator=g, device=dev) - 0.5).half()
+        xh = torch.randn((8192, K), generator=g, device=dev).half()
+        row = {}
+        for M in (64, 1024, 4096, 8192):
+            xq = torch.empty((M, K), dtype=torch.int8, device=dev)
+            xs = torch.empty((M,), dtype=torch.float32, device=dev)
+            out = torch.empty((M, N), dtype=torch.float16, device=dev)
+            wsp = torch.empty((M, N), dtype=torch.float32, device=dev)
+            ops.fused_quantize_activation(xh[:M], M, K, out=xq, scales=xs)
+            t_sp = graph_median_ms(lambda: ops.sparse_int8_gemm(comp, xq, meta, xs, ws, b, splitk_workspace=wsp,
+                                                                split_k=0, out=out))
+            t_de = graph_median_ms(lambda: ops.int8_gemm_dequant(xq, W, xs, ws, b, out=out))
+            tops = 2.0 * M * N * K / t_sp / 1e9
+            best = max(best, tops)
+            row[str(M)] = {"sparse_us": round(t_sp * 1e3, 2), "sparse_tops": round(tops, 1),
+                           "dense_us": round(t_de * 1e3, 2)}
+        gemm[f"{K}x{N}"] = row
+        del W, comp, raw, meta, xh
+    for K, N, M in ((1280, 320, 147456), (640, 320, 147456), (640, 640, 36864), (1024, 640, 37008),
+                    (1024, 320, 37008), (1280, 1280, 9216)):
+        W = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+        comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+        raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+        meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+        ops.prune_compress_24(W, comp, raw, N, K)
+        ops.pack_metadata(raw, meta, N, K)
+        ws = (torch.rand((N,), generator=g, device=dev) * 0.01 + 0.001).half()
+        b = (torch.rand((N,), generator=g, device=dev) - 0.5).half()
+        x = (torch.rand((M, K), generator=g, device=dev) * 4 - 2).half()
+        sq = torch.empty((M, K), dtype=torch.int8, device=dev)
+        ss = torch.empty((M,), dtype=torch.float32, device=dev)
+        wsp = torch.empty((M, N), dtype=torch.float32, device=dev)
+        t = [graph_median_ms(lambda p=p: ops.sparse_int8_linear(x, comp, meta, ws, b, sq, ss, wsp, 0, p))
+             for p in (0, 1, -1)]
+        layers[f"{K}x{N}@{M}"] = {"two_pass_us": round(t[0] * 1e3, 2), "fused_us": round(t[1] * 1e3, 2),
+                                  "auto_us": round(t[2] * 1e3, 2)}
+        del W, comp, raw, meta, x, sq, ss, wsp
+    torch.cuda.empty_cache()
+    return {"protocol": "bench_int8_sparse.cu: graph of n calls >= 0.2 ms, 50 warm-up + 100 timed replays, "
+                        "median / n, L2-resident inputs",
+            "gemm": gemm, "layers": layers, "peak_sparse_tops": round(best, 1)}
 
 
 def make_c2(dev, seed=2):
@@ -430,6 +531,7 @@ def main() -> int:
         line["cpu_baseline"] = cpu_baseline()
     if not args.no_extra:
         line["extra"] = {k: round(v, 3) for k, v in bench_extra(dev).items()}
+        line["extra"]["reference_sweep"] = bench_reference_sweep(dev)
     print(json.dumps(line))
     return 0
 
