@@ -248,6 +248,112 @@ __device__ __forceinline__ void swap8_rows(v4i own0, v4i own1, bool hi, v4i& h0,
     h1 = hi ? own1 : y;
 }
 
+// Fused quantize prologue of the decode kernels (M <= kDecodeFqMaxM = 2 tokens, the
+// int8_linear / sparse_int8_linear entry points): the workgroup quantizes the FP16 token rows
+// (fq.x, (M, K), K % 8 == 0, 16-byte aligned) into LDS rows of stride K + kFqPad, with the
+// arithmetic of quantize_rows_block_kernel -- the row absmax as a packed u16 maximum of fp16
+// magnitude bit patterns (two rows per DPP wave reduction), the fp32 maximum for a row that
+// holds a NaN, quant8_row -- so the INT8 tokens and scales are bit-identical to the quantize
+// kernel's. Thread t holds vectors t, t + 256, ... (VPR per row) of every row, loaded before any
+// use; loads past the row end re-read its last vector, rows past M re-read row M - 1 (neither
+// changes a result). When fq.q is set, workgroup 0 also writes the INT8 rows and the scales to
+// the caller's scratch, as the two-pass path leaves them there (int8_linear); the sparse fused
+// path leaves the scratch untouched, as the reference's does. The 128-byte row padding puts the two token
+// rows of a 16-lane LDS read phase in different bank halves.
+struct FqArgs {
+    const uint16_t* x;   // (M, K) FP16 tokens
+    int8_t* q;           // (M, K) INT8 scratch, 8-byte aligned, or null (not written)
+    float* scale;        // (M,) scratch (written with q)
+};
+constexpr int kFqPad = 128;
+constexpr int kFqTokAhead = 2;   // token stages read from LDS ahead of their MFMAs
+constexpr int kFqTokBytes = kDecodeFqMaxM * (kDecodeMaxK + kFqPad);
+
+// The prologue in two parts: the token loads (issued before the kernel's first weight loads, so
+// that waiting for them does not wait for the weights: loads retire in issue order), then the
+// rest once the weights are in flight.
+template <int VPR>
+__device__ __forceinline__ void fq_load_tokens(const FqArgs& fq, int M, int K, uint4 (&v)[kDecodeFqMaxM][VPR])
+{
+    const int t = threadIdx.x;
+    const int nvec = K >> 3;
+#pragma unroll
+    for (int r = 0; r < kDecodeFqMaxM; r++) {
+        const uint4* src = reinterpret_cast<const uint4*>(fq.x + static_cast<size_t>(r < M ? r : M - 1) * K);
+#pragma unroll
+        for (int i = 0; i < VPR; i++) v[r][i] = src[min(t + i * 256, nvec - 1)];
+    }
+}
+
+template <int VPR>
+__device__ __forceinline__ void fq_quantize_tokens(const FqArgs& fq, int M, int K, const uint4 (&v)[kDecodeFqMaxM][VPR],
+                                                   int8_t* tok, float* sscale, uint32_t* sbits, float* smax)
+{
+    constexpr int MT = kDecodeFqMaxM;
+    static_assert(MT == 2, "one packed row pair");
+    const int t = threadIdx.x, lane = t & (kWave - 1), wave = t / kWave;
+    const int nvec = K >> 3;
+    const int ld = K + kFqPad;
+    uint32_t m[MT];
+#pragma unroll
+    for (int r = 0; r < MT; r++) {
+        m[r] = 0u;
+#pragma unroll
+        for (int i = 0; i < VPR; i++) m[r] = absbits8(v[r][i], m[r]);
+    }
+    const uint32_t p01 = wave_max_pk_u16(pk_rows2(m[0], m[1]));
+    if (lane == 0) {
+        sbits[wave * MT + 0] = p01 & 0xFFFFu;
+        sbits[wave * MT + 1] = p01 >> 16;
+    }
+    __syncthreads();
+    uint32_t bits[MT];
+    bool nan_row = false;
+#pragma unroll
+    for (int r = 0; r < MT; r++) {
+        bits[r] = max(max(sbits[r], sbits[MT + r]), max(sbits[2 * MT + r], sbits[3 * MT + r]));
+        nan_row |= r < M && bits[r] > kHalfInfBits;
+    }
+    float amax[MT];
+#pragma unroll
+    for (int r = 0; r < MT; r++) amax[r] = h2f(static_cast<uint16_t>(bits[r]));
+    if (nan_row) {                  // uniform: a row holding a NaN takes the fp32 maximum
+#pragma unroll
+        for (int r = 0; r < MT; r++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < VPR; i++) a = absmax8(v[r][i], a);
+            a = wave_max(a);
+            if (lane == 0) smax[wave * MT + r] = a;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < MT; r++)
+            if (bits[r] > kHalfInfBits)
+                amax[r] = fmaxf(fmaxf(smax[r], smax[MT + r]), fmaxf(smax[2 * MT + r], smax[3 * MT + r]));
+    }
+    const bool out = blockIdx.x == 0 && fq.q != nullptr;
+#pragma unroll
+    for (int r = 0; r < MT; r++) {
+        if (r >= M) break;
+        const float scale = row_scale(amax[r]);
+        const float inv = 1.0f / scale;
+        if (t == 0) {
+            sscale[r] = scale;
+            if (out) fq.scale[r] = scale;
+        }
+#pragma unroll
+        for (int i = 0; i < VPR; i++) {
+            const int idx = t + i * 256;
+            if (idx >= nvec) continue;
+            const uint2 q = quant8_row(v[r][i], inv);
+            *reinterpret_cast<uint2*>(tok + r * ld + idx * 8) = q;
+            if (out) *reinterpret_cast<uint2*>(fq.q + static_cast<size_t>(r) * K + idx * 8) = q;
+        }
+    }
+    __syncthreads();
+}
+
 // Epilogue of the register kernels with several token blocks: red holds each wave's INT32
 // partials, block (b, tb) of wave w at ((w * RB + b) * TB + tb) * 64 + lane; lane l holds
 // rows n0 + 16 b + 4 (l / 16) + e of token 16 tb + l % 16. Waves take the RB x TB blocks in
@@ -298,10 +404,13 @@ __device__ __forceinline__ void decode_epilogue_blocks(const v4i* red, const Gem
     }
 }
 
-template <bool DEQUANT, int S, int RB, int WV, int AH>
+// VPR > 0: fused quantize (fq_quantize_tokens with VPR vectors per thread per row); the tokens
+// are then read from LDS instead of X.
+template <bool DEQUANT, int S, int RB, int WV, int AH, int VPR = 0>
 __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void decode_dense_kernel(
-    const int8_t* __restrict__ W, const int8_t* __restrict__ X, GemmEpilogue ep, int K)
+    const int8_t* __restrict__ W, const int8_t* __restrict__ X, GemmEpilogue ep, int K, FqArgs fq)
 {
+    constexpr bool FQ = VPR > 0;
     __shared__ v4i red[WV * RB * kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -323,19 +432,29 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
             const int r = n0 + 16 * b + 8 * j + (lane & 7);
             pw[b][j] = W + static_cast<size_t>(r < N ? r : N - 1) * K + 16 * (lane >> 3);
         }
+    [[maybe_unused]] int8_t* ftok = nullptr;
+    [[maybe_unused]] float* fscale = nullptr;
+    if constexpr (FQ) {
+        __shared__ __align__(16) int8_t s_tok[kFqTokBytes];
+        __shared__ float s_scale[kDecodeFqMaxM];
+        ftok = s_tok;
+        fscale = s_scale;
+    }
     const int8_t* px[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const int r = 8 * j + (lane & 7);
-        px[j] = X + static_cast<size_t>(r < M ? r : M - 1) * K + 16 * (lane >> 3);
+        if constexpr (FQ) px[j] = ftok + (r < M ? r : M - 1) * (K + kFqPad) + 16 * (lane >> 3);
+        else px[j] = X + static_cast<size_t>(r < M ? r : M - 1) * K + 16 * (lane >> 3);
     }
     const bool tok = r16 < M;   // after the swap, lane l holds token row l % 16
 
     // Epilogue operands of waves 0..RB-1 (block b = wave: rows n0 + 16 b + 4 g + e, token
-    // r16), fetched before the K loop so that their latency hides behind it.
+    // r16), fetched before the K loop so that their latency hides behind it (the act scale
+    // comes from the fused prologue when it runs).
     float e_as = 0.0f, e_ws[4] = {0.0f, 0.0f, 0.0f, 0.0f}, e_b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (DEQUANT && wave < RB) {
-        e_as = ep.act_scale[tok ? r16 : 0];
+        if constexpr (!FQ) e_as = ep.act_scale[tok ? r16 : 0];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int n = n0 + 16 * wave + 4 * g + e;
@@ -346,14 +465,21 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
     }
 
     struct Stage { v4i w[RB][2], x[2]; };
-    auto load = [&](int t, Stage& f) {
+    auto load_w = [&](int t, Stage& f) {
         const int st = s0 + (t < ns ? t : ns - 1);
 #pragma unroll
         for (int b = 0; b < RB; b++)
 #pragma unroll
             for (int j = 0; j < 2; j++) f.w[b][j] = ld_stream<v4i>(pw[b][j] + st * 128);
+    };
+    auto load_x = [&](int t, Stage& f) {
+        const int st = s0 + (t < ns ? t : ns - 1);
 #pragma unroll
         for (int j = 0; j < 2; j++) f.x[j] = *reinterpret_cast<const v4i*>(px[j] + st * 128);
+    };
+    auto load = [&](int t, Stage& f) {
+        load_w(t, f);
+        load_x(t, f);
     };
 
     v4i acc[RB];
@@ -375,14 +501,37 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
         }
     };
 
-    if (ns > 0) {
-        constexpr int A = AH < S ? AH : S;
-        Stage f[S];
+    // Fused: the first A weight stages are issued before the prologue (issuing all of them
+    // measured slower); the token stages then come from LDS kFqTokAhead ahead.
+    constexpr int A = AH < S ? AH : S;
+    constexpr int AX = FQ ? (kFqTokAhead < S ? kFqTokAhead : S) : A;
+    Stage f[S];
+    if constexpr (FQ) {
+        // The first weight stages stream in while the workgroup quantizes its tokens (every wave
+        // takes part in the prologue, idle K slices included).
+        uint4 xv[kDecodeFqMaxM][VPR];
+        fq_load_tokens<VPR>(fq, M, K, xv);
+        if (ns > 0) {
+#pragma unroll
+            for (int t = 0; t < A; t++) load_w(t, f[t]);
+        }
+        __shared__ uint32_t s_bits[4 * kDecodeFqMaxM];
+        __shared__ float s_max[4 * kDecodeFqMaxM];
+        fq_quantize_tokens<VPR>(fq, M, K, xv, ftok, fscale, s_bits, s_max);
+        if (DEQUANT && wave < RB) e_as = fscale[tok ? r16 : 0];
+        if (ns > 0) {
+#pragma unroll
+            for (int t = 0; t < AX; t++) load_x(t, f[t]);
+        }
+    } else if (ns > 0) {
 #pragma unroll
         for (int t = 0; t < A; t++) load(t, f[t]);
+    }
+    if (ns > 0) {
 #pragma unroll
         for (int t = 0; t < S; t++) {
-            if (t + A < S) load(t + A, f[t + A]);
+            if (t + A < S) load_w(t + A, f[t + A]);
+            if (t + AX < S) load_x(t + AX, f[t + AX]);
             compute(f[t], t < ns);
         }
     }
@@ -420,11 +569,14 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
 // for the instruction's K range [32 G, +32) of its 128-deep step. Whole 4-groups move, so the
 // index nibbles stay valid: the lane's index word is the packed word of 32-K chunk
 // 8 seg + 2 G + h, and the token operand is gathered with the same permutation.
-template <bool DEQUANT, int S, int RB, int WV, int AH, int TB = 1>
+// VPR > 0 (one token block only): fused quantize, as in decode_dense_kernel.
+template <bool DEQUANT, int S, int RB, int WV, int AH, int TB = 1, int VPR = 0>
 __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void decode_sparse_reg_kernel(
     const int8_t* __restrict__ W, const uint32_t* __restrict__ meta, const int8_t* __restrict__ X,
-    GemmEpilogue ep, int K)
+    GemmEpilogue ep, int K, FqArgs fq)
 {
+    constexpr bool FQ = VPR > 0;
+    static_assert(!FQ || TB == 1, "the fused prologue serves one token block");
     __shared__ v4i red[WV * RB * TB * kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -461,17 +613,27 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
     }
     // Tokens of block tb: row 16 tb + r16 (clamped; rows >= M are zeroed). Step h reads the
     // segment's dense bytes [64 (g >> 1) + 32 h + 16 (g & 1), +16) and the same + 128.
+    [[maybe_unused]] int8_t* ftok = nullptr;
+    [[maybe_unused]] float* fscale = nullptr;
+    if constexpr (FQ) {
+        __shared__ __align__(16) int8_t s_tok[kFqTokBytes];
+        __shared__ float s_scale[kDecodeFqMaxM];
+        ftok = s_tok;
+        fscale = s_scale;
+    }
     bool tok[TB];
     const int8_t* px[TB];
 #pragma unroll
     for (int tb = 0; tb < TB; tb++) {
         const int r = 16 * tb + r16;
         tok[tb] = r < M;
-        px[tb] = X + static_cast<size_t>(tok[tb] ? r : M - 1) * K + 64 * (g >> 1) + 16 * (g & 1);
+        const int rr = tok[tb] ? r : M - 1;
+        if constexpr (FQ) px[tb] = ftok + rr * (K + kFqPad) + 64 * (g >> 1) + 16 * (g & 1);
+        else px[tb] = X + static_cast<size_t>(rr) * K + 64 * (g >> 1) + 16 * (g & 1);
     }
 
     struct Stage { v4i w[RB][2], x[TB][4]; int ix[RB][2]; };
-    auto load = [&](int t, Stage& f) {
+    auto load_w = [&](int t, Stage& f) {
         const int sg = s0 + (t < ns ? t : ns - 1);
 #pragma unroll
         for (int b = 0; b < RB; b++) {
@@ -480,6 +642,9 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
 #pragma unroll
             for (int h = 0; h < 2; h++) f.ix[b][h] = static_cast<int>(ld_stream<uint32_t>(pi[b][h] + sg * 128));
         }
+    };
+    auto load_x = [&](int t, Stage& f) {
+        const int sg = s0 + (t < ns ? t : ns - 1);
 #pragma unroll
         for (int tb = 0; tb < TB; tb++)
 #pragma unroll
@@ -487,6 +652,10 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
                 f.x[tb][2 * h] = *reinterpret_cast<const v4i*>(px[tb] + sg * 256 + 32 * h);
                 f.x[tb][2 * h + 1] = *reinterpret_cast<const v4i*>(px[tb] + sg * 256 + 32 * h + 128);
             }
+    };
+    auto load = [&](int t, Stage& f) {
+        load_w(t, f);
+        load_x(t, f);
     };
 
     v4i acc[RB][TB];
@@ -516,14 +685,34 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
         }
     };
 
-    if (ns > 0) {
-        constexpr int A = AH < S ? AH : S;
-        Stage f[S];
+    // Fused: the first A weight stages are issued before the prologue (issuing all of them
+    // measured slower); the token stages then come from LDS kFqTokAhead ahead.
+    constexpr int A = AH < S ? AH : S;
+    constexpr int AX = FQ ? (kFqTokAhead < S ? kFqTokAhead : S) : A;
+    Stage f[S];
+    if constexpr (FQ) {
+        uint4 xv[kDecodeFqMaxM][VPR];
+        fq_load_tokens<VPR>(fq, M, K, xv);
+        if (ns > 0) {
+#pragma unroll
+            for (int t = 0; t < A; t++) load_w(t, f[t]);
+        }
+        __shared__ uint32_t s_bits[4 * kDecodeFqMaxM];
+        __shared__ float s_max[4 * kDecodeFqMaxM];
+        fq_quantize_tokens<VPR>(fq, M, K, xv, ftok, fscale, s_bits, s_max);
+        if (ns > 0) {
+#pragma unroll
+            for (int t = 0; t < AX; t++) load_x(t, f[t]);
+        }
+    } else if (ns > 0) {
 #pragma unroll
         for (int t = 0; t < A; t++) load(t, f[t]);
+    }
+    if (ns > 0) {
 #pragma unroll
         for (int t = 0; t < S; t++) {
-            if (t + A < S) load(t + A, f[t + A]);
+            if (t + A < S) load_w(t + A, f[t + A]);
+            if (t + AX < S) load_x(t + AX, f[t + AX]);
             compute(f[t], t < ns);
         }
     }
@@ -543,7 +732,8 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
         const int m = r16;
         if (m < M) {
             const int nb = n0 + 16 * b + 4 * g;
-            const float as = DEQUANT ? ep.act_scale[m] : 0.0f;
+            float as = 0.0f;
+            if constexpr (DEQUANT) as = FQ ? fscale[m] : ep.act_scale[m];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int n = nb + e;
@@ -566,7 +756,7 @@ static int launch_decode_sparse_reg(const int8_t* W, const uint32_t* meta, const
 {
     const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
     const int per = divup(K / 256, WV);
-#define FORGE_DEC_SPREG(SS) decode_sparse_reg_kernel<DEQUANT, SS, RB, WV, AH><<<grid, WV * kWave, 0, s>>>(W, meta, X, ep, K)
+#define FORGE_DEC_SPREG(SS) decode_sparse_reg_kernel<DEQUANT, SS, RB, WV, AH><<<grid, WV * kWave, 0, s>>>(W, meta, X, ep, K, FqArgs{})
     if (per <= 1) FORGE_DEC_SPREG(1);
     else if (per <= 2) FORGE_DEC_SPREG(2);
     else if (per <= 4) FORGE_DEC_SPREG(4);
@@ -580,7 +770,7 @@ static int launch_decode_dense(const int8_t* W, const int8_t* X, const GemmEpilo
 {
     const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
     const int per = divup(K / 128, WV);
-#define FORGE_DEC_DENSE(SS) decode_dense_kernel<DEQUANT, SS, RB, WV, AH><<<grid, WV * kWave, 0, s>>>(W, X, ep, K)
+#define FORGE_DEC_DENSE(SS) decode_dense_kernel<DEQUANT, SS, RB, WV, AH><<<grid, WV * kWave, 0, s>>>(W, X, ep, K, FqArgs{})
     if (per <= 1) FORGE_DEC_DENSE(1);
     else if (per <= 2) FORGE_DEC_DENSE(2);
     else if (per <= 4) FORGE_DEC_DENSE(4);
@@ -630,7 +820,7 @@ static int launch_tb_sparse(const int8_t* W, const uint32_t* meta, const int8_t*
     const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
     const int S = pad_stages(divup(K / 256, WV));
 #define FORGE_TB_SPARSE(SS) \
-    decode_sparse_reg_kernel<DEQUANT, SS, RB, WV, AH, TB><<<grid, WV * kWave, 0, s>>>(W, meta, X, ep, K)
+    decode_sparse_reg_kernel<DEQUANT, SS, RB, WV, AH, TB><<<grid, WV * kWave, 0, s>>>(W, meta, X, ep, K, FqArgs{})
     switch (S) {
     case 1: FORGE_TB_SPARSE(1); break;
     case 2: FORGE_TB_SPARSE(2); break;
@@ -664,6 +854,56 @@ int launch_skinny_tb(const int8_t* W, const uint32_t* meta, const int8_t* X, con
 }
 
 bool decode_supported(int M, int K) { return M <= kDecodeMaxM && K % 128 == 0 && K <= kDecodeMaxK; }
+
+bool decode_fq_supported(int M, int K, bool sparse)
+{
+    return M <= kDecodeFqMaxM && K <= kDecodeMaxK && K % (sparse ? 256 : 128) == 0;
+}
+
+template <int VPR>
+static int launch_decode_fq_vpr(const int8_t* W, const uint32_t* meta, const GemmEpilogue& ep, int K, bool sparse,
+                                const FqArgs& fq, hipStream_t s)
+{
+    if (sparse) {
+        constexpr int RB = 2, WV = 4, AH = 4;
+        const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
+        const int per = divup(K / 256, WV);
+#define FORGE_DEC_FQ_SP(SS) \
+    decode_sparse_reg_kernel<true, SS, RB, WV, AH, 1, VPR><<<grid, WV * kWave, 0, s>>>(W, meta, nullptr, ep, K, fq)
+        if (per <= 1) FORGE_DEC_FQ_SP(1);
+        else if (per <= 2) FORGE_DEC_FQ_SP(2);
+        else if (per <= 4) FORGE_DEC_FQ_SP(4);
+        else FORGE_DEC_FQ_SP(8);
+#undef FORGE_DEC_FQ_SP
+        return launch_status();
+    }
+    constexpr int RB = 1, WV = kDecDenseWaves, AH = kDecDenseAhead;
+    const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
+    const int per = divup(K / 128, WV);
+#define FORGE_DEC_FQ_DENSE(SS) \
+    decode_dense_kernel<true, SS, RB, WV, AH, VPR><<<grid, WV * kWave, 0, s>>>(W, nullptr, ep, K, fq)
+    if (per <= 1) FORGE_DEC_FQ_DENSE(1);
+    else if (per <= 2) FORGE_DEC_FQ_DENSE(2);
+    else if (per <= 4) FORGE_DEC_FQ_DENSE(4);
+    else if (per <= 8) FORGE_DEC_FQ_DENSE(8);
+    else FORGE_DEC_FQ_DENSE(16);
+#undef FORGE_DEC_FQ_DENSE
+    return launch_status();
+}
+
+int launch_decode_fq(const uint16_t* x, const int8_t* W, const uint32_t* meta, const uint16_t* w_scale,
+                     const uint16_t* bias, uint16_t* out, int8_t* q_scratch, float* scale_scratch, int M, int K,
+                     int N, bool sparse, hipStream_t s)
+{
+    if (!decode_fq_supported(M, K, sparse) || !aligned(x, 16) || (q_scratch && !aligned(q_scratch, 8)))
+        return FORGE_EINVAL;
+    const GemmEpilogue ep{nullptr, out, nullptr, w_scale, bias, M, N, 0};
+    const FqArgs fq{x, q_scratch, scale_scratch};
+    const int vpr = divup(K, 8 * 256);
+    if (vpr <= 1) return launch_decode_fq_vpr<1>(W, meta, ep, K, sparse, fq, s);
+    if (vpr <= 2) return launch_decode_fq_vpr<2>(W, meta, ep, K, sparse, fq, s);
+    return launch_decode_fq_vpr<4>(W, meta, ep, K, sparse, fq, s);
+}
 
 int launch_decode(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep, int K,
                   bool sparse, hipStream_t s)

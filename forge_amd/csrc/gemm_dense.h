@@ -31,7 +31,21 @@ int launch_gemm_skinny(const int8_t* A, const int8_t* B, const GemmEpilogue& ep,
 // gfx950 index words (sparse), tokens X (M,K) int8; 16-byte aligned operands.
 constexpr int kDecodeMaxM = 16;
 constexpr int kDecodeMaxK = 8192;   // dense: 4 waves x 16 stages of 128; sparse: 8 waves x 8 stages
+// Decode with the per-token quantize fused into the kernel (FP16 tokens in): up to this many
+// tokens each workgroup quantizes the whole token block itself. Measured against quantize kernel
+// + decode GEMM replayed in a graph (N = K = 8192, 6 rotating weight copies): dense 13.4-14.2 vs
+// 14.8-15.1 us at M = 1-2, sparse 10.6-11.1 vs 11.3-11.5 us; a 4-row prologue was level with the
+// two launches at 3-4 tokens (sparse 0.2-0.7 us behind), so those keep the quantize kernel.
+constexpr int kDecodeFqMaxM = 2;
 bool decode_supported(int M, int K);
+// int8_linear / sparse_int8_linear at M <= kDecodeFqMaxM on the decode kernels with the per-token
+// quantize fused in (dense K % 128 == 0, sparse K % 256 == 0, K <= kDecodeMaxK; x, W, W_comp and
+// the index words 16-byte aligned, q_scratch 8-byte aligned). Same bits as quantize + GEMM; with
+// q_scratch non-null the quantized rows and scales are also left in the scratch buffers.
+bool decode_fq_supported(int M, int K, bool sparse);
+int launch_decode_fq(const uint16_t* x, const int8_t* W, const uint32_t* meta, const uint16_t* w_scale,
+                     const uint16_t* bias, uint16_t* out, int8_t* q_scratch, float* scale_scratch, int M, int K,
+                     int N, bool sparse, hipStream_t s);
 int launch_decode(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep, int K,
                   bool sparse, hipStream_t s);
 

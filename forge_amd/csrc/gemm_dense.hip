@@ -259,6 +259,10 @@ extern "C" int forge_int8_linear(const uint16_t* x, const int8_t* w, const uint1
     if (M <= 0 || K <= 0 || N <= 0) return FORGE_OK;
     if (!x || !w || !w_scale || !out || !scratch_q || !scratch_scale) return FORGE_EINVAL;
     hipStream_t s = as_stream(stream);
+    // Decode shapes: one kernel, the quantize fused into the decode GEMM's prologue (each
+    // workgroup quantizes the few token rows itself while its first weight stages stream in).
+    if (decode_fq_supported(M, K, false) && aligned(x, 16) && aligned(w, 16) && aligned(scratch_q, 8))
+        return launch_decode_fq(x, w, nullptr, w_scale, bias, out, scratch_q, scratch_scale, M, K, N, false, s);
     int st = launch_quantize(x, scratch_q, scratch_scale, M, K, s);
     if (st != FORGE_OK) return st;
     return gemm_dense(scratch_q, w, scratch_scale, w_scale, bias, out, nullptr, M, K, N, s);

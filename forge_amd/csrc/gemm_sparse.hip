@@ -1264,12 +1264,15 @@ extern "C" int forge_sparse_int8_gemm_s32(const int8_t* W_comp, const int8_t* x,
                        -1, as_stream(stream));
 }
 
-// Whether the automatic path of sparse_int8_linear takes the fused quantize + GEMM kernel at
-// this shape (reference sp_use_fused, int8_sparse.cu:926-938; MI355X chooser fq_pays).
+// Whether the automatic path of sparse_int8_linear (with no split-K asked for, and aligned
+// operands) takes a fused quantize + GEMM kernel at this shape (reference sp_use_fused,
+// int8_sparse.cu:926-938): the decode kernel with its quantize prologue at decode shapes, the
+// persistent fused kernel where the MI355X chooser fq_pays says so.
 extern "C" int forge_sparse_int8_linear_fused(int M, int K, int N_out, int* out_flag)
 {
     if (!out_flag) return FORGE_EINVAL;
-    *out_flag = (M > 0 && N_out > 0 && N_out % 16 == 0 && fq_pays(M, K, N_out)) ? 1 : 0;
+    const bool ok = M > 0 && N_out > 0 && N_out % 16 == 0 && K > 0 && K % 64 == 0;
+    *out_flag = (ok && (decode_fq_supported(M, K, true) || fq_pays(M, K, N_out))) ? 1 : 0;
     return FORGE_OK;
 }
 
@@ -1285,6 +1288,12 @@ extern "C" int forge_sparse_int8_linear(const uint16_t* x, const int8_t* W_comp,
     // int8_sparse.cu:1022-1033: the fused kernel when forced (path 1) or, on auto (-1) with no
     // split-K asked for, when it pays; it needs its shape and alignment, else two-pass. Every
     // path gives the same bits.
+    // Decode shapes on the fused path: the decode kernel quantizes the few token rows in its
+    // prologue (one kernel instead of two); like the reference's fused path it leaves the scratch
+    // buffers untouched (int8_sparse.cuh:87-89).
+    if ((path == 1 || (path == -1 && split_k <= 1)) && decode_fq_supported(M, K, true) && aligned(x, 16) &&
+        aligned(W_comp, 16) && aligned(w_meta, 16))
+        return launch_decode_fq(x, W_comp, w_meta, w_scale, bias, out, nullptr, nullptr, M, K, N_out, true, s);
     if (fq_fits(x, W_comp, out, K, N_out) &&
         (path == 1 || (path == -1 && split_k <= 1 && fq_pays(M, K, N_out))))
         return launch_sparse_fq(x, W_comp, w_meta, w_scale, bias, out, M, K, N_out, s);

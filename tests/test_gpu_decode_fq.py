@@ -1,0 +1,93 @@
+"""GPU parity: int8_linear and sparse_int8_linear at decode shapes (M <= 2 tokens), where the
+per-token quantize runs inside the decode GEMM kernel's prologue (one launch).
+
+Bar: bit-exact against the oracle's two-pass composition (quantize rows -> INT32 GEMM -> dequant
+epilogue) and against the library's own two-pass launches (quantize kernel + GEMM), on token rows
+holding the quantizers' edge cases (NaN payloads, +-inf, subnormals, -0, exact ties, the fp16
+maximum); K covering 1, 2 and 4 token vectors per thread and 1-16 stages per wave (idle waves
+at small K); ragged N. Dense: the quantized rows and scales left in the scratch buffers equal
+the quantize kernel's (the reference's int8_linear leaves them there). Sparse: the fused path
+leaves the scratch untouched (int8_sparse.cuh:87-89) and equals paths 0 and -1."""
+import numpy as np
+import pytest
+
+from helpers import int8_uniform, poison, say, special_fp16_rows, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+DENSE = [(1, 128, 48), (2, 1152, 200), (1, 2048, 96), (2, 3072, 1000), (2, 8192, 64), (1, 8192, 4096),
+         (2, 640, 16)]
+SPARSE = [(1, 256, 48), (2, 1280, 208), (1, 2048, 96), (2, 3072, 1024), (2, 8192, 64), (1, 8192, 4096)]
+
+
+def _x(rng, M, K, special):
+    if special:
+        return special_fp16_rows(rng, M, K)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    x[:, rng.choice(K, 2, replace=False)] *= 20
+    return x.astype(np.float16)
+
+
+@pytest.mark.parametrize("special", [False, True])
+@pytest.mark.parametrize("M,K,N", DENSE)
+def test_fused_decode_dense(dev, orc, M, K, N, special):
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(M * 11 + K + N + special)
+    x = _x(rng, M, K, special)
+    W = int8_uniform(rng, (N, K))
+    ws = rng.uniform(1e-3, 1e-2, N).astype(np.float16)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float16)
+    ref, qr, sr = orc.linear(x, W, ws, b)
+    say(f"fused decode dense M={M} K={K} N={N} special={special}")
+    xd, Wd, wsd, bd = to_dev(x, dev), to_dev(W, dev), to_dev(ws, dev), to_dev(b, dev)
+    sq = torch.empty((M, K), dtype=torch.int8, device=dev)
+    ss = torch.empty((M,), dtype=torch.float32, device=dev)
+    poison(sq, 0x5A)
+    poison(ss, 0x5A)
+    y = to_host(ops.int8_linear(xd, Wd, wsd, bd, sq, ss))
+    assert np.array_equal(y.view(np.uint16), ref.view(np.uint16))
+    assert np.array_equal(to_host(sq), qr)
+    assert np.array_equal(to_host(ss).view(np.uint32), sr.view(np.uint32))
+    # the library's two-pass launches (quantize kernel, then the decode GEMM on its output)
+    q2 = torch.empty((M, K), dtype=torch.int8, device=dev)
+    s2 = torch.empty((M,), dtype=torch.float32, device=dev)
+    ops.fused_quantize_activation(xd, M, K, out=q2, scales=s2)
+    y2 = to_host(ops.int8_gemm_dequant(q2, Wd, s2, wsd, bd))
+    assert np.array_equal(y.view(np.uint16), y2.view(np.uint16))
+
+
+@pytest.mark.parametrize("special", [False, True])
+@pytest.mark.parametrize("M,K,N", SPARSE)
+def test_fused_decode_sparse(dev, orc, M, K, N, special):
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(M * 5 + K + N + special)
+    x = _x(rng, M, K, special)
+    W = int8_uniform(rng, (N, K))
+    ws = rng.uniform(1e-3, 1e-2, N).astype(np.float16)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float16)
+    cr, mr = orc.prune_compress_24(W)
+    qr, sr = orc.quantize_rows(x)
+    ref = orc.dequant_epilogue(orc.sparse_gemm_s32(cr, qr, mr, N, K), sr, ws, b).view(np.uint16)
+    comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+    raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+    meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+    ops.prune_compress_24(to_dev(W, dev), comp, raw, N, K)
+    ops.pack_metadata(raw, meta, N, K)
+    assert ops.sparse_int8_linear_fused(M, K, N)
+    say(f"fused decode sparse M={M} K={K} N={N} special={special}")
+    xd, wsd, bd = to_dev(x, dev), to_dev(ws, dev), to_dev(b, dev)
+    sq = torch.empty((M, K), dtype=torch.int8, device=dev)
+    ss = torch.empty((M,), dtype=torch.float32, device=dev)
+    sq.fill_(0x5A)
+    ss.view(torch.int32).fill_(0x5A5A5A5A)
+    outs = {}
+    for path in (1, -1):
+        outs[path] = to_host(ops.sparse_int8_linear(xd, comp, meta, wsd, bd, sq, ss, None, 1, path)).view(np.uint16)
+        assert np.array_equal(outs[path], ref)
+    # the fused path leaves the scratch buffers untouched
+    assert bool((sq == 0x5A).all()) and bool((ss.view(torch.int32) == 0x5A5A5A5A).all())
+    y0 = to_host(ops.sparse_int8_linear(xd, comp, meta, wsd, bd, sq, ss, None, 1, 0)).view(np.uint16)
+    assert np.array_equal(y0, ref)
+    assert np.array_equal(to_host(sq), qr)

@@ -70,6 +70,10 @@ FUSED_CHOICE = [
     ((147456, 1280, 640), False),    # wide N
     ((147456, 2176, 256), False),    # K beyond the fused kernel's 2048
     ((147456, 1280, 328), False),    # N not a multiple of 16
+    ((1, 8192, 8192), True),         # decode: the decode kernel with its quantize prologue
+    ((2, 512, 96), True), ((2, 384, 96), False),   # ... needs K % 256 == 0
+    ((3, 8192, 8192), False),        # more tokens than the prologue quantizes
+    ((2, 8448, 8192), False),        # K beyond the decode kernel's 8192
 ]
 
 
