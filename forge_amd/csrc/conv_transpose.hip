@@ -33,9 +33,11 @@ static size_t up256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 // 64 consecutive pixels of one image and writes their whole (C_out, 2x2) output, so the INT8
 // activations never leave the chip and the input is read once.
 //   1. Thread t loads pixels 8*(t%8) .. +8 of channels t/8 + 32k as 16-byte rows (KC loads
-//      in flight), takes the per-pixel absmax over its channels, then over the wave's 8
-//      channel groups (lane shuffles) and the 4 waves (LDS): the row arithmetic of
-//      quantize_rows on each pixel's C_in values.
+//      in flight; the wave's first MFMA item's weight rows and scales load behind them, later
+//      items one item ahead), takes the per-pixel absmax over its channels on fp16 bit patterns
+//      (one packed u16 maximum per two pixels; the fp32 maximum for a pixel holding a NaN),
+//      then over the wave's 8 channel groups (lane shuffles) and the 4 waves (LDS): the row
+//      arithmetic of quantize_rows on each pixel's C_in values.
 //   2. The quantized pixels form the A tile in LDS (64 x C_in bytes, 16-byte chunks swizzled
 //      by row so the MFMA row reads spread over the banks).
 //   3. Work items (m-block i of 32 pixels, n-block j of 32 GEMM columns) go round-robin to the
@@ -53,18 +55,24 @@ __global__ __launch_bounds__(256) void convt_fused_kernel(
 {
     constexpr int C = 32 * KC;
     constexpr int kNch = C / 16;
+    constexpr int PT = 64;                           // pixels per tile (128 measured slower)
+    constexpr int kNW = PT / 16;                     // waves: 4 * PT threads
+    constexpr int kPG = PT / 8;                      // 8-pixel groups per tile
+    constexpr int kMB = PT / 32;                     // 32-pixel MFMA row blocks
     static_assert((kNch & (kNch - 1)) == 0, "row swizzle needs a power-of-two chunk count");
-    __shared__ __align__(16) int8_t As[64 * C];
-    __shared__ float red[4][64];
-    __shared__ float ascale[64];
-    __shared__ float sinv[64];
+    __shared__ __align__(16) int8_t As[PT * C];
+    __shared__ float red[kNW][PT];
+    __shared__ uint32_t redb[kNW][PT];
+    __shared__ int nan_px[PT];
+    __shared__ float ascale[PT];
+    __shared__ float sinv[PT];
     const int t = threadIdx.x, lane = t & (kWave - 1), wave = t >> 6;
     const int img = blockIdx.x / tiles;
-    const int p0 = (blockIdx.x - img * tiles) * 64;
-    const int np = min(64, HW - p0);                 // a multiple of 8
+    const int p0 = (blockIdx.x - img * tiles) * PT;
+    const int np = min(PT, HW - p0);                 // a multiple of 8
 
     // 1. loads and per-pixel absmax
-    const int po = t & 7, cg = t >> 3;
+    const int po = t % kPG, cg = t / kPG;
     const bool pin = 8 * po < np;
     const uint16_t* xi = x + static_cast<size_t>(img) * C * HW + p0 + 8 * po;
     uint4 v[KC];
@@ -72,34 +80,101 @@ __global__ __launch_bounds__(256) void convt_fused_kernel(
     for (int k = 0; k < KC; k++)
         v[k] = pin ? *reinterpret_cast<const uint4*>(xi + static_cast<size_t>(cg + 32 * k) * HW)
                    : make_uint4(0u, 0u, 0u, 0u);
-    float m[8];
+
+    // The wave's first MFMA item's weight fragments and scales load now, behind the input loads
+    // (they do not depend on them); later items load one item ahead.
+    const int N = 4 * C_out;
+    const int items = kMB * ((N + 31) / 32);
+    const int l31 = lane & 31, hi = lane >> 5;
+    const bool has_bias = bias != nullptr;
+    struct Item { v4i fb[KC]; uint16_t ws[4], b[4]; };
+    auto load_item = [&](int it, Item& I) {
+        const int j = it / kMB;
+        const int n = 32 * j + l31;
+        const int nc = n < N ? n : N - 1;
 #pragma unroll
-    for (int e = 0; e < 8; e++) m[e] = 0.0f;
+        for (int ks = 0; ks < KC; ks++)
+            I.fb[ks] = *reinterpret_cast<const v4i*>(w + static_cast<size_t>(nc) * C + 16 * (2 * ks + hi));
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const int co = min(8 * j + 2 * g + hi, C_out - 1);
+            I.ws[g] = w_scale[co];
+            I.b[g] = has_bias ? bias[co] : static_cast<uint16_t>(0);
+        }
+    };
+    Item cur;
+    if (wave < items) load_item(wave, cur);
+
+    // Per-pixel absmax on fp16 bit patterns: lane word q holds pixels 2q, 2q + 1 of one channel,
+    // so one packed u16 maximum covers two pixels (magnitude bits order as the magnitudes); a
+    // pixel whose maximum pattern is a NaN takes the fp32 maximum (fmaxf skips NaN).
+    uint32_t mb[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int k = 0; k < KC; k++) {
-        const uint32_t u[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-            m[e] = fmaxf(m[e], fabsf(h2f(static_cast<uint16_t>((e & 1) ? (u[e >> 1] >> 16) : (u[e >> 1] & 0xFFFFu)))));
+        mb[0] = pk_max_u16(mb[0], v[k].x & 0x7FFF7FFFu);
+        mb[1] = pk_max_u16(mb[1], v[k].y & 0x7FFF7FFFu);
+        mb[2] = pk_max_u16(mb[2], v[k].z & 0x7FFF7FFFu);
+        mb[3] = pk_max_u16(mb[3], v[k].w & 0x7FFF7FFFu);
     }
 #pragma unroll
-    for (int e = 0; e < 8; e++)
+    for (int q = 0; q < 4; q++)
 #pragma unroll
-        for (int off = 8; off < kWave; off <<= 1) m[e] = fmaxf(m[e], __shfl_xor(m[e], off, kWave));
-    if (lane < 8) {
+        for (int off = kPG; off < kWave; off <<= 1)
+            mb[q] = pk_max_u16(mb[q], static_cast<uint32_t>(__shfl_xor(static_cast<int>(mb[q]), off, kWave)));
+    if (lane < kPG) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) red[wave][8 * po + e] = m[e];
+        for (int q = 0; q < 4; q++) {
+            redb[wave][8 * po + 2 * q] = mb[q] & 0xFFFFu;
+            redb[wave][8 * po + 2 * q + 1] = mb[q] >> 16;
+        }
     }
     __syncthreads();
-    if (t < 64) {
-        const float a = fmaxf(fmaxf(red[0][t], red[1][t]), fmaxf(red[2][t], red[3][t]));
-        const float scale = row_scale(a);
+    if (t < PT) {
+        uint32_t bits = redb[0][t];
+#pragma unroll
+        for (int wv = 1; wv < kNW; wv++) bits = max(bits, redb[wv][t]);
+        nan_px[t] = bits > kHalfInfBits ? 1 : 0;
+        ascale[t] = h2f(static_cast<uint16_t>(bits));
+    }
+    __syncthreads();
+    if (__builtin_amdgcn_readfirstlane(__syncthreads_or(t < PT && nan_px[t]))) {
+        // rare: some pixel holds a NaN -- its fp32 maximum over the channels
+        float m[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) m[e] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KC; k++) {
+            const uint32_t u[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                m[e] = fmaxf(m[e], fabsf(h2f(static_cast<uint16_t>((e & 1) ? (u[e >> 1] >> 16) : (u[e >> 1] & 0xFFFFu)))));
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+#pragma unroll
+            for (int off = kPG; off < kWave; off <<= 1) m[e] = fmaxf(m[e], __shfl_xor(m[e], off, kWave));
+        if (lane < kPG) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) red[wave][8 * po + e] = m[e];
+        }
+        __syncthreads();
+        if (t < PT && nan_px[t]) {
+            float a = red[0][t];
+#pragma unroll
+            for (int wv = 1; wv < kNW; wv++) a = fmaxf(a, red[wv][t]);
+            ascale[t] = a;
+        }
+        __syncthreads();
+    }
+    if (t < PT) {
+        const float scale = row_scale(ascale[t]);
         ascale[t] = scale;
         sinv[t] = 1.0f / scale;
     }
     __syncthreads();
 
-    // 2. quantize into the A tile: As[p][c] at chunk (c / 16) ^ (p % kNch)
+    // 2. quantize into the A tile: As[p][c] at chunk (c / 16) ^ (p % kNch). qrow_bits gives the
+    //    byte of clamp(rne(x * inv)) for a value of the pixel whose absmax gave inv.
 #pragma unroll
     for (int e = 0; e < 8; e++) {
         const int p = 8 * po + e;
@@ -109,33 +184,26 @@ __global__ __launch_bounds__(256) void convt_fused_kernel(
             const int c = cg + 32 * k;
             const uint32_t word = (e & 1) ? ((&v[k].x)[e >> 1] >> 16) : ((&v[k].x)[e >> 1] & 0xFFFFu);
             As[p * C + ((((c >> 4) ^ (p & (kNch - 1)))) << 4) + (c & 15)] =
-                static_cast<int8_t>(quant1(h2f(static_cast<uint16_t>(word)), inv));
+                static_cast<int8_t>(qrow_bits(static_cast<uint16_t>(word), inv) & 0xFFu);
         }
     }
     __syncthreads();
 
     // 3./4. MFMA items and the in-register scatter
-    const int N = 4 * C_out;
-    const int items = 2 * ((N + 31) / 32);
-    const int l31 = lane & 31, hi = lane >> 5;
-    const bool has_bias = bias != nullptr;
     const size_t plane = 4 * static_cast<size_t>(HW);
     const size_t W2 = 2 * static_cast<size_t>(W);
-    for (int it = wave; it < items; it += 4) {
-        const int i = it & 1, j = it >> 1;
-        const int n = 32 * j + l31;
+    for (int it = wave; it < items; it += kNW) {
+        const int i = it % kMB, j = it / kMB;
         v4i fb[KC];
 #pragma unroll
-        for (int ks = 0; ks < KC; ks++)
-            fb[ks] = n < N ? *reinterpret_cast<const v4i*>(w + static_cast<size_t>(n) * C + 16 * (2 * ks + hi))
-                           : v4i{0, 0, 0, 0};
+        for (int ks = 0; ks < KC; ks++) fb[ks] = cur.fb[ks];
         float wsv[4], bv[4];
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-            const int co = min(8 * j + 2 * g + hi, C_out - 1);
-            wsv[g] = h2f(w_scale[co]);
-            bv[g] = has_bias ? h2f(bias[co]) : 0.0f;
+            wsv[g] = h2f(cur.ws[g]);
+            bv[g] = h2f(cur.b[g]);
         }
+        if (it + kNW < items) load_item(it + kNW, cur);
         v16i acc;
 #pragma unroll
         for (int e = 0; e < 16; e++) acc[e] = 0;

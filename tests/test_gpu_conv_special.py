@@ -164,6 +164,8 @@ CT_CASES = [
     (2, 64, 6, 12, 5, True),        # partial pixel tile, C_out % 8 != 0 (partial column block)
     (1, 32, 3, 8, 33, True),        # 5 column blocks over 4 waves
     (1, 128, 8, 3, 16, True),       # odd W: a 32-pixel block spans image rows
+    (2, 64, 10, 20, 24, True),      # 8-pixel last tile per image, 3 waves of MFMA items
+    (1, 256, 16, 24, 8, False),     # C_in = 256, one column block (waves without an item)
     # two-kernel path: pixel quantizer + GEMM with the scatter epilogue
     (3, 24, 7, 5, 10, True),        # W % 4 != 0: element stores; chunked images
     (2, 13, 6, 8, 5, True),         # C_in % 4 != 0: byte rows, byte-gather GEMM
@@ -227,3 +229,44 @@ def test_conv_transpose_full_size(dev, orc):
     y = to_host(ops.int8_conv_transpose2d_k2s2_forward(to_dev(x, dev), to_dev(w, dev), to_dev(ws, dev),
                                                        to_dev(b, dev)))
     assert _bits_equal(y, want)
+
+
+@pytest.mark.parametrize("C_in", [32, 64, 256])
+def test_conv_transpose_special_pixels(dev, orc, C_in):
+    """Pixels holding the quantizer's edge cases -- a NaN among finite channels (several
+    payloads), an all-NaN pixel, +-inf, subnormals with +-0, exact ties after scaling (absmax
+    127 gives scale 1), the fp16 maximum -- through the fused kernel (aligned output) and the
+    two-kernel path (an output view 2 bytes off a 4-byte boundary), both against the oracle."""
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(C_in)
+    N, H, W, C_out = 1, 12, 16, 24
+    x, w, ws, b = _ct_inputs(rng, N, C_in, H, W, C_out, True)
+    xb = x.view(np.uint16)
+    px = lambda p: (p // W, p % W)
+    for p, bits in [(0, 0x7E00), (3, 0x7C01), (9, 0xFE00), (17, 0x7D55)]:   # one NaN channel
+        h, wc = px(p)
+        xb[0, rng.integers(C_in), h, wc] = bits
+    h, wc = px(20)
+    xb[0, :, h, wc] = 0x7E00                                                # all NaN
+    h, wc = px(24)
+    xb[0, 5 % C_in, h, wc] = 0x7C00                                         # +inf
+    h, wc = px(33)
+    xb[0, 7 % C_in, h, wc] = 0xFC00                                         # -inf
+    h, wc = px(40)
+    xb[0, :, h, wc] = rng.choice(np.array([0x0001, 0x8001, 0x03FF, 0x0200, 0x8000, 0x0000], np.uint16), C_in)
+    h, wc = px(47)
+    xb[0, :, h, wc] = 0
+    xb[0, :8, h, wc] = np.array([127.0, 2.5, 3.5, -2.5, 0.5, -0.5, 1.5, -126.5], np.float16).view(np.uint16)
+    h, wc = px(58)
+    xb[0, :, h, wc] = np.float16(-65504).view(np.uint16)
+    xb[0, ::3, h, wc] = np.float16(65504).view(np.uint16)
+    want = orc.conv_transpose2d_k2s2(x, w, ws, b)
+    say(f"conv_transpose special pixels C_in={C_in}")
+    xd, wd, wsd, bd = to_dev(x, dev), to_dev(w, dev), to_dev(ws, dev), to_dev(b, dev)
+    y1 = to_host(ops.int8_conv_transpose2d_k2s2_forward(xd, wd, wsd, bd))
+    assert _bits_equal(y1, want)
+    buf = torch.zeros((want.size + 8,), dtype=torch.float16, device=dev)
+    out = buf[1:1 + want.size].view(want.shape)
+    ops.int8_conv_transpose2d_k2s2_forward(xd, wd, wsd, bd, out=out)
+    assert _bits_equal(to_host(out), want)
