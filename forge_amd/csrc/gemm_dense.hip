@@ -118,6 +118,42 @@ static int cu_count(int* st) {
 
 // DMA engine with the tile chosen for the grid (256 or 128; smaller grids take the
 // register-staged engine): returns -1 when the DMA engine does not apply.
+// The rows from m1 on, as an operand of their own (a second launch over them).
+static DmaRowMajor rows_from(const DmaRowMajor& a, int m1) {
+    return DmaRowMajor{a.p + static_cast<size_t>(m1) * a.K, a.rows - m1, a.K};
+}
+static DmaConv rows_from(const DmaConv& a, int m1) {
+    DmaConv b = a;
+    b.r0 += m1;
+    return b;
+}
+
+// A single column of 256x256 tiles whose last tile wave is under 3/4 full (configs[4]: 392
+// tiles on 256 CUs, the second wave 53 % full): the first full waves run as 256-row tiles, the
+// remaining rows as one wave of 192-row tiles (3/4 of a tile's work each), 1.75 tile times
+// instead of 2 there. Returns -1 when the split does not apply.
+template <bool DEQUANT, class OpA>
+static int launch_dma_tail_split(const OpA& opa, const DmaRowMajor& opb, const GemmEpilogue& ep, int M, int N, int K,
+                                 int cu, hipStream_t s)
+{
+    const long long tiles = divup(M, 256);
+    if (N > 256 || ep.up_w != 0 || tiles <= cu) return -1;
+    const long long waves = divupll(tiles, cu);
+    const long long last = tiles - (waves - 1) * cu;
+    const long long m1 = (waves - 1) * cu * 256;
+    if (4 * last >= 3LL * cu || m1 >= M || divup(M - static_cast<int>(m1), 192) > cu) return -1;
+    const int M1 = static_cast<int>(m1), M2 = M - M1;
+    int st = launch_dma<256, 256, DEQUANT>(opa, opb, ep, M1, N, K, s);
+    if (st != FORGE_OK) return st;
+    GemmEpilogue ep2 = ep;
+    ep2.M = M2;
+    if (ep.c16) ep2.c16 = ep.c16 + static_cast<size_t>(M1) * N;
+    if (ep.c32) ep2.c32 = ep.c32 + static_cast<size_t>(M1) * N;
+    if (ep.act_scale) ep2.act_scale = ep.act_scale + M1;
+    // 16-byte row stores stay aligned: M1 * N * elem is a multiple of 256 * 16.
+    return launch_dma<192, 256, DEQUANT>(rows_from(opa, M1), opb, ep2, M2, N, K, s);
+}
+
 template <class OpA>
 static int dispatch_dma(const OpA& opa, const DmaRowMajor& opb, const GemmEpilogue& ep, int M, int N, int K,
                         hipStream_t s)
@@ -127,8 +163,12 @@ static int dispatch_dma(const OpA& opa, const DmaRowMajor& opb, const GemmEpilog
     if (st != FORGE_OK) return st;
     const TileCfg t = pick_tile(M, N, cu);
     const bool out16 = ep.c16 != nullptr;
-    if (t == TileCfg::k256)
+    if (t == TileCfg::k256) {
+        const int r = out16 ? launch_dma_tail_split<true>(opa, opb, ep, M, N, K, cu, s)
+                            : launch_dma_tail_split<false>(opa, opb, ep, M, N, K, cu, s);
+        if (r != -1) return r;
         return out16 ? launch_dma<256, 256, true>(opa, opb, ep, M, N, K, s) : launch_dma<256, 256, false>(opa, opb, ep, M, N, K, s);
+    }
     if (t == TileCfg::k128)
         return out16 ? launch_dma<128, 128, true>(opa, opb, ep, M, N, K, s) : launch_dma<128, 128, false>(opa, opb, ep, M, N, K, s);
     return -1;

@@ -151,6 +151,7 @@ struct ConvGeom {
     int K;      // kH * kW * C
     int H, W, C, Ho, Wo, kW;
     int padH, padW, strideH, strideW, dilH, dilW;
+    int r0 = 0; // operand row r is output pixel r0 + r (a launch over the rows from r0 on)
 };
 
 // Needs C % 16 == 0 (a chunk never straddles two taps) and a 16-byte aligned image.
@@ -345,6 +346,7 @@ struct DmaConv : ConvGeom {
         int c16;             // 16 * chunk
     };
     __device__ __forceinline__ Lane lane(int r, int c) const {
+        r += r0;
         r = r < rows ? r : rows - 1;
         const int wo = r % Wo;
         const int t = r / Wo;
@@ -753,8 +755,14 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[BN / 64][BM / 64], 
                 }
             }
         }
-        if (ep.up_w) flush_up2x2<kU, BM / 2>(stage, bl, ep, wm, wn);
-        else flush_rows<kU, kEsz, true, true, BM / 2>(stage, ep, wm, wn);
+        // The upsample scatter (4-pixel groups across the wave) exists for tile heights whose
+        // wave tile splits into such groups; other heights never take it (the caller checks).
+        if constexpr (kWave % ((BM / 2) / 4) == 0) {
+            if (ep.up_w) flush_up2x2<kU, BM / 2>(stage, bl, ep, wm, wn);
+            else flush_rows<kU, kEsz, true, true, BM / 2>(stage, ep, wm, wn);
+        } else {
+            flush_rows<kU, kEsz, true, true, BM / 2>(stage, ep, wm, wn);
+        }
     } else {
         int8_t* strip = lds + wave * (32 * kRowBytes);
 #pragma unroll

@@ -67,18 +67,22 @@ def test_conv_dma_gather(dev, orc, N, H, W, C, Co, k, pad, stride, dil, check):
 
 def test_config5_full_size(dev, orc):
     """NHWC (32,56,56,256) x (256,3,3,256), stride 1, pad 1; INT32 checked
-    bit-exactly on the first and last image (images are independent), dequant on one."""
+    bit-exactly on the first and last image and on image 20, which holds output row 65,536
+    where the 392 tiles split into a 256-row launch and a 192-row one (images are
+    independent); dequant on the last image."""
     import torch
     from forge_amd import ops
     rng = np.random.default_rng(5)
     x = int8_uniform(rng, (32, 56, 56, 256))
     w = int8_uniform(rng, (256, 3, 3, 256))
     ref0 = orc.conv2d_nhwc_s32(x[:1], w, (1, 1))
+    ref20 = orc.conv2d_nhwc_s32(x[20:21], w, (1, 1))
     ref31 = orc.conv2d_nhwc_s32(x[31:], w, (1, 1))
     say("config5 conv 32x56x56x256")
     xd, wd = to_dev(x, dev), to_dev(w, dev)
     out = to_host(ops.int8_conv2d_nhwc_s32(xd, wd, (1, 1)))
     assert np.array_equal(out[:1], ref0) and np.array_equal(out[31:], ref31)
+    assert np.array_equal(out[20:21], ref20)
     M = 32 * 56 * 56
     act = np.full(M, 0.02, np.float32)
     ws = rng.uniform(1e-3, 1e-2, 256).astype(np.float16)

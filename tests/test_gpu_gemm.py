@@ -127,3 +127,34 @@ def test_4096_cube_int32_sampled(dev, orc):
     # column checksum identity: sum_m C[m, :] == (sum_m A[m, :]) . B^T  (exact in int64)
     colsum = C.astype(np.int64).sum(axis=0)
     assert np.array_equal(colsum, A.astype(np.int64).sum(axis=0) @ B.astype(np.int64).T)
+
+
+@pytest.mark.parametrize("N", [256, 200])
+def test_gemm_tail_split(dev, orc, N):
+    """M = 70,000 rows in one column of 256x256 tiles: 274 tiles, the second wave 7 % full, so
+    the first 65,536 rows run as 256-row tiles and the rest as 192-row tiles in a second
+    launch. Rows on both sides of the boundary and the last rows bit-exact (INT32 and FP16);
+    every column's sum over all rows equals (sum of A's rows) . B (exact in int64)."""
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(70000 + N)
+    M, K = 70000, 256
+    A = int8_uniform(rng, (M, K))
+    B = int8_uniform(rng, (N, K))
+    rows = np.array([0, 255, 65535, 65536, 65537, 65727, 65728, 69887, 69888, 69999])
+    ref = orc.gemm_s32(A[rows], B)
+    say(f"gemm tail split M={M} K={K} N={N}")
+    Ad, Bd = to_dev(A, dev), to_dev(B, dev)
+    out = torch.empty((M, N), dtype=torch.int32, device=dev)
+    poison(out, 0x7B)
+    C = to_host(ops.int8_gemm_s32(Ad, Bd, out=out))
+    assert np.array_equal(C[rows], ref)
+    assert np.array_equal(C.astype(np.int64).sum(axis=0), A.astype(np.int64).sum(axis=0) @ B.astype(np.int64).T)
+    act = rng.uniform(0.001, 0.05, M).astype(np.float32)
+    ws = rng.uniform(0.001, 0.05, N).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
+    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    poison(Y, 0x7B)
+    ops.int8_gemm_dequant(Ad, Bd, to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev), out=Y)
+    refy = orc.dequant_epilogue(ref, act[rows], ws, b)
+    assert np.array_equal(to_host(Y)[rows].view(np.uint16), refy.view(np.uint16))
