@@ -688,6 +688,184 @@ static int launch_sparse_dma(const int8_t* W, const int8_t* X, const uint32_t* m
     return launch_status();
 }
 
+// ---- DMA ring engine for small tiles: 128 weight rows x 64 tokens -------------------
+// For shapes whose 256-row tiles leave most CUs idle (narrow N, deep K: the reference
+// benchmark's 6144x1536 and 5120x1280 at M = 1024 give 48 and 40 such tiles). A stage is small
+// (18 KB: 128 compressed rows x 64 B, 64 token rows x 128 B, 8 blocks x 64 index words, the
+// layouts of SpDmaTile), so one stage of lead cannot cover the load latency; D slots give
+// D - 1 stages in flight. One barrier per stage publishes stage kt (every wave waited for its
+// own DMAs of it) and marks stage kt - 1's slot read by every wave, which then receives stage
+// kt + D - 1. Waves in a 2 x 2 grid own 64 weight rows x 32 tokens: 4 x 2 blocks of
+// v_smfmac_i32_16x16x128_i8 per stage.
+template <int D>
+struct SpRingTile {
+    static constexpr int BNW = 128, BMT = 64;
+    static constexpr int kTN = 4, kTM = 2;
+    static constexpr int kWBytes = BNW * 64, kXBytes = BMT * 128, kIBytes = BNW / 16 * 256;
+    static constexpr int kSlotBytes = kWBytes + kXBytes + kIBytes;
+    static constexpr int kLdsBytes = D * kSlotBytes;
+    static constexpr int kWIns = kWBytes / 1024 / 4;    // 1 KB DMA instructions per wave per stage
+    static constexpr int kXIns = kXBytes / 1024 / 4;
+    static constexpr int kVm = kWIns + kXIns + 1;       // + one half-wave index DMA
+    static_assert(kIBytes == 4 * 512, "each wave copies 512 bytes of index words per stage");
+    static_assert(D >= 2 && (D - 2) * kVm < 64, "ring depth");
+
+    v4i acc[kTN][kTM];
+
+    __device__ __forceinline__ void run(const int8_t* W, const int8_t* X, const uint32_t* meta, int M, int N, int K,
+                                        int n0, int m0, int8_t* lds) {
+        const int lane = threadIdx.x & (kWave - 1);
+        const int wave = threadIdx.x / kWave;
+        const int wn = (wave >> 1) * (BNW / 2);
+        const int wm = (wave & 1) * (BMT / 2);
+        const int r16 = lane & 15, g = lane >> 4;
+        const int Kc = K >> 1, cpr = K >> 5;
+#pragma unroll
+        for (int i = 0; i < kTN; i++)
+#pragma unroll
+            for (int j = 0; j < kTM; j++) acc[i][j] = v4i{0, 0, 0, 0};
+
+        const int8_t* pw[kWIns];
+        const int8_t* px[kXIns];
+#pragma unroll
+        for (int q = 0; q < kWIns; q++) {
+            const int s = (wave * kWIns + q) * kWave + lane;
+            const int r = s >> 2, c = (s & 3) ^ lds_swz4(r);
+            const int gr = (n0 + r) < N ? (n0 + r) : N - 1;
+            pw[q] = W + static_cast<size_t>(gr) * Kc + 16 * c;
+        }
+#pragma unroll
+        for (int q = 0; q < kXIns; q++) {
+            const int s = (wave * kXIns + q) * kWave + lane;
+            const int r = s >> 3, c = (s & 7) ^ lds_swz8(r);
+            const int gr = (m0 + r) < M ? (m0 + r) : M - 1;
+            px[q] = X + static_cast<size_t>(gr) * K + 16 * c;
+        }
+        const int8_t* pi;
+        {
+            const int s = wave * 32 + (lane & 31);        // 16-byte chunk of the stage's index area
+            int b = (n0 >> 4) + (s >> 4);
+            b = b < (N >> 4) ? b : (N >> 4) - 1;
+            pi = reinterpret_cast<const int8_t*>(meta + static_cast<size_t>(b) * cpr * 16) + 16 * (s & 15);
+        }
+        const int nst = K / 128;
+        auto slot_of = [&](int st) { return lds + (st % D) * kSlotBytes; };
+        auto issue = [&](int st) {
+            int8_t* slot = slot_of(st);
+#pragma unroll
+            for (int q = 0; q < kWIns; q++) dma16(pw[q] + st * 64, slot + (wave * kWIns + q) * 1024);
+#pragma unroll
+            for (int q = 0; q < kXIns; q++) dma16(px[q] + st * 128, slot + kWBytes + (wave * kXIns + q) * 1024);
+            if (lane < 32) dma16(pi + st * 256, slot + kWBytes + kXBytes + wave * 512);
+        };
+        // Waits for this wave's DMAs of stage kt when `later` stages were issued after it.
+        auto wait_stage = [&](int later) {
+            switch (later) {
+            case 0: wait_vmcnt<0>(); break;
+            case 1: wait_vmcnt<kVm>(); break;
+            case 2: wait_vmcnt<2 * kVm>(); break;
+            case 3: wait_vmcnt<3 * kVm>(); break;
+            case 4: wait_vmcnt<4 * kVm>(); break;
+            case 5: wait_vmcnt<5 * kVm>(); break;
+            default: wait_vmcnt<(D - 2) * kVm>(); break;
+            }
+        };
+        for (int d = 0; d < D - 1; d++)
+            if (d < nst) issue(d);
+        for (int kt = 0; kt < nst; kt++) {
+            const int later = (nst - 1 - kt) < (D - 2) ? (nst - 1 - kt) : (D - 2);
+            wait_stage(later);
+            lds_barrier();
+            if (kt + D - 1 < nst) issue(kt + D - 1);
+            const int8_t* Ws = slot_of(kt);
+            const int8_t* Xs = Ws + kWBytes;
+            const uint32_t* Is = reinterpret_cast<const uint32_t*>(Xs + kXBytes);
+            v4i a[kTN];
+            int idx[kTN];
+            v8i b[kTM];
+#pragma unroll
+            for (int i = 0; i < kTN; i++) {
+                a[i] = *reinterpret_cast<const v4i*>(Ws + lds_off64(wn + 16 * i + r16, g));
+                idx[i] = static_cast<int>(Is[((wn >> 4) + i) * 64 + lane]);
+            }
+#pragma unroll
+            for (int j = 0; j < kTM; j++) {
+                const int r = wm + 16 * j + r16;
+                const v4i lo = *reinterpret_cast<const v4i*>(Xs + lds_off128(r, g));
+                const v4i hi = *reinterpret_cast<const v4i*>(Xs + lds_off128(r, g + 4));
+                b[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+#pragma unroll
+            for (int j = 0; j < kTM; j++)
+#pragma unroll
+                for (int i = 0; i < kTN; i++)
+                    acc[i][j] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a[i], b[j], acc[i][j], idx[i], 0, 0);
+        }
+    }
+};
+
+constexpr int kSpRingSlots = 8;
+
+// Lane l of block (i, j) holds outputs (m = 16 j + l % 16, n = 16 i + 4 (l / 16) + e): one
+// 8-byte FP16 or 16-byte INT32 store each (N % 16 == 0, so the 4 columns are in or out together).
+template <bool DEQUANT>
+__global__ __launch_bounds__(256) void sparse_ring_kernel(const int8_t* __restrict__ W, const int8_t* __restrict__ X,
+                                                          const uint32_t* __restrict__ meta, GemmEpilogue ep,
+                                                          int tiles_n, int tiles_m, int K)
+{
+    using T = SpRingTile<kSpRingSlots>;
+    extern __shared__ __align__(16) int8_t lds[];
+    int tn, tm;
+    tile_coords(blockIdx.x, tiles_n, tiles_m, tn, tm);
+    const int n0 = tn * T::BNW, m0 = tm * T::BMT;
+    T t;
+    t.run(W, X, meta, ep.M, ep.N, K, n0, m0, lds);
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int wn = n0 + (wave >> 1) * (T::BNW / 2), wm = m0 + (wave & 1) * (T::BMT / 2);
+    const int M = ep.M, N = ep.N;
+#pragma unroll
+    for (int j = 0; j < T::kTM; j++) {
+        const int m = wm + 16 * j + (lane & 15);
+        if (m >= M) continue;
+        const float as = DEQUANT ? ep.act_scale[m] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < T::kTN; i++) {
+            const int n = wn + 16 * i + 4 * (lane >> 4);
+            if (n >= N) continue;
+            const size_t o = static_cast<size_t>(m) * N + n;
+            if constexpr (DEQUANT) {
+                uint16_t h[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float bv = ep.bias ? h2f(ep.bias[n + e]) : 0.0f;
+                    h[e] = dequant_gemm(t.acc[i][j][e], as, h2f(ep.w_scale[n + e]), bv, ep.bias != nullptr);
+                }
+                *reinterpret_cast<uint2*>(ep.c16 + o) =
+                    make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+            } else {
+                *reinterpret_cast<int4*>(ep.c32 + o) =
+                    make_int4(t.acc[i][j][0], t.acc[i][j][1], t.acc[i][j][2], t.acc[i][j][3]);
+            }
+        }
+    }
+}
+
+template <bool DEQUANT>
+static int launch_sparse_ring(const int8_t* W, const int8_t* X, const uint32_t* meta, const GemmEpilogue& ep, int K,
+                              hipStream_t s)
+{
+    using T = SpRingTile<kSpRingSlots>;
+    constexpr int lds = T::kLdsBytes;
+    const int tiles_n = divup(ep.N, T::BNW), tiles_m = divup(ep.M, T::BMT);
+    const long long total = static_cast<long long>(tiles_n) * tiles_m;
+    if (total > 0x7FFFFFFFLL) return FORGE_EINVAL;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&sparse_ring_kernel<DEQUANT>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (attr != hipSuccess) return static_cast<int>(attr);
+    sparse_ring_kernel<DEQUANT><<<static_cast<unsigned>(total), 256, lds, s>>>(W, X, meta, ep, tiles_n, tiles_m, K);
+    return launch_status();
+}
+
 // ---- tile configurations ----------------------------------------------------------
 
 constexpr int kSpTileBW[FORGE_SPARSE_NUM_TILES] = {256, 128, 128};
@@ -777,20 +955,31 @@ static int cu_count_or_default() {
     return (st == FORGE_OK && d.cu_count > 0) ? d.cu_count : default_cu_count();
 }
 
-// Unsplit DMA engine choice for M > 128: 256 weight rows x 256 tokens (sparse_dma32) or x 128
-// tokens (sparse_dma<128>). Both stream about the same bytes per CU per microsecond on MI355X,
-// so a 128-deep stage costs in proportion to its bytes (52 KB: ~1.16 us; 36 KB: ~0.80 us) and
-// the wider tile wins only where its tile waves are not much emptier: measured, 1536x6144 at
-// M = 1024 (96 vs 192 tiles) 20.0 vs 15.6 us, 6144x1536 at M = 4096 55.7 vs 43.4 us, while
-// configs[2] (688 vs 1376 tiles) runs 1.4x faster on the wide tile. Fixed cost per tile wave:
-// ring fill and the epilogue.
-static bool sparse_prefer_wide(int M, int N, int K, int cu)
+// Unsplit DMA engine choice (automatic plans, M > 64, K % 128 == 0): 256 weight rows x 256
+// tokens (sparse_dma32, M > 128), x 128 tokens (sparse_dma<128>), or the 128 x 64 ring engine
+// (sparse_ring). A tile wave costs stages x stage time + a fixed part (ring fill, epilogue),
+// with stage times measured on MI355X: the two 256-row engines stream about the same bytes per
+// CU per microsecond, so their stages cost in proportion to their bytes (52 KB: ~1.16 us; 36 KB:
+// ~0.80 us); a ring stage (18 KB) costs ~0.62 us. Measured: 1536x6144 at M = 1024 256x128
+// 15.6 us (256x256 20.0); 6144x1536 at M = 4096 256x128 43.0 us (256x256 55.7, ring 86.2);
+// 6144x1536 at M = 1024 ring 30.3 us (256x128 39.8); configs[2] on 256x256.
+enum class SpEngine { k256x256, k256x128, kRing };
+
+static SpEngine sparse_pick_engine(int M, int N, int K, int cu)
 {
-    const long long tn = divup(N, 256);
     const double steps = static_cast<double>(divup(K, kSpStep));
-    const double w256 = static_cast<double>(divupll(tn * divup(M, 256), cu));
-    const double w128 = static_cast<double>(divupll(tn * divup(M, 128), cu));
-    return w256 * (1.16 * steps + 4.0) <= w128 * (0.80 * steps + 3.0);
+    const long long tn256 = divup(N, 256), tn128 = divup(N, 128);
+    const double w128 = static_cast<double>(divupll(tn256 * divup(M, 128), cu));
+    const double wring = static_cast<double>(divupll(tn128 * divup(M, 64), cu));
+    double best = w128 * (0.80 * steps + 3.0);
+    SpEngine e = SpEngine::k256x128;
+    if (M > 128) {
+        const double w256 = static_cast<double>(divupll(tn256 * divup(M, 256), cu));
+        const double t = w256 * (1.16 * steps + 4.0);
+        if (t <= best) { best = t; e = SpEngine::k256x256; }
+    }
+    if (wring * (0.62 * steps + 1.5) < best) e = SpEngine::kRing;
+    return e;
 }
 
 int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, const float* act_scale,
@@ -842,16 +1031,20 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
         splitk_finalize_kernel<<<fblocks, 256, 0, s>>>(ws, act_scale, w_scale, bias, out16, N, total);
         return launch_status();
     }
-    // Unsplit plans on 128-deep K stages run on the DMA-fed engine: 256 weight rows x 256
-    // tokens when the planner chose freely, x 128 tokens for the reference's 256x128 tile.
+    // Unsplit plans on 128-deep K stages run on the DMA-fed engines: chosen by tile waves when
+    // the planner chose freely, 256 weight rows x 128 tokens for the reference's 256x128 tile.
     if (K % 128 == 0 && M > 64 && (tile == FORGE_SPARSE_TILE_AUTO || pt == FORGE_SPARSE_TILE_256x128) &&
         (tile == FORGE_SPARSE_TILE_AUTO || tile == FORGE_SPARSE_TILE_256x128)) {
         void* o = out16 ? static_cast<void*>(out16) : static_cast<void*>(out32);
         GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N, aligned(o, 16) ? 1 : 0};
-        const bool wide = tile == FORGE_SPARSE_TILE_AUTO && M > 128 && sparse_prefer_wide(M, N, K, cu_count_or_default());
-        if (wide)
+        const SpEngine e = tile == FORGE_SPARSE_TILE_AUTO ? sparse_pick_engine(M, N, K, cu_count_or_default())
+                                                          : SpEngine::k256x128;
+        if (e == SpEngine::k256x256)
             return out16 ? launch_sparse_dma32<true>(W_comp, x, meta, ep, K, s)
                          : launch_sparse_dma32<false>(W_comp, x, meta, ep, K, s);
+        if (e == SpEngine::kRing)
+            return out16 ? launch_sparse_ring<true>(W_comp, x, meta, ep, K, s)
+                         : launch_sparse_ring<false>(W_comp, x, meta, ep, K, s);
         return out16 ? launch_sparse_dma<128, true>(W_comp, x, meta, ep, K, s)
                      : launch_sparse_dma<128, false>(W_comp, x, meta, ep, K, s);
     }

@@ -167,3 +167,47 @@ def test_config3_full_size_sampled(dev, orc):
     say("config3 sparse 4096x11008x4096")
     C = to_host(ops.sparse_int8_gemm_s32(comp, to_dev(x, dev), meta))
     assert np.array_equal(C[rows], ref)
+
+
+# Automatic plans on each unsplit DMA engine, chosen by tile waves: the 128 x 64 ring engine
+# (narrow N or few token tiles with deep K: fewer stages than ring slots, more, partial last
+# token tile, partial last 16-row weight block), the 256 x 128 engine and the 256 x 256 one.
+ENGINE_SHAPES = [
+    (200, 2048, 256),    # ring: 4 token tiles (last 8 rows), 2 weight tiles
+    (100, 384, 144),     # ring: 3 stages (< 7 in flight), weight tile of 144 rows (+16)
+    (1024, 6144, 1536),  # ring: the reference benchmark's narrow deep-K layer
+    (512, 128, 2048),    # 256 x 128 engine: one stage
+    (1024, 1536, 6144),  # 256 x 128 engine
+    (600, 4096, 4096),   # 256 x 256 engine (ragged token tile)
+]
+
+
+@pytest.mark.parametrize("M,K,N", ENGINE_SHAPES)
+def test_sparse_auto_engines(dev, orc, M, K, N):
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(M + 3 * K + 7 * N)
+    W = int8_uniform(rng, (N, K))
+    x = int8_uniform(rng, (M, K))
+    act = rng.uniform(0.001, 0.05, M).astype(np.float32)
+    ws = rng.uniform(0.001, 0.05, N).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
+    rows = np.unique(np.r_[0:17, M // 2, M - 70:M])
+    rows = rows[rows < M]
+    cr, mr = orc.prune_compress_24(W)
+    acc = orc.sparse_gemm_s32(cr, x[rows], mr, N, K)
+    comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+    raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+    meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+    ops.prune_compress_24(to_dev(W, dev), comp, raw, N, K)
+    ops.pack_metadata(raw, meta, N, K)
+    say(f"sparse auto engine M={M} K={K} N={N}")
+    xd = to_dev(x, dev)
+    C = torch.empty((M, N), dtype=torch.int32, device=dev)
+    poison(C, 0x7B)
+    assert np.array_equal(to_host(ops.sparse_int8_gemm_s32(comp, xd, meta, out=C))[rows], acc)
+    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    poison(Y, 0x7B)
+    ops.sparse_int8_gemm(comp, xd, meta, to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev), split_k=0, out=Y)
+    ref = orc.dequant_epilogue(acc, act[rows], ws, b).view(np.uint16)
+    assert np.array_equal(to_host(Y)[rows].view(np.uint16), ref)
