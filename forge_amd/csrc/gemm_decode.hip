@@ -5,8 +5,9 @@
 // with a handful of tokens, src/gemm/int8_sparse.cu:1005-1043, src/gemm/int8_dense.cu:213-232),
 // where the weights are read once per call and every other operand is tiny.
 //
-// Dense (decode_dense_kernel): a 256-thread workgroup owns 32 weight rows (16 for up to 4
-// tokens) and all of K; its 4 wavefronts split K into contiguous slices of 128-deep stages.
+// Dense (decode_dense_kernel): a workgroup owns 32 weight rows (16 for up to 4 tokens) and all
+// of K; its wavefronts (8 with 32 rows, 4 with 16) split K into contiguous slices of 128-deep
+// stages.
 // Operands are loaded straight into registers with coalesced 8-row x 128-byte instructions
 // (non-temporal for the weights, which are read once), rearranged into the matrix-core layout
 // by one DPP lane swap, and fed to v_mfma_i32_16x16x64_i8. Measured on MI355X, this streams a
@@ -44,6 +45,8 @@ constexpr int kDecTokRows = 16;    // token rows staged per stage (the MFMA's 16
 constexpr int kDecDenseBlocks = 2;
 constexpr int kDecDenseOneBlockMaxM = 4;   // one 16-row block per workgroup up to this many tokens
 constexpr int kDecDenseWaves = 4;
+constexpr int kDecDenseWavesTwoBlock = 8;   // 8 tokens and more: measured 17.96 -> 17.47 us at M = 16
+                                            // (graph-replayed int8_linear); 4 waves stay faster at M <= 4
 constexpr int kDecDenseAhead = 6;
 constexpr int kDecSparseRegMaxM = 8;   // register sparse kernel up to this many tokens
 
@@ -920,8 +923,8 @@ int launch_decode(const int8_t* W, const uint32_t* meta, const int8_t* X, const 
     if (ep.M <= kDecDenseOneBlockMaxM)
         return ep.c16 ? launch_decode_dense<true, 1, kDecDenseWaves, kDecDenseAhead>(W, X, ep, K, s)
                       : launch_decode_dense<false, 1, kDecDenseWaves, kDecDenseAhead>(W, X, ep, K, s);
-    return ep.c16 ? launch_decode_dense<true, kDecDenseBlocks, kDecDenseWaves, kDecDenseAhead>(W, X, ep, K, s)
-                  : launch_decode_dense<false, kDecDenseBlocks, kDecDenseWaves, kDecDenseAhead>(W, X, ep, K, s);
+    return ep.c16 ? launch_decode_dense<true, kDecDenseBlocks, kDecDenseWavesTwoBlock, kDecDenseAhead>(W, X, ep, K, s)
+                  : launch_decode_dense<false, kDecDenseBlocks, kDecDenseWavesTwoBlock, kDecDenseAhead>(W, X, ep, K, s);
 }
 
 }  // namespace forge_amd
