@@ -19,7 +19,8 @@ what the same counters read for a device copy of known size in the same runs.
 extra: configs[2] (2:4 sparse vs dense at 4096x11008x4096), configs[3] (decode
 M = 1/4/16, N = K = 8192, dense and 2:4, HBM GB/s with 6 rotating weight copies so the
 256 MB MALL cannot hold them; calls captured into a HIP graph and replayed so host launch
-overhead is not timed), configs[4] (INT8 NHWC 3x3 conv, INT32 and dequant outputs), and
+overhead is not timed; the whole int8_linear / sparse_int8_linear, and the GEMM alone on
+pre-quantized tokens, *_gemm_*), configs[4] (INT8 NHWC 3x3 conv, INT32 and dequant outputs), and
 the rest of the INT8 conv family on NCHW FP16 maps: depthwise 3x3 (1, 64, 540, 960) and
 ConvTranspose2d k2s2 (1, 64, 270, 480) -> (1, 32, 540, 960), as time and HBM GB/s of
 input + output bytes; and SparseLinear's weight preparation at 11008 x 4096 fp32, one pass
@@ -334,6 +335,20 @@ def bench_extra(dev):
         out[f"c4_M{M}_sparse_GBs"] = bytes_s / ts / 1e6
         out[f"c4_M{M}_dense_us"] = td * 1e3
         out[f"c4_M{M}_sparse_us"] = ts * 1e3
+        # The decode GEMM alone (the gate's "decode-shape GEMM"): on the quantized tokens left in
+        # the scratch, INT8 tokens in its algorithmic bytes.
+        ops.fused_quantize_activation(xh, M, K, out=sq, scales=ss)
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        gd = [lambda c=c: ops.int8_gemm_dequant(sq, Ws[c], ss, ws, b, out=y) for c in range(copies)]
+        gs = [lambda c=c: ops.sparse_int8_gemm(comps[c], sq, metas[c], ss, ws, b, out=y) for c in range(copies)]
+        tgd = graph_time_ms(gd * 6)
+        tgs = graph_time_ms(gs * 6)
+        gbytes_d = N * K + M * K + M * N * 2 + N * 4 + M * 4
+        gbytes_s = N * K // 2 + N * K // 8 + M * K + M * N * 2 + N * 4 + M * 4
+        out[f"c4_M{M}_dense_gemm_us"] = tgd * 1e3
+        out[f"c4_M{M}_dense_gemm_GBs"] = gbytes_d / tgd / 1e6
+        out[f"c4_M{M}_sparse_gemm_us"] = tgs * 1e3
+        out[f"c4_M{M}_sparse_gemm_GBs"] = gbytes_s / tgs / 1e6
     del Ws, comps, metas
     torch.cuda.empty_cache()
 
