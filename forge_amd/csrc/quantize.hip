@@ -74,9 +74,10 @@ __global__ __launch_bounds__(256) void quantize_rows_block_kernel(
     }
 }
 
-// Short rows (K <= 2048) at large M: one wavefront per row, 4 rows per workgroup, so a
-// workgroup moves 4 rows and the grid is M/4 workgroups instead of M tiny ones (at
-// M = 147,456, K = 1280 the per-row workgroups ran at 3.6 TB/s). Lane t holds vectors t, t + 64,
+// Rows up to K = 4096 at large M: one wavefront per row, 4 rows per workgroup, so a workgroup
+// moves 4 rows, needs no barrier, and the grid is M/4 workgroups instead of M (at M = 147,456,
+// K = 1280 the per-row workgroups ran at 3.6 TB/s; configs[1], 4096 x 4096: 9.3 -> 8.3 us,
+// 6.06 TB/s of 50.3 MB). Lane t holds vectors t, t + 64,
 // ... of its row; loads, absmax and quantization as in the kernel above, the absmax reduced
 // within the wave by DPP.
 template <int VPT>
@@ -299,12 +300,13 @@ constexpr int kWaveRowsMinM = 2048;
 int launch_quantize(const uint16_t* x, int8_t* q, float* scales, int M, int K, hipStream_t s)
 {
     const bool vec_ok = (K % 8 == 0) && K <= 8 * 2048 && aligned(x, 16) && aligned(q, 8);
-    if (vec_ok && K <= 2048 && M >= kWaveRowsMinM) {
+    if (vec_ok && K <= 4096 && M >= kWaveRowsMinM) {
         const int vpt = divup(K, 8 * kWave);
         const unsigned grid = static_cast<unsigned>(divup(M, 4));
         if (vpt <= 1)      quantize_rows_wave_kernel<1><<<grid, 256, 0, s>>>(x, q, scales, M, K);
         else if (vpt <= 2) quantize_rows_wave_kernel<2><<<grid, 256, 0, s>>>(x, q, scales, M, K);
-        else               quantize_rows_wave_kernel<4><<<grid, 256, 0, s>>>(x, q, scales, M, K);
+        else if (vpt <= 4) quantize_rows_wave_kernel<4><<<grid, 256, 0, s>>>(x, q, scales, M, K);
+        else               quantize_rows_wave_kernel<8><<<grid, 256, 0, s>>>(x, q, scales, M, K);
         return launch_status();
     }
     if (vec_ok) {

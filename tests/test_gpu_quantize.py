@@ -82,7 +82,8 @@ def test_quantize_outlier_rows_and_ties(dev, orc):
 
 # Shapes reaching each kernel: block kernel VPT 1 / 2 / 8, wave kernel VPT 1 / 2 / 4 (ragged
 # last workgroup at 2050 rows), and the scalar kernel (K % 8 != 0).
-SPECIAL_CASES = [(9, 1024), (16, 4096), (4, 16384), (2050, 8), (2048, 1000), (2051, 2048), (6, 1003)]
+SPECIAL_CASES = [(9, 1024), (16, 4096), (4, 16384), (2050, 8), (2048, 1000), (2051, 2048), (6, 1003),
+                 (2049, 3072), (2048, 4096)]   # wave-per-row kernel with 6 and 8 vectors per lane
 
 
 @pytest.mark.parametrize("M,K", SPECIAL_CASES)
