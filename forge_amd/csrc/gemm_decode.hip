@@ -35,6 +35,8 @@
 #include "gemm_dense.h"
 #include "mfma_tile.h"
 
+#include <mutex>
+
 namespace forge_amd {
 
 // Sparse decode geometry.
@@ -268,6 +270,44 @@ struct FqArgs {
     int8_t* q;           // (M, K) INT8 scratch, 8-byte aligned, or null (not written)
     float* scale;        // (M,) scratch (written with q)
 };
+
+// K split across the workgroups of one row block: acc holds gridDim.x x RB x 256 INT32 sums
+// (16 x 16 outputs per 16-row block), cnt one arrival counter per row block; both are zero
+// between launches (the last workgroup of a row block leaves them so).
+struct KSplit {
+    int* acc;
+    unsigned* cnt;
+};
+
+// Exact INT32 hand-off between the KP workgroups of a row block, through device-scope atomics
+// only (no cache write-back or invalidate fences, which stall every workgroup on the XCD):
+// every workgroup adds its lane partials (threads with `has` set, 16-row block `blk`) into the
+// row block's sums, waits for the adds to complete, and one thread counts the arrival with
+// atomicInc(cnt, KP - 1), which wraps the counter back to 0 on the last arrival. Workgroups
+// that arrive earlier return false; the last one takes the sums with atomicExch(..., 0), which
+// clears them for the next launch, and returns true. No workgroup waits for another, so the
+// hand-off cannot stall on a workgroup that is not resident. INT32 addition is associative, so
+// the result is exact in any arrival order.
+template <int KP>
+__device__ bool ksplit_handoff(const KSplit& ks, v4i& sum, bool has, int blk, int lane)
+{
+    __shared__ int s_last;
+    int* slot = ks.acc + static_cast<size_t>(blk) * 4 * kWave + lane;
+    if (has) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) atomicAdd(slot + e * kWave, sum[e]);
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (threadIdx.x == 0) s_last = atomicInc(ks.cnt + blockIdx.x, KP - 1) == KP - 1;
+    __syncthreads();
+    if (!s_last) return false;
+    if (has) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) sum[e] = atomicExch(slot + e * kWave, 0);
+    }
+    return true;
+}
 constexpr int kFqPad = 128;
 constexpr int kFqTokAhead = 2;   // token stages read from LDS ahead of their MFMAs
 constexpr int kFqTokBytes = kDecodeFqMaxM * (kDecodeMaxK + kFqPad);
@@ -409,11 +449,16 @@ __device__ __forceinline__ void decode_epilogue_blocks(const v4i* red, const Gem
 
 // VPR > 0: fused quantize (fq_quantize_tokens with VPR vectors per thread per row); the tokens
 // are then read from LDS instead of X.
-template <bool DEQUANT, int S, int RB, int WV, int AH, int VPR = 0>
+// KP > 1: the KP workgroups blockIdx.y = 0..KP-1 of a row block each take one contiguous K/KP
+// range and hand their INT32 partials over through ks (ksplit_handoff), so that a row block
+// can be taller (each workgroup reads 16 token rows per 16 x RB weight rows) at the same
+// number of workgroups.
+template <bool DEQUANT, int S, int RB, int WV, int AH, int VPR = 0, int KP = 1>
 __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void decode_dense_kernel(
-    const int8_t* __restrict__ W, const int8_t* __restrict__ X, GemmEpilogue ep, int K, FqArgs fq)
+    const int8_t* __restrict__ W, const int8_t* __restrict__ X, GemmEpilogue ep, int K, FqArgs fq, KSplit ks)
 {
     constexpr bool FQ = VPR > 0;
+    static_assert(!(FQ && KP > 1), "the fused quantize prologue needs the whole token rows");
     __shared__ v4i red[WV * RB * kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -421,8 +466,10 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
     const int M = ep.M, N = ep.N;
     const int r16 = lane & 15, g = lane >> 4;
     const bool hi = (lane >> 3) & 1;
+    const int kp = KP > 1 ? static_cast<int>(blockIdx.y) : 0;
+    const int k0 = kp * (K / KP);
 
-    const int nst = K / 128;
+    const int nst = K / KP / 128;
     const int s0 = wave * S < nst ? wave * S : nst;
     const int ns = (s0 + S < nst ? s0 + S : nst) - s0;
 
@@ -433,7 +480,7 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int r = n0 + 16 * b + 8 * j + (lane & 7);
-            pw[b][j] = W + static_cast<size_t>(r < N ? r : N - 1) * K + 16 * (lane >> 3);
+            pw[b][j] = W + static_cast<size_t>(r < N ? r : N - 1) * K + k0 + 16 * (lane >> 3);
         }
     [[maybe_unused]] int8_t* ftok = nullptr;
     [[maybe_unused]] float* fscale = nullptr;
@@ -448,7 +495,7 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
     for (int j = 0; j < 2; j++) {
         const int r = 8 * j + (lane & 7);
         if constexpr (FQ) px[j] = ftok + (r < M ? r : M - 1) * (K + kFqPad) + 16 * (lane >> 3);
-        else px[j] = X + static_cast<size_t>(r < M ? r : M - 1) * K + 16 * (lane >> 3);
+        else px[j] = X + static_cast<size_t>(r < M ? r : M - 1) * K + k0 + 16 * (lane >> 3);
     }
     const bool tok = r16 < M;   // after the swap, lane l holds token row l % 16
 
@@ -542,11 +589,17 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
 #pragma unroll
     for (int b = 0; b < RB; b++) red[(wave * RB + b) * kWave + lane] = acc[b];
     __syncthreads();
+    v4i sum = v4i{0, 0, 0, 0};
+    if (wave < RB) {
+        sum = red[wave * kWave + lane];
+#pragma unroll
+        for (int w = 1; w < WV; w++) sum += red[(w * RB + wave) * kWave + lane];
+    }
+    if constexpr (KP > 1) {
+        if (!ksplit_handoff<KP>(ks, sum, wave < RB, blockIdx.x * RB + wave, lane)) return;
+    }
     if (wave < RB) {
         const int b = wave;
-        v4i sum = red[b * kWave + lane];
-#pragma unroll
-        for (int w = 1; w < WV; w++) sum += red[(w * RB + b) * kWave + lane];
         const int m = r16;
         if (m < M) {
             const int nb = n0 + 16 * b + 4 * g;
@@ -768,19 +821,124 @@ static int launch_decode_sparse_reg(const int8_t* W, const uint32_t* meta, const
     return launch_status();
 }
 
-template <bool DEQUANT, int RB, int WV, int AH>
-static int launch_decode_dense(const int8_t* W, const int8_t* X, const GemmEpilogue& ep, int K, hipStream_t s)
+// K split for narrow N (row blocks fewer than CUs): the KP workgroups of a row block each take
+// K / KP and hand their sums over (ksplit_handoff). The sums and counters live in static device
+// slots, zero when the code object loads and left zero by every launch, one slot per stream, so
+// calls on different streams never share one (calls on one stream run in order) and nothing is
+// allocated. Measured at M = 16, K = 8192 (128 and 32 row blocks of 32 rows): N = 4096
+// 13.6 -> 9.9 us, N = 1000 13.2 -> 8.8 us. Where the row blocks already fill the chip the split
+// only adds the hand-off (N = 8192: 14.4 -> 15.2 us), so it is not used there.
+constexpr int kKSplitSlots = 8;
+constexpr int kKSplitMaxBlocks = 512;   // 16-row blocks per slot (N <= 8192)
+constexpr int kKSplitMaxParts = 8;
+static __device__ int g_ksplit_acc[kKSplitSlots * kKSplitMaxBlocks * 4 * kWave];
+static __device__ unsigned g_ksplit_cnt[kKSplitSlots * kKSplitMaxBlocks];
+
+// The K-split slot of stream s on the current device, or {} (no split) when every slot is held
+// by another stream, for hipStreamPerThread (one handle for many host threads' streams), or
+// when the slot symbols cannot be resolved. A slot stays with its stream until the process ends.
+static KSplit ksplit_slot(hipStream_t s)
 {
-    const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
-    const int per = divup(K / 128, WV);
-#define FORGE_DEC_DENSE(SS) decode_dense_kernel<DEQUANT, SS, RB, WV, AH><<<grid, WV * kWave, 0, s>>>(W, X, ep, K, FqArgs{})
+    constexpr int kMaxDev = 64;
+    static std::mutex mu;
+    static int* acc[kMaxDev];
+    static unsigned* cnt[kMaxDev];
+    static bool failed[kMaxDev];
+    static hipStream_t owner[kMaxDev][kKSplitSlots];
+    static int used[kMaxDev];
+    if (s == hipStreamPerThread) return {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+        (void)hipGetLastError();
+        return {};
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!acc[dev] && !failed[dev]) {
+        void* a = nullptr;
+        void* c = nullptr;
+        if (hipGetSymbolAddress(&a, HIP_SYMBOL(g_ksplit_acc)) != hipSuccess ||
+            hipGetSymbolAddress(&c, HIP_SYMBOL(g_ksplit_cnt)) != hipSuccess) {
+            (void)hipGetLastError();
+            failed[dev] = true;
+        } else {
+            acc[dev] = static_cast<int*>(a);
+            cnt[dev] = static_cast<unsigned*>(c);
+        }
+    }
+    if (failed[dev]) return {};
+    int slot = -1;
+    for (int i = 0; i < used[dev]; i++)
+        if (owner[dev][i] == s) slot = i;
+    if (slot < 0) {
+        if (used[dev] == kKSplitSlots) return {};
+        slot = used[dev]++;
+        owner[dev][slot] = s;
+    }
+    return {acc[dev] + static_cast<size_t>(slot) * kKSplitMaxBlocks * 4 * kWave,
+            cnt[dev] + static_cast<size_t>(slot) * kKSplitMaxBlocks};
+}
+
+// K parts for a dense decode launch: doubled while twice the workgroups still fit 1.25 waves
+// of CUs and each part stays at least 1024 deep in whole 128-deep stages; no split below
+// K = 4096, where one launch is already near its fixed cost. Measured (K = 8192, M = 16 / 1):
+// N = 4096 13.5 -> 9.9 us (2 parts), N = 2048 13.5 -> 7.5 us (4), N = 1024 13.3 / 7.2 -> 6.6 /
+// 5.9 us (8 / 4); K = 2048 splits measured slower at every N.
+constexpr int kKSplitMinK = 4096;
+constexpr int kKSplitMinPartK = 1024;
+
+static int decode_dense_kparts(int N, int K, int rb, int cu)
+{
+    const int g = divup(N, 16 * rb);
+    if (K < kKSplitMinK || g * rb > kKSplitMaxBlocks) return 1;
+    int kp = 1;
+    while (kp < kKSplitMaxParts && 2 * g * kp * 4 <= 5 * cu && K % (256 * kp) == 0 && K / (2 * kp) >= kKSplitMinPartK)
+        kp *= 2;
+    return kp;
+}
+
+template <bool DEQUANT, int RB, int WV, int AH, int KP>
+static int launch_decode_dense_kp(const int8_t* W, const int8_t* X, const GemmEpilogue& ep, int K, const KSplit& ks,
+                                  hipStream_t s)
+{
+    const dim3 grid(static_cast<unsigned>(divup(ep.N, 16 * RB)), KP);
+    const int per = divup(K / KP / 128, WV);
+    // Largest per-wave stage count K <= kDecodeMaxK can need at this KP (no larger S is built).
+    constexpr int SM = kDecodeMaxK / 128 / KP / WV > 1 ? kDecodeMaxK / 128 / KP / WV : 1;
+    constexpr int S2 = 2 < SM ? 2 : SM, S4 = 4 < SM ? 4 : SM, S8 = 8 < SM ? 8 : SM, S16 = 16 < SM ? 16 : SM;
+#define FORGE_DEC_DENSE(SS) \
+    decode_dense_kernel<DEQUANT, SS, RB, WV, AH, 0, KP><<<grid, WV * kWave, 0, s>>>(W, X, ep, K, FqArgs{}, ks)
     if (per <= 1) FORGE_DEC_DENSE(1);
-    else if (per <= 2) FORGE_DEC_DENSE(2);
-    else if (per <= 4) FORGE_DEC_DENSE(4);
-    else if (per <= 8) FORGE_DEC_DENSE(8);
-    else FORGE_DEC_DENSE(16);
+    else if (per <= 2) FORGE_DEC_DENSE(S2);
+    else if (per <= 4) FORGE_DEC_DENSE(S4);
+    else if (per <= 8) FORGE_DEC_DENSE(S8);
+    else FORGE_DEC_DENSE(S16);
 #undef FORGE_DEC_DENSE
     return launch_status();
+}
+
+// kp = 0: choose the K parts (decode_dense_kparts); otherwise that many (1, 2, 4 or 8; the
+// caller checks K % (128 kp) == 0). Without a free slot the launch is not split.
+template <bool DEQUANT, int RB, int WV, int AH>
+static int launch_decode_dense(const int8_t* W, const int8_t* X, const GemmEpilogue& ep, int K, hipStream_t s,
+                               int kp = 0)
+{
+    if (kp == 0) {
+        int st = FORGE_OK;
+        const DeviceInfo& di = device_info(&st);
+        if (st != FORGE_OK) return st;
+        kp = decode_dense_kparts(ep.N, K, RB, di.cu_count);
+    }
+    KSplit ks{};
+    if (kp > 1) {
+        ks = ksplit_slot(s);
+        if (!ks.acc) kp = 1;
+    }
+    switch (kp) {
+    case 2: return launch_decode_dense_kp<DEQUANT, RB, WV, AH, 2>(W, X, ep, K, ks, s);
+    case 4: return launch_decode_dense_kp<DEQUANT, RB, WV, AH, 4>(W, X, ep, K, ks, s);
+    case 8: return launch_decode_dense_kp<DEQUANT, RB, WV, AH, 8>(W, X, ep, K, ks, s);
+    default: return launch_decode_dense_kp<DEQUANT, RB, WV, AH, 1>(W, X, ep, K, ks, s);
+    }
 }
 
 template <bool DEQUANT>
@@ -884,7 +1042,7 @@ static int launch_decode_fq_vpr(const int8_t* W, const uint32_t* meta, const Gem
     const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
     const int per = divup(K / 128, WV);
 #define FORGE_DEC_FQ_DENSE(SS) \
-    decode_dense_kernel<true, SS, RB, WV, AH, VPR><<<grid, WV * kWave, 0, s>>>(W, nullptr, ep, K, fq)
+    decode_dense_kernel<true, SS, RB, WV, AH, VPR><<<grid, WV * kWave, 0, s>>>(W, nullptr, ep, K, fq, KSplit{})
     if (per <= 1) FORGE_DEC_FQ_DENSE(1);
     else if (per <= 2) FORGE_DEC_FQ_DENSE(2);
     else if (per <= 4) FORGE_DEC_FQ_DENSE(4);

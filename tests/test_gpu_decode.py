@@ -6,7 +6,8 @@ Bar: INT32 bit-exact; FP16 bit-exact to the oracle's epilogue. Shapes exercise t
 K split over 8 wavefronts (K = 128: one wave works; K = 1152: 9 stages, uneven slices and
 idle waves), ragged N (not a multiple of the 32-row workgroup tile), M from 1 to 16 (the
 sparse register kernel for M <= 8 with K % 256 == 0, the DMA-ring kernel otherwise), and
-configs[3] at full size (M = 16 and 1, N = K = 8192; sampled output columns)."""
+configs[3] at full size (M = 16 and 1, N = K = 8192; sampled output columns); narrow N with K
+split across workgroups (exact INT32 hand-off), repeated and on two streams at once."""
 import numpy as np
 import pytest
 
@@ -177,3 +178,59 @@ def test_token_blocks_sparse(dev, orc, M, K, N):
         ops.sparse_int8_gemm(comp, xd, meta, to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev),
                              splitk_workspace=wsp, split_k=split, out=Y)
         assert np.array_equal(to_host(Y).view(np.uint16)[:, cols], ref)
+
+
+# Narrow N with K >= 4096: the dense decode splits K over 2, 4 or 8 workgroups per row block and
+# hands the INT32 sums over through per-stream device slots. Ragged and odd N, 16- and 32-row
+# blocks. Every shape runs twice with new operands: the hand-off must leave its sums and
+# counters at zero for the next launch.
+KSPLIT_DENSE = [(16, 8192, 1000), (1, 8192, 520), (4, 8192, 2048), (12, 4096, 4100), (2, 6144, 777),
+                (9, 8192, 33), (16, 4096, 2047), (7, 4096, 200)]
+
+
+@pytest.mark.parametrize("M,K,N", KSPLIT_DENSE)
+def test_decode_dense_ksplit(dev, orc, M, K, N):
+    import torch
+    from forge_amd import ops
+    for rep in range(2):
+        rng = np.random.default_rng(M * 19 + K + N + 1000 * rep)
+        A = int8_uniform(rng, (M, K))
+        B = int8_uniform(rng, (N, K))
+        act = rng.uniform(0.001, 0.05, M).astype(np.float32)
+        ws = rng.uniform(0.001, 0.05, N).astype(np.float16)
+        b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
+        acc = orc.gemm_s32(A, B)
+        say(f"decode dense K split M={M} K={K} N={N} rep={rep}")
+        Ad, Bd = to_dev(A, dev), to_dev(B, dev)
+        C = torch.empty((M, N), dtype=torch.int32, device=dev)
+        poison(C, 0x7B)
+        assert np.array_equal(to_host(ops.int8_gemm_s32(Ad, Bd, out=C)), acc)
+        Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        poison(Y, 0x7B)
+        ops.int8_gemm_dequant(Ad, Bd, to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev), out=Y)
+        assert np.array_equal(to_host(Y).view(np.uint16), orc.dequant_epilogue(acc, act, ws, b).view(np.uint16))
+
+
+def test_decode_dense_ksplit_two_streams(dev, orc):
+    """Split launches queued on two streams at once, without synchronising between them: each
+    stream has its own sum slots, so every output matches the oracle."""
+    import torch
+    from forge_amd import ops
+    M, K, N, n = 16, 8192, 1000, 6
+    rng = np.random.default_rng(77)
+    xs = [int8_uniform(rng, (M, K)) for _ in range(n)]
+    B = int8_uniform(rng, (N, K))
+    Bd = to_dev(B, dev)
+    Ad = [to_dev(x, dev) for x in xs]
+    outs = [torch.empty((M, N), dtype=torch.int32, device=dev) for _ in range(n)]
+    for o in outs:
+        poison(o, 0x7B)
+    streams = [torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)]
+    torch.cuda.synchronize(dev)
+    say("decode dense K split on two streams")
+    for i in range(n):
+        with torch.cuda.stream(streams[i % 2]):
+            ops.int8_gemm_s32(Ad[i], Bd, out=outs[i])
+    torch.cuda.synchronize(dev)
+    for i in range(n):
+        assert np.array_equal(to_host(outs[i]), orc.gemm_s32(xs[i], B))
