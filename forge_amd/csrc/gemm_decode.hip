@@ -626,13 +626,14 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
 // index nibbles stay valid: the lane's index word is the packed word of 32-K chunk
 // 8 seg + 2 G + h, and the token operand is gathered with the same permutation.
 // VPR > 0 (one token block only): fused quantize, as in decode_dense_kernel.
-template <bool DEQUANT, int S, int RB, int WV, int AH, int TB = 1, int VPR = 0>
+template <bool DEQUANT, int S, int RB, int WV, int AH, int TB = 1, int VPR = 0, int KP = 1>
 __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void decode_sparse_reg_kernel(
     const int8_t* __restrict__ W, const uint32_t* __restrict__ meta, const int8_t* __restrict__ X,
-    GemmEpilogue ep, int K, FqArgs fq)
+    GemmEpilogue ep, int K, FqArgs fq, KSplit ks)
 {
     constexpr bool FQ = VPR > 0;
     static_assert(!FQ || TB == 1, "the fused prologue serves one token block");
+    static_assert(KP == 1 || (!FQ && TB == 1), "the K split serves the plain one-block kernel");
     __shared__ v4i red[WV * RB * TB * kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -640,8 +641,10 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
     const int M = ep.M, N = ep.N;
     const int r16 = lane & 15, g = lane >> 4;
     const bool hi = (lane >> 3) & 1;
+    const int kp = KP > 1 ? static_cast<int>(blockIdx.y) : 0;
+    const int k0 = kp * (K / KP);   // a multiple of 256: k0 / 2 compressed bytes, k0 / 2 index words
 
-    const int nseg = K / 256;
+    const int nseg = K / KP / 256;
     const int s0 = wave * S < nseg ? wave * S : nseg;
     const int ns = (s0 + S < nseg ? s0 + S : nseg) - s0;
 
@@ -654,13 +657,13 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int r = n0 + 16 * b + 8 * j + (lane & 7);
-            pw[b][j] = W + static_cast<size_t>(r < N ? r : N - 1) * (K / 2) + 16 * (lane >> 3);
+            pw[b][j] = W + static_cast<size_t>(r < N ? r : N - 1) * (K / 2) + k0 / 2 + 16 * (lane >> 3);
         }
         // Packed index words of block b: stage s (128 dense K) holds 64 words, the word of
         // (row r, 32-K chunk 4 s + q) at 16 q + r. Chunk 8 seg + 2 g + h lies in stage
         // 2 seg + (2 g + h) / 4 at q = (2 g + h) % 4.
         const int blk = (n0 >> 4) + b < (N >> 4) ? (n0 >> 4) + b : (N >> 4) - 1;
-        const uint32_t* base = meta + static_cast<size_t>(blk) * (K / 2) + r16;
+        const uint32_t* base = meta + static_cast<size_t>(blk) * (K / 2) + k0 / 2 + r16;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int c = 2 * g + h;
@@ -685,7 +688,7 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
         tok[tb] = r < M;
         const int rr = tok[tb] ? r : M - 1;
         if constexpr (FQ) px[tb] = ftok + rr * (K + kFqPad) + 64 * (g >> 1) + 16 * (g & 1);
-        else px[tb] = X + static_cast<size_t>(rr) * K + 64 * (g >> 1) + 16 * (g & 1);
+        else px[tb] = X + static_cast<size_t>(rr) * K + k0 + 64 * (g >> 1) + 16 * (g & 1);
     }
 
     struct Stage { v4i w[RB][2], x[TB][4]; int ix[RB][2]; };
@@ -780,11 +783,19 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
     __syncthreads();
     if constexpr (TB > 1) {
         decode_epilogue_blocks<DEQUANT, RB, TB, WV>(red, ep, n0, wave, lane);
-    } else if (wave < RB) {
-        const int b = wave;
-        v4i sum = red[b * kWave + lane];
+        return;
+    }
+    v4i sum = v4i{0, 0, 0, 0};
+    if (wave < RB) {
+        sum = red[wave * kWave + lane];
 #pragma unroll
-        for (int w = 1; w < WV; w++) sum += red[(w * RB + b) * kWave + lane];
+        for (int w = 1; w < WV; w++) sum += red[(w * RB + wave) * kWave + lane];
+    }
+    if constexpr (KP > 1) {
+        if (!ksplit_handoff<KP>(ks, sum, wave < RB, blockIdx.x * RB + wave, lane)) return;
+    }
+    if (wave < RB) {
+        const int b = wave;
         const int m = r16;
         if (m < M) {
             const int nb = n0 + 16 * b + 4 * g;
@@ -804,21 +815,6 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
             }
         }
     }
-}
-
-template <bool DEQUANT, int RB, int WV, int AH>
-static int launch_decode_sparse_reg(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep,
-                                    int K, hipStream_t s)
-{
-    const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
-    const int per = divup(K / 256, WV);
-#define FORGE_DEC_SPREG(SS) decode_sparse_reg_kernel<DEQUANT, SS, RB, WV, AH><<<grid, WV * kWave, 0, s>>>(W, meta, X, ep, K, FqArgs{})
-    if (per <= 1) FORGE_DEC_SPREG(1);
-    else if (per <= 2) FORGE_DEC_SPREG(2);
-    else if (per <= 4) FORGE_DEC_SPREG(4);
-    else FORGE_DEC_SPREG(8);
-#undef FORGE_DEC_SPREG
-    return launch_status();
 }
 
 // K split for narrow N (row blocks fewer than CUs): the KP workgroups of a row block each take
@@ -941,6 +937,66 @@ static int launch_decode_dense(const int8_t* W, const int8_t* X, const GemmEpilo
     }
 }
 
+template <bool DEQUANT, int RB, int WV, int AH, int KP>
+static int launch_decode_sparse_reg_kp(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep,
+                                       int K, const KSplit& ks, hipStream_t s)
+{
+    const dim3 grid(static_cast<unsigned>(divup(ep.N, 16 * RB)), KP);
+    const int per = divup(K / KP / 256, WV);
+    constexpr int SM = kDecodeMaxK / 256 / KP / WV > 1 ? kDecodeMaxK / 256 / KP / WV : 1;
+    constexpr int S2 = 2 < SM ? 2 : SM, S4 = 4 < SM ? 4 : SM, S8 = 8 < SM ? 8 : SM;
+#define FORGE_DEC_SPREG(SS) \
+    decode_sparse_reg_kernel<DEQUANT, SS, RB, WV, AH, 1, 0, KP><<<grid, WV * kWave, 0, s>>>(W, meta, X, ep, K, FqArgs{}, ks)
+    if (per <= 1) FORGE_DEC_SPREG(1);
+    else if (per <= 2) FORGE_DEC_SPREG(S2);
+    else if (per <= 4) FORGE_DEC_SPREG(S4);
+    else FORGE_DEC_SPREG(S8);
+#undef FORGE_DEC_SPREG
+    return launch_status();
+}
+
+// K parts for the sparse register kernel (up to 8 tokens): as decode_dense_kparts, in whole
+// 256-deep segments, from K = 8192 on and with parts at least 2048 deep (a launch streams half
+// the dense bytes per K). Measured (M = 8 / 1, K = 8192): N = 4096 9.7 / 8.4 -> 8.2 / 7.7 us,
+// N = 1024 9.5 / 8.1 -> 6.3 / 5.8 us; at K = 4096 splits moved times by -0.45 to +0.4 us.
+constexpr int kKSplitMinKSparse = 8192;
+constexpr int kKSplitMinPartKSparse = 2048;
+
+static int decode_sparse_kparts(int N, int K, int rb, int cu)
+{
+    const int g = divup(N, 16 * rb);
+    if (K < kKSplitMinKSparse || g * rb > kKSplitMaxBlocks) return 1;
+    int kp = 1;
+    while (kp < kKSplitMaxParts && 2 * g * kp * 4 <= 5 * cu && K % (512 * kp) == 0 &&
+           K / (2 * kp) >= kKSplitMinPartKSparse)
+        kp *= 2;
+    return kp;
+}
+
+// kp = 0: choose (decode_sparse_kparts); otherwise that many parts (K % (256 kp) == 0).
+template <bool DEQUANT, int RB, int WV, int AH>
+static int launch_decode_sparse_reg(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep,
+                                    int K, hipStream_t s, int kp = 0)
+{
+    if (kp == 0) {
+        int st = FORGE_OK;
+        const DeviceInfo& di = device_info(&st);
+        if (st != FORGE_OK) return st;
+        kp = decode_sparse_kparts(ep.N, K, RB, di.cu_count);
+    }
+    KSplit ks{};
+    if (kp > 1) {
+        ks = ksplit_slot(s);
+        if (!ks.acc) kp = 1;
+    }
+    switch (kp) {
+    case 2: return launch_decode_sparse_reg_kp<DEQUANT, RB, WV, AH, 2>(W, meta, X, ep, K, ks, s);
+    case 4: return launch_decode_sparse_reg_kp<DEQUANT, RB, WV, AH, 4>(W, meta, X, ep, K, ks, s);
+    case 8: return launch_decode_sparse_reg_kp<DEQUANT, RB, WV, AH, 8>(W, meta, X, ep, K, ks, s);
+    default: return launch_decode_sparse_reg_kp<DEQUANT, RB, WV, AH, 1>(W, meta, X, ep, K, ks, s);
+    }
+}
+
 template <bool DEQUANT>
 static int launch_decode_sparse(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep,
                                 int K, hipStream_t s)
@@ -981,7 +1037,7 @@ static int launch_tb_sparse(const int8_t* W, const uint32_t* meta, const int8_t*
     const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
     const int S = pad_stages(divup(K / 256, WV));
 #define FORGE_TB_SPARSE(SS) \
-    decode_sparse_reg_kernel<DEQUANT, SS, RB, WV, AH, TB><<<grid, WV * kWave, 0, s>>>(W, meta, X, ep, K, FqArgs{})
+    decode_sparse_reg_kernel<DEQUANT, SS, RB, WV, AH, TB><<<grid, WV * kWave, 0, s>>>(W, meta, X, ep, K, FqArgs{}, KSplit{})
     switch (S) {
     case 1: FORGE_TB_SPARSE(1); break;
     case 2: FORGE_TB_SPARSE(2); break;
@@ -1030,7 +1086,7 @@ static int launch_decode_fq_vpr(const int8_t* W, const uint32_t* meta, const Gem
         const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
         const int per = divup(K / 256, WV);
 #define FORGE_DEC_FQ_SP(SS) \
-    decode_sparse_reg_kernel<true, SS, RB, WV, AH, 1, VPR><<<grid, WV * kWave, 0, s>>>(W, meta, nullptr, ep, K, fq)
+    decode_sparse_reg_kernel<true, SS, RB, WV, AH, 1, VPR><<<grid, WV * kWave, 0, s>>>(W, meta, nullptr, ep, K, fq, KSplit{})
         if (per <= 1) FORGE_DEC_FQ_SP(1);
         else if (per <= 2) FORGE_DEC_FQ_SP(2);
         else if (per <= 4) FORGE_DEC_FQ_SP(4);

@@ -234,3 +234,36 @@ def test_decode_dense_ksplit_two_streams(dev, orc):
     torch.cuda.synchronize(dev)
     for i in range(n):
         assert np.array_equal(to_host(outs[i]), orc.gemm_s32(xs[i], B))
+
+
+# Sparse register kernel (M <= 8) at K = 8192 with narrow N: 2 or 4 K parts.
+KSPLIT_SPARSE = [(8, 8192, 1008), (1, 8192, 4096), (5, 8192, 2000), (3, 8192, 48)]
+
+
+@pytest.mark.parametrize("M,K,N", KSPLIT_SPARSE)
+def test_decode_sparse_ksplit(dev, orc, M, K, N):
+    import torch
+    from forge_amd import ops
+    for rep in range(2):
+        rng = np.random.default_rng(M * 23 + K + N + 1000 * rep)
+        W = int8_uniform(rng, (N, K))
+        x = int8_uniform(rng, (M, K))
+        act = rng.uniform(0.001, 0.05, M).astype(np.float32)
+        ws = rng.uniform(0.001, 0.05, N).astype(np.float16)
+        b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
+        cr, mr = orc.prune_compress_24(W)
+        acc = orc.sparse_gemm_s32(cr, x, mr, N, K)
+        comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+        raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+        meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+        ops.prune_compress_24(to_dev(W, dev), comp, raw, N, K)
+        ops.pack_metadata(raw, meta, N, K)
+        say(f"decode sparse K split M={M} K={K} N={N} rep={rep}")
+        xd = to_dev(x, dev)
+        C = torch.empty((M, N), dtype=torch.int32, device=dev)
+        poison(C, 0x7B)
+        assert np.array_equal(to_host(ops.sparse_int8_gemm_s32(comp, xd, meta, out=C)), acc)
+        Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        poison(Y, 0x7B)
+        ops.sparse_int8_gemm(comp, xd, meta, to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev), out=Y)
+        assert np.array_equal(to_host(Y).view(np.uint16), orc.dequant_epilogue(acc, act, ws, b).view(np.uint16))
