@@ -281,30 +281,35 @@ struct KSplit {
 
 // Exact INT32 hand-off between the KP workgroups of a row block, through device-scope atomics
 // only (no cache write-back or invalidate fences, which stall every workgroup on the XCD):
-// every workgroup adds its lane partials (threads with `has` set, 16-row block `blk`) into the
-// row block's sums, waits for the adds to complete, and one thread counts the arrival with
+// every workgroup adds its lane partials (per thread NQ 16 x 16 output blocks; block i when
+// has[i], at sum slot blk[i]) into the row block's sums, waits for the adds to complete, and one thread counts the arrival with
 // atomicInc(cnt, KP - 1), which wraps the counter back to 0 on the last arrival. Workgroups
 // that arrive earlier return false; the last one takes the sums with atomicExch(..., 0), which
 // clears them for the next launch, and returns true. No workgroup waits for another, so the
 // hand-off cannot stall on a workgroup that is not resident. INT32 addition is associative, so
 // the result is exact in any arrival order.
-template <int KP>
-__device__ bool ksplit_handoff(const KSplit& ks, v4i& sum, bool has, int blk, int lane)
+template <int KP, int NQ>
+__device__ bool ksplit_handoff(const KSplit& ks, v4i (&sum)[NQ], const bool (&has)[NQ], const int (&blk)[NQ], int lane)
 {
     __shared__ int s_last;
-    int* slot = ks.acc + static_cast<size_t>(blk) * 4 * kWave + lane;
-    if (has) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) atomicAdd(slot + e * kWave, sum[e]);
+    for (int i = 0; i < NQ; i++) {
+        if (!has[i]) continue;
+        int* slot = ks.acc + static_cast<size_t>(blk[i]) * 4 * kWave + lane;
+#pragma unroll
+        for (int e = 0; e < 4; e++) atomicAdd(slot + e * kWave, sum[i][e]);
     }
     wait_vmcnt<0>();
     __syncthreads();
     if (threadIdx.x == 0) s_last = atomicInc(ks.cnt + blockIdx.x, KP - 1) == KP - 1;
     __syncthreads();
     if (!s_last) return false;
-    if (has) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) sum[e] = atomicExch(slot + e * kWave, 0);
+    for (int i = 0; i < NQ; i++) {
+        if (!has[i]) continue;
+        int* slot = ks.acc + static_cast<size_t>(blk[i]) * 4 * kWave + lane;
+#pragma unroll
+        for (int e = 0; e < 4; e++) sum[i][e] = atomicExch(slot + e * kWave, 0);
     }
     return true;
 }
@@ -402,49 +407,62 @@ __device__ __forceinline__ void fq_quantize_tokens(const FqArgs& fq, int M, int 
 // rows n0 + 16 b + 4 (l / 16) + e of token 16 tb + l % 16. Waves take the RB x TB blocks in
 // turn, sum the WV partials exactly and store each lane's 4 consecutive outputs of one token
 // row together (8-byte FP16 or 16-byte INT32 stores when the rows allow it).
+template <int RB, int TB, int WV>
+__device__ __forceinline__ v4i decode_block_sum(const v4i* red, int q, int lane)
+{
+    const int b = q / TB, tb = q - b * TB;
+    v4i sum = red[(b * TB + tb) * kWave + lane];
+#pragma unroll
+    for (int w = 1; w < WV; w++) sum += red[((w * RB + b) * TB + tb) * kWave + lane];
+    return sum;
+}
+
+// Stores block q = b * TB + tb of a row block (rows n0 + 16 b + 4 g + e, token 16 tb + lane % 16).
+template <bool DEQUANT, int TB>
+__device__ __forceinline__ void decode_store_block(const GemmEpilogue& ep, const v4i& sum, int n0, int q, int lane)
+{
+    const int M = ep.M, N = ep.N;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int b = q / TB, tb = q - b * TB;
+    const int m = 16 * tb + r16;
+    const int nb = n0 + 16 * b + 4 * g;
+    if (m >= M || nb >= N) return;
+    const size_t o = static_cast<size_t>(m) * N + nb;
+    const bool whole = ep.vec_out && nb + 4 <= N;
+    if constexpr (DEQUANT) {
+        const float as = ep.act_scale[m];
+        uint16_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int n = nb + e < N ? nb + e : N - 1;
+            const float bv = ep.bias ? h2f(ep.bias[n]) : 0.0f;
+            h[e] = dequant_gemm(sum[e], as, h2f(ep.w_scale[n]), bv, ep.bias != nullptr);
+        }
+        if (whole) {
+            *reinterpret_cast<uint2*>(ep.c16 + o) =
+                make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (nb + e < N) ep.c16[o + e] = h[e];
+        }
+    } else {
+        if (whole) {
+            *reinterpret_cast<int4*>(ep.c32 + o) = make_int4(sum[0], sum[1], sum[2], sum[3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (nb + e < N) ep.c32[o + e] = sum[e];
+        }
+    }
+}
+
 template <bool DEQUANT, int RB, int TB, int WV>
 __device__ __forceinline__ void decode_epilogue_blocks(const v4i* red, const GemmEpilogue& ep, int n0, int wave,
                                                        int lane)
 {
-    const int M = ep.M, N = ep.N;
-    const int r16 = lane & 15, g = lane >> 4;
-    for (int q = wave; q < RB * TB; q += WV) {
-        const int b = q / TB, tb = q - b * TB;
-        v4i sum = red[(b * TB + tb) * kWave + lane];
-#pragma unroll
-        for (int w = 1; w < WV; w++) sum += red[((w * RB + b) * TB + tb) * kWave + lane];
-        const int m = 16 * tb + r16;
-        const int nb = n0 + 16 * b + 4 * g;
-        if (m >= M || nb >= N) continue;
-        const size_t o = static_cast<size_t>(m) * N + nb;
-        const bool whole = ep.vec_out && nb + 4 <= N;
-        if constexpr (DEQUANT) {
-            const float as = ep.act_scale[m];
-            uint16_t h[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int n = nb + e < N ? nb + e : N - 1;
-                const float bv = ep.bias ? h2f(ep.bias[n]) : 0.0f;
-                h[e] = dequant_gemm(sum[e], as, h2f(ep.w_scale[n]), bv, ep.bias != nullptr);
-            }
-            if (whole) {
-                *reinterpret_cast<uint2*>(ep.c16 + o) =
-                    make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (nb + e < N) ep.c16[o + e] = h[e];
-            }
-        } else {
-            if (whole) {
-                *reinterpret_cast<int4*>(ep.c32 + o) = make_int4(sum[0], sum[1], sum[2], sum[3]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (nb + e < N) ep.c32[o + e] = sum[e];
-            }
-        }
-    }
+    for (int q = wave; q < RB * TB; q += WV)
+        decode_store_block<DEQUANT, TB>(ep, decode_block_sum<RB, TB, WV>(red, q, lane), n0, q, lane);
 }
 
 // VPR > 0: fused quantize (fq_quantize_tokens with VPR vectors per thread per row); the tokens
@@ -596,7 +614,11 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
         for (int w = 1; w < WV; w++) sum += red[(w * RB + wave) * kWave + lane];
     }
     if constexpr (KP > 1) {
-        if (!ksplit_handoff<KP>(ks, sum, wave < RB, blockIdx.x * RB + wave, lane)) return;
+        v4i sums[1] = {sum};
+        const bool has[1] = {wave < RB};
+        const int blk[1] = {static_cast<int>(blockIdx.x) * RB + wave};
+        if (!ksplit_handoff<KP, 1>(ks, sums, has, blk, lane)) return;
+        sum = sums[0];
     }
     if (wave < RB) {
         const int b = wave;
@@ -633,7 +655,7 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
 {
     constexpr bool FQ = VPR > 0;
     static_assert(!FQ || TB == 1, "the fused prologue serves one token block");
-    static_assert(KP == 1 || (!FQ && TB == 1), "the K split serves the plain one-block kernel");
+    static_assert(KP == 1 || !FQ, "the fused prologue needs the whole token rows");
     __shared__ v4i red[WV * RB * TB * kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -782,7 +804,26 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
         for (int tb = 0; tb < TB; tb++) red[((wave * RB + b) * TB + tb) * kWave + lane] = acc[b][tb];
     __syncthreads();
     if constexpr (TB > 1) {
-        decode_epilogue_blocks<DEQUANT, RB, TB, WV>(red, ep, n0, wave, lane);
+        if constexpr (KP == 1) {
+            decode_epilogue_blocks<DEQUANT, RB, TB, WV>(red, ep, n0, wave, lane);
+        } else {
+            // Wave w reduces blocks q = w, w + WV, ...; the sums are handed over, then stored.
+            constexpr int NQ = (RB * TB + WV - 1) / WV;
+            v4i sums[NQ];
+            bool has[NQ];
+            int blk[NQ];
+#pragma unroll
+            for (int i = 0; i < NQ; i++) {
+                const int q = wave + i * WV;
+                has[i] = q < RB * TB;
+                blk[i] = static_cast<int>(blockIdx.x) * RB * TB + q;
+                sums[i] = has[i] ? decode_block_sum<RB, TB, WV>(red, q, lane) : v4i{0, 0, 0, 0};
+            }
+            if (!ksplit_handoff<KP, NQ>(ks, sums, has, blk, lane)) return;
+#pragma unroll
+            for (int i = 0; i < NQ; i++)
+                if (has[i]) decode_store_block<DEQUANT, TB>(ep, sums[i], n0, wave + i * WV, lane);
+        }
         return;
     }
     v4i sum = v4i{0, 0, 0, 0};
@@ -792,7 +833,11 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
         for (int w = 1; w < WV; w++) sum += red[(w * RB + wave) * kWave + lane];
     }
     if constexpr (KP > 1) {
-        if (!ksplit_handoff<KP>(ks, sum, wave < RB, blockIdx.x * RB + wave, lane)) return;
+        v4i sums[1] = {sum};
+        const bool has[1] = {wave < RB};
+        const int blk[1] = {static_cast<int>(blockIdx.x) * RB + wave};
+        if (!ksplit_handoff<KP, 1>(ks, sums, has, blk, lane)) return;
+        sum = sums[0];
     }
     if (wave < RB) {
         const int b = wave;
@@ -1029,15 +1074,17 @@ static int pad_stages(int per)
     return -1;
 }
 
-template <bool DEQUANT, int RB, int TB>
+template <bool DEQUANT, int RB, int TB, int KP>
 static int launch_tb_sparse(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep, int K,
-                            hipStream_t s)
+                            const KSplit& ks, hipStream_t s)
 {
     constexpr int WV = kDecDenseWaves, AH = kSkinnyTbAheadSparse;
-    const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
-    const int S = pad_stages(divup(K / 256, WV));
+    const dim3 grid(static_cast<unsigned>(divup(ep.N, 16 * RB)), KP);
+    const int S = pad_stages(divup(K / KP / 256, WV));
+    // Largest padded per-wave segment count K <= kDecodeMaxK can need at this KP.
+    constexpr int SM = kDecodeMaxK / 256 / KP / WV;
 #define FORGE_TB_SPARSE(SS) \
-    decode_sparse_reg_kernel<DEQUANT, SS, RB, WV, AH, TB><<<grid, WV * kWave, 0, s>>>(W, meta, X, ep, K, FqArgs{}, KSplit{})
+    decode_sparse_reg_kernel<DEQUANT, (SS <= SM ? SS : SM), RB, WV, AH, TB, 0, KP><<<grid, WV * kWave, 0, s>>>(W, meta, X, ep, K, FqArgs{}, ks)
     switch (S) {
     case 1: FORGE_TB_SPARSE(1); break;
     case 2: FORGE_TB_SPARSE(2); break;
@@ -1056,18 +1103,57 @@ bool skinny_tb_supported(int M, int K)
     return M > kDecodeMaxM && M <= kSkinnyTbMaxM && K <= kDecodeMaxK && K % 256 == 0;
 }
 
+// K parts for the token-block kernel with 16-row workgroups: as decode_dense_kparts, in whole
+// 256-deep segments, parts at least kKSplitMinPartKTb deep, the sums of RB x TB blocks per
+// workgroup within a slot.
+constexpr int kKSplitMinPartKTb = 1024;
+
+static int skinny_tb_kparts(int N, int K, int blocks, int cu)
+{
+    const int g = divup(N, 16);
+    if (K < kKSplitMinK || g * blocks > kKSplitMaxBlocks) return 1;
+    int kp = 1;
+    while (kp < 4 && 2 * g * kp * 4 <= 5 * cu && K % (512 * kp) == 0 && K / (2 * kp) >= kKSplitMinPartKTb) kp *= 2;
+    return kp;
+}
+
+template <bool DEQUANT, int TB>
+static int launch_tb_sparse_narrow(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep,
+                                   int K, int cu, hipStream_t s, int kp)
+{
+    if (kp == 0) kp = skinny_tb_kparts(ep.N, K, TB, cu);
+    KSplit ks{};
+    if (kp > 1) {
+        ks = ksplit_slot(s);
+        if (!ks.acc) kp = 1;
+    }
+    switch (kp) {
+    case 2: return launch_tb_sparse<DEQUANT, 1, TB, 2>(W, meta, X, ep, K, ks, s);
+    case 4: return launch_tb_sparse<DEQUANT, 1, TB, 4>(W, meta, X, ep, K, ks, s);
+    default: return launch_tb_sparse<DEQUANT, 1, TB, 1>(W, meta, X, ep, K, ks, s);
+    }
+}
+
+// kp: 0 chooses the K parts for 16-row workgroups (skinny_tb_kparts); otherwise 1, 2 or 4
+// (K % (256 kp) == 0).
 int launch_skinny_tb(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep, int K, int cu,
-                     hipStream_t s)
+                     hipStream_t s, int kp)
 {
     if (!skinny_tb_supported(ep.M, K)) return FORGE_EINVAL;
     const bool tall = 2 * divup(ep.N, 32) >= cu;
     const bool dq = ep.c16 != nullptr;
     if (ep.M <= 32) {
-        if (tall) return dq ? launch_tb_sparse<true, 2, 2>(W, meta, X, ep, K, s) : launch_tb_sparse<false, 2, 2>(W, meta, X, ep, K, s);
-        return dq ? launch_tb_sparse<true, 1, 2>(W, meta, X, ep, K, s) : launch_tb_sparse<false, 1, 2>(W, meta, X, ep, K, s);
+        if (tall)
+            return dq ? launch_tb_sparse<true, 2, 2, 1>(W, meta, X, ep, K, KSplit{}, s)
+                      : launch_tb_sparse<false, 2, 2, 1>(W, meta, X, ep, K, KSplit{}, s);
+        return dq ? launch_tb_sparse_narrow<true, 2>(W, meta, X, ep, K, cu, s, kp)
+                  : launch_tb_sparse_narrow<false, 2>(W, meta, X, ep, K, cu, s, kp);
     }
-    if (tall) return dq ? launch_tb_sparse<true, 2, 4>(W, meta, X, ep, K, s) : launch_tb_sparse<false, 2, 4>(W, meta, X, ep, K, s);
-    return dq ? launch_tb_sparse<true, 1, 4>(W, meta, X, ep, K, s) : launch_tb_sparse<false, 1, 4>(W, meta, X, ep, K, s);
+    if (tall)
+        return dq ? launch_tb_sparse<true, 2, 4, 1>(W, meta, X, ep, K, KSplit{}, s)
+                  : launch_tb_sparse<false, 2, 4, 1>(W, meta, X, ep, K, KSplit{}, s);
+    return dq ? launch_tb_sparse_narrow<true, 4>(W, meta, X, ep, K, cu, s, kp)
+              : launch_tb_sparse_narrow<false, 4>(W, meta, X, ep, K, cu, s, kp);
 }
 
 bool decode_supported(int M, int K) { return M <= kDecodeMaxM && K % 128 == 0 && K <= kDecodeMaxK; }

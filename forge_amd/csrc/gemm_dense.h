@@ -51,11 +51,12 @@ int launch_decode(const int8_t* W, const uint32_t* meta, const int8_t* X, const 
 
 // Sparse GEMM at 16 < M <= kSkinnyTbMaxM tokens on the sparse register decode kernel with
 // several 16-token blocks per weight fragment: K % 256 == 0, K <= kDecodeMaxK, 16-byte aligned
-// operands (W_comp, gfx950 index words, tokens).
+// operands (W_comp, gfx950 index words, tokens). Narrow N splits K over 2 or 4 workgroups per
+// row block (exact INT32 hand-off); kp forces the parts (1, 2, 4; 0 = chosen by shape).
 constexpr int kSkinnyTbMaxM = 64;
 bool skinny_tb_supported(int M, int K);
 int launch_skinny_tb(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep, int K, int cu,
-                     hipStream_t s);
+                     hipStream_t s, int kp = 0);
 
 // Implicit-GEMM NHWC conv through the dense tile engine (conv.hip supplies the geometry).
 int launch_conv_gemm(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep, int Co, bool vec,

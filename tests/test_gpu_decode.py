@@ -110,8 +110,12 @@ def test_config4_full_size_sampled(dev, orc, M):
 # odd (element stores), and >= 4096 (32-row workgroups instead of 16).
 TB_DENSE = [(17, 128, 48), (32, 384, 200), (33, 640, 201), (48, 1152, 96), (64, 1536, 4160),
             (40, 5120, 64), (64, 8192, 32), (25, 2048, 4112)]
+# From K = 4096 on, narrow N (16-row workgroups fewer than the CUs) splits K over 2 or 4
+# workgroups per row block: (40, 5120, 64), (64, 8192, 32), (64, 6144, 1536), (64, 8192, 1024),
+# (30, 4096, 1008).
 TB_SPARSE = [(17, 256, 48), (32, 768, 208), (33, 1280, 16), (48, 2048, 96), (64, 1536, 4160),
-             (40, 5120, 64), (64, 8192, 32), (25, 3072, 4112), (64, 6144, 1536)]
+             (40, 5120, 64), (64, 8192, 32), (25, 3072, 4112), (64, 6144, 1536), (64, 8192, 1024),
+             (30, 4096, 1008)]
 
 
 def _check_cols(N):
