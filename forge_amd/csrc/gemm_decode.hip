@@ -380,7 +380,7 @@ __device__ __forceinline__ void fq_quantize_tokens(const FqArgs& fq, int M, int 
             if (bits[r] > kHalfInfBits)
                 amax[r] = fmaxf(fmaxf(smax[r], smax[MT + r]), fmaxf(smax[2 * MT + r], smax[3 * MT + r]));
     }
-    const bool out = blockIdx.x == 0 && fq.q != nullptr;
+    const bool out = blockIdx.x == 0 && blockIdx.y == 0 && fq.q != nullptr;
 #pragma unroll
     for (int r = 0; r < MT; r++) {
         if (r >= M) break;
@@ -476,7 +476,6 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
     const int8_t* __restrict__ W, const int8_t* __restrict__ X, GemmEpilogue ep, int K, FqArgs fq, KSplit ks)
 {
     constexpr bool FQ = VPR > 0;
-    static_assert(!(FQ && KP > 1), "the fused quantize prologue needs the whole token rows");
     __shared__ v4i red[WV * RB * kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -512,7 +511,7 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const int r = 8 * j + (lane & 7);
-        if constexpr (FQ) px[j] = ftok + (r < M ? r : M - 1) * (K + kFqPad) + 16 * (lane >> 3);
+        if constexpr (FQ) px[j] = ftok + (r < M ? r : M - 1) * (K + kFqPad) + k0 + 16 * (lane >> 3);
         else px[j] = X + static_cast<size_t>(r < M ? r : M - 1) * K + k0 + 16 * (lane >> 3);
     }
     const bool tok = r16 < M;   // after the swap, lane l holds token row l % 16
@@ -655,7 +654,6 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
 {
     constexpr bool FQ = VPR > 0;
     static_assert(!FQ || TB == 1, "the fused prologue serves one token block");
-    static_assert(KP == 1 || !FQ, "the fused prologue needs the whole token rows");
     __shared__ v4i red[WV * RB * TB * kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -709,7 +707,7 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
         const int r = 16 * tb + r16;
         tok[tb] = r < M;
         const int rr = tok[tb] ? r : M - 1;
-        if constexpr (FQ) px[tb] = ftok + rr * (K + kFqPad) + 64 * (g >> 1) + 16 * (g & 1);
+        if constexpr (FQ) px[tb] = ftok + rr * (K + kFqPad) + k0 + 64 * (g >> 1) + 16 * (g & 1);
         else px[tb] = X + static_cast<size_t>(rr) * K + k0 + 64 * (g >> 1) + 16 * (g & 1);
     }
 
@@ -1163,16 +1161,21 @@ bool decode_fq_supported(int M, int K, bool sparse)
     return M <= kDecodeFqMaxM && K <= kDecodeMaxK && K % (sparse ? 256 : 128) == 0;
 }
 
-template <int VPR>
-static int launch_decode_fq_vpr(const int8_t* W, const uint32_t* meta, const GemmEpilogue& ep, int K, bool sparse,
-                                const FqArgs& fq, hipStream_t s)
+// The fused path takes the same K split as the two-pass decode launches (every workgroup of a
+// row block quantizes the whole token rows in its prologue, then reads its K part from LDS);
+// 2 or 4 parts.
+template <int VPR, int KP>
+static int launch_decode_fq_kp(const int8_t* W, const uint32_t* meta, const GemmEpilogue& ep, int K, bool sparse,
+                               const FqArgs& fq, const KSplit& ks, hipStream_t s)
 {
     if (sparse) {
         constexpr int RB = 2, WV = 4, AH = 4;
-        const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
-        const int per = divup(K / 256, WV);
-#define FORGE_DEC_FQ_SP(SS) \
-    decode_sparse_reg_kernel<true, SS, RB, WV, AH, 1, VPR><<<grid, WV * kWave, 0, s>>>(W, meta, nullptr, ep, K, fq, KSplit{})
+        const dim3 grid(static_cast<unsigned>(divup(ep.N, 16 * RB)), KP);
+        const int per = divup(K / KP / 256, WV);
+        constexpr int SM = kDecodeMaxK / 256 / KP / WV;
+#define FORGE_DEC_FQ_SP(SS)                                                                              \
+    decode_sparse_reg_kernel<true, (SS <= SM ? SS : SM), RB, WV, AH, 1, VPR, KP><<<grid, WV * kWave, 0, s>>>( \
+        W, meta, nullptr, ep, K, fq, ks)
         if (per <= 1) FORGE_DEC_FQ_SP(1);
         else if (per <= 2) FORGE_DEC_FQ_SP(2);
         else if (per <= 4) FORGE_DEC_FQ_SP(4);
@@ -1181,10 +1184,11 @@ static int launch_decode_fq_vpr(const int8_t* W, const uint32_t* meta, const Gem
         return launch_status();
     }
     constexpr int RB = 1, WV = kDecDenseWaves, AH = kDecDenseAhead;
-    const unsigned grid = static_cast<unsigned>(divup(ep.N, 16 * RB));
-    const int per = divup(K / 128, WV);
+    const dim3 grid(static_cast<unsigned>(divup(ep.N, 16 * RB)), KP);
+    const int per = divup(K / KP / 128, WV);
+    constexpr int SM = kDecodeMaxK / 128 / KP / WV;
 #define FORGE_DEC_FQ_DENSE(SS) \
-    decode_dense_kernel<true, SS, RB, WV, AH, VPR><<<grid, WV * kWave, 0, s>>>(W, nullptr, ep, K, fq, KSplit{})
+    decode_dense_kernel<true, (SS <= SM ? SS : SM), RB, WV, AH, VPR, KP><<<grid, WV * kWave, 0, s>>>(W, nullptr, ep, K, fq, ks)
     if (per <= 1) FORGE_DEC_FQ_DENSE(1);
     else if (per <= 2) FORGE_DEC_FQ_DENSE(2);
     else if (per <= 4) FORGE_DEC_FQ_DENSE(4);
@@ -1192,6 +1196,27 @@ static int launch_decode_fq_vpr(const int8_t* W, const uint32_t* meta, const Gem
     else FORGE_DEC_FQ_DENSE(16);
 #undef FORGE_DEC_FQ_DENSE
     return launch_status();
+}
+
+template <int VPR>
+static int launch_decode_fq_vpr(const int8_t* W, const uint32_t* meta, const GemmEpilogue& ep, int K, bool sparse,
+                                const FqArgs& fq, hipStream_t s)
+{
+    int st = FORGE_OK;
+    const DeviceInfo& di = device_info(&st);
+    if (st != FORGE_OK) return st;
+    int kp = sparse ? decode_sparse_kparts(ep.N, K, 2, di.cu_count) : decode_dense_kparts(ep.N, K, 1, di.cu_count);
+    kp = kp < 4 ? kp : 4;
+    KSplit ks{};
+    if (kp > 1) {
+        ks = ksplit_slot(s);
+        if (!ks.acc) kp = 1;
+    }
+    switch (kp) {
+    case 2: return launch_decode_fq_kp<VPR, 2>(W, meta, ep, K, sparse, fq, ks, s);
+    case 4: return launch_decode_fq_kp<VPR, 4>(W, meta, ep, K, sparse, fq, ks, s);
+    default: return launch_decode_fq_kp<VPR, 1>(W, meta, ep, K, sparse, fq, ks, s);
+    }
 }
 
 int launch_decode_fq(const uint16_t* x, const int8_t* W, const uint32_t* meta, const uint16_t* w_scale,

@@ -15,9 +15,14 @@ from helpers import int8_uniform, poison, say, special_fp16_rows, to_dev, to_hos
 
 pytestmark = pytest.mark.gpu
 
+# Narrow N at K >= 4096 (dense) or K = 8192 (sparse) also splits K over 2 or 4 workgroups per
+# row block, each quantizing the whole token rows in its prologue: dense (2, 8192, 64),
+# (1, 8192, 1000), (2, 4096, 2048), (1, 6144, 520); sparse (2, 8192, 64), (1, 8192, 4096),
+# (2, 8192, 1008).
 DENSE = [(1, 128, 48), (2, 1152, 200), (1, 2048, 96), (2, 3072, 1000), (2, 8192, 64), (1, 8192, 4096),
-         (2, 640, 16)]
-SPARSE = [(1, 256, 48), (2, 1280, 208), (1, 2048, 96), (2, 3072, 1024), (2, 8192, 64), (1, 8192, 4096)]
+         (2, 640, 16), (1, 8192, 1000), (2, 4096, 2048), (1, 6144, 520)]
+SPARSE = [(1, 256, 48), (2, 1280, 208), (1, 2048, 96), (2, 3072, 1024), (2, 8192, 64), (1, 8192, 4096),
+          (2, 8192, 1008)]
 
 
 def _x(rng, M, K, special):
