@@ -94,10 +94,54 @@ __device__ __forceinline__ void lds_read_idx(const uint32_t* q0, const uint32_t*
 // S: stages per wave after padding (1, 2, 4 or 8). The per-wave stage sequence is
 // straight-line code with constant ring slots; every load in it is a DMA into LDS, so the only
 // vmcnt waits are the ring's own (whole stages, counted from the end).
-template <bool DEQUANT, int S>
+// K split across the workgroups of one row block: acc holds gridDim.x x RB x 256 INT32 sums
+// (16 x 16 outputs per 16-row block), cnt one arrival counter per row block; both are zero
+// between launches (the last workgroup of a row block leaves them so).
+struct KSplit {
+    int* acc;
+    unsigned* cnt;
+};
+
+// Exact INT32 hand-off between the KP workgroups of a row block, through device-scope atomics
+// only (no cache write-back or invalidate fences, which stall every workgroup on the XCD):
+// every workgroup adds its lane partials (per thread NQ 16 x 16 output blocks; block i when
+// has[i], at sum slot blk[i]) into the row block's sums, waits for the adds to complete, and one thread counts the arrival with
+// atomicInc(cnt, KP - 1), which wraps the counter back to 0 on the last arrival. Workgroups
+// that arrive earlier return false; the last one takes the sums with atomicExch(..., 0), which
+// clears them for the next launch, and returns true. No workgroup waits for another, so the
+// hand-off cannot stall on a workgroup that is not resident. INT32 addition is associative, so
+// the result is exact in any arrival order.
+template <int KP, int NQ>
+__device__ bool ksplit_handoff(const KSplit& ks, v4i (&sum)[NQ], const bool (&has)[NQ], const int (&blk)[NQ], int lane)
+{
+    __shared__ int s_last;
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+        if (!has[i]) continue;
+        int* slot = ks.acc + static_cast<size_t>(blk[i]) * 4 * kWave + lane;
+#pragma unroll
+        for (int e = 0; e < 4; e++) atomicAdd(slot + e * kWave, sum[i][e]);
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (threadIdx.x == 0) s_last = atomicInc(ks.cnt + blockIdx.x, KP - 1) == KP - 1;
+    __syncthreads();
+    if (!s_last) return false;
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+        if (!has[i]) continue;
+        int* slot = ks.acc + static_cast<size_t>(blk[i]) * 4 * kWave + lane;
+#pragma unroll
+        for (int e = 0; e < 4; e++) sum[i][e] = atomicExch(slot + e * kWave, 0);
+    }
+    return true;
+}
+
+// KP > 1: K split over the KP workgroups blockIdx.y of a row block (ksplit_handoff).
+template <bool DEQUANT, int S, int KP = 1>
 __global__ __launch_bounds__(kDecWaves * kWave) void decode_sparse_kernel(
     const int8_t* __restrict__ W, const uint32_t* __restrict__ meta, const int8_t* __restrict__ X,
-    GemmEpilogue ep, int K)
+    GemmEpilogue ep, int K, KSplit ks)
 {
     using Cfg = SparseDecodeCfg;
     constexpr int D = Cfg::kSlots;
@@ -117,8 +161,11 @@ __global__ __launch_bounds__(kDecWaves * kWave) void decode_sparse_kernel(
     const int M = ep.M, N = ep.N;
     const int r16 = lane & 15, g = lane >> 4;
 
+    const int kp = KP > 1 ? static_cast<int>(blockIdx.y) : 0;
+    const int k0 = kp * (K / KP);   // whole 128-deep stages: k0 / 2 compressed bytes, k0 / 2 index words
+
     // This wave's stages [s0, s0 + ns), ns <= S; stages ns..S-1 are padding.
-    const int nst = K / 128;
+    const int nst = K / KP / 128;
     const int s0 = wave * S < nst ? wave * S : nst;
     const int ns = (s0 + S < nst ? s0 + S : nst) - s0;
 
@@ -132,7 +179,7 @@ __global__ __launch_bounds__(kDecWaves * kWave) void decode_sparse_kernel(
         const int r = s >> 2;
         const int c = (s & 3) ^ lds_swz4(r);
         const int gr = (n0 + r) < N ? (n0 + r) : N - 1;
-        pw[q] = W + static_cast<size_t>(gr) * (K / 2) + 16 * c;
+        pw[q] = W + static_cast<size_t>(gr) * (K / 2) + k0 / 2 + 16 * c;
     }
     const int8_t* px[2];
 #pragma unroll
@@ -140,12 +187,12 @@ __global__ __launch_bounds__(kDecWaves * kWave) void decode_sparse_kernel(
         const int s = q * kWave + lane;
         const int r = s >> 3;
         const int c = (s & 7) ^ lds_swz8(r);
-        px[q] = X + static_cast<size_t>(r < M ? r : M - 1) * K + 16 * c;   // rows >= M: zeroed on read
+        px[q] = X + static_cast<size_t>(r < M ? r : M - 1) * K + k0 + 16 * c;   // rows >= M: zeroed on read
     }
     // 2 blocks of 16 rows x 64 index words per stage; lanes 0..31 each copy 16 bytes.
     int blk = (n0 >> 4) + ((lane & 31) >> 4);
     blk = blk < (N >> 4) ? blk : (N >> 4) - 1;
-    const int8_t* pi = reinterpret_cast<const int8_t*>(meta + static_cast<size_t>(blk) * (K / 2)) + 16 * (lane & 15);
+    const int8_t* pi = reinterpret_cast<const int8_t*>(meta + static_cast<size_t>(blk) * (K / 2) + k0 / 2) + 16 * (lane & 15);
 
     auto issue = [&](int t, int slot) {
         const int st = s0 + (t < ns ? t : ns - 1);
@@ -206,11 +253,20 @@ __global__ __launch_bounds__(kDecWaves * kWave) void decode_sparse_kernel(
     red[(wave * 2 + 0) * kWave + lane] = acc[0];
     red[(wave * 2 + 1) * kWave + lane] = acc[1];
     __syncthreads();
+    const int b = threadIdx.x / kWave;
+    v4i sum = v4i{0, 0, 0, 0};
     if (threadIdx.x < 2 * kWave) {
-        const int b = threadIdx.x / kWave;
-        v4i sum = v4i{0, 0, 0, 0};
 #pragma unroll
         for (int w = 0; w < kDecWaves; w++) sum += red[(w * 2 + b) * kWave + lane];
+    }
+    if constexpr (KP > 1) {
+        v4i sums[1] = {sum};
+        const bool has[1] = {threadIdx.x < 2 * kWave};
+        const int blk[1] = {static_cast<int>(blockIdx.x) * 2 + b};
+        if (!ksplit_handoff<KP, 1>(ks, sums, has, blk, lane)) return;
+        sum = sums[0];
+    }
+    if (threadIdx.x < 2 * kWave) {
         const int m = r16;
         if (m < M) {
             const int nb = n0 + 16 * b + 4 * g;
@@ -271,48 +327,6 @@ struct FqArgs {
     float* scale;        // (M,) scratch (written with q)
 };
 
-// K split across the workgroups of one row block: acc holds gridDim.x x RB x 256 INT32 sums
-// (16 x 16 outputs per 16-row block), cnt one arrival counter per row block; both are zero
-// between launches (the last workgroup of a row block leaves them so).
-struct KSplit {
-    int* acc;
-    unsigned* cnt;
-};
-
-// Exact INT32 hand-off between the KP workgroups of a row block, through device-scope atomics
-// only (no cache write-back or invalidate fences, which stall every workgroup on the XCD):
-// every workgroup adds its lane partials (per thread NQ 16 x 16 output blocks; block i when
-// has[i], at sum slot blk[i]) into the row block's sums, waits for the adds to complete, and one thread counts the arrival with
-// atomicInc(cnt, KP - 1), which wraps the counter back to 0 on the last arrival. Workgroups
-// that arrive earlier return false; the last one takes the sums with atomicExch(..., 0), which
-// clears them for the next launch, and returns true. No workgroup waits for another, so the
-// hand-off cannot stall on a workgroup that is not resident. INT32 addition is associative, so
-// the result is exact in any arrival order.
-template <int KP, int NQ>
-__device__ bool ksplit_handoff(const KSplit& ks, v4i (&sum)[NQ], const bool (&has)[NQ], const int (&blk)[NQ], int lane)
-{
-    __shared__ int s_last;
-#pragma unroll
-    for (int i = 0; i < NQ; i++) {
-        if (!has[i]) continue;
-        int* slot = ks.acc + static_cast<size_t>(blk[i]) * 4 * kWave + lane;
-#pragma unroll
-        for (int e = 0; e < 4; e++) atomicAdd(slot + e * kWave, sum[i][e]);
-    }
-    wait_vmcnt<0>();
-    __syncthreads();
-    if (threadIdx.x == 0) s_last = atomicInc(ks.cnt + blockIdx.x, KP - 1) == KP - 1;
-    __syncthreads();
-    if (!s_last) return false;
-#pragma unroll
-    for (int i = 0; i < NQ; i++) {
-        if (!has[i]) continue;
-        int* slot = ks.acc + static_cast<size_t>(blk[i]) * 4 * kWave + lane;
-#pragma unroll
-        for (int e = 0; e < 4; e++) sum[i][e] = atomicExch(slot + e * kWave, 0);
-    }
-    return true;
-}
 constexpr int kFqPad = 128;
 constexpr int kFqTokAhead = 2;   // token stages read from LDS ahead of their MFMAs
 constexpr int kFqTokBytes = kDecodeFqMaxM * (kDecodeMaxK + kFqPad);
@@ -1040,19 +1054,57 @@ static int launch_decode_sparse_reg(const int8_t* W, const uint32_t* meta, const
     }
 }
 
-template <bool DEQUANT>
-static int launch_decode_sparse(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep,
-                                int K, hipStream_t s)
+template <bool DEQUANT, int KP>
+static int launch_decode_sparse_kp(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep,
+                                   int K, const KSplit& ks, hipStream_t s)
 {
-    const unsigned grid = static_cast<unsigned>(divup(ep.N, kDecRows));
-    const int per = divup(K / 128, kDecWaves);
-#define FORGE_DEC_SPARSE(SS) decode_sparse_kernel<DEQUANT, SS><<<grid, kDecWaves * kWave, 0, s>>>(W, meta, X, ep, K)
+    const dim3 grid(static_cast<unsigned>(divup(ep.N, kDecRows)), KP);
+    const int per = divup(K / KP / 128, kDecWaves);
+    constexpr int SM = kDecodeMaxK / 128 / KP / kDecWaves;
+#define FORGE_DEC_SPARSE(SS) \
+    decode_sparse_kernel<DEQUANT, (SS <= SM ? SS : SM), KP><<<grid, kDecWaves * kWave, 0, s>>>(W, meta, X, ep, K, ks)
     if (per <= 1) FORGE_DEC_SPARSE(1);
     else if (per <= 2) FORGE_DEC_SPARSE(2);
     else if (per <= 4) FORGE_DEC_SPARSE(4);
     else FORGE_DEC_SPARSE(8);
 #undef FORGE_DEC_SPARSE
     return launch_status();
+}
+
+// K parts for the LDS-ring kernel (9-16 tokens, 32-row workgroups, 128-deep stages): as
+// decode_dense_kparts from K = 6144 on, up to 4 parts of at least 1536. Measured (M = 16):
+// K = 8192 N = 4096 11.0 -> 9.6 us, N = 2048 10.1 -> 7.7 us, N = 1024 8.2 -> 6.2 us; K = 6144
+// N = 2048 8.7 -> 7.1 us.
+static int decode_ring_kparts(int N, int K, int cu)
+{
+    const int g = divup(N, kDecRows);
+    if (K < 6144 || g * (kDecRows / 16) > kKSplitMaxBlocks) return 1;
+    int kp = 1;
+    while (kp < 4 && 2 * g * kp * 4 <= 5 * cu && K % (256 * kp) == 0 && K / (2 * kp) >= 1536) kp *= 2;
+    return kp;
+}
+
+// 9-16 tokens: the LDS-ring kernel (kp = 0 chooses the K parts, otherwise 1, 2 or 4).
+template <bool DEQUANT>
+static int launch_decode_sparse(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep,
+                                int K, hipStream_t s, int kp = 0)
+{
+    if (kp == 0) {
+        int st = FORGE_OK;
+        const DeviceInfo& di = device_info(&st);
+        if (st != FORGE_OK) return st;
+        kp = decode_ring_kparts(ep.N, K, di.cu_count);
+    }
+    KSplit ks{};
+    if (kp > 1) {
+        ks = ksplit_slot(s);
+        if (!ks.acc) kp = 1;
+    }
+    switch (kp) {
+    case 2: return launch_decode_sparse_kp<DEQUANT, 2>(W, meta, X, ep, K, ks, s);
+    case 4: return launch_decode_sparse_kp<DEQUANT, 4>(W, meta, X, ep, K, ks, s);
+    default: return launch_decode_sparse_kp<DEQUANT, 1>(W, meta, X, ep, K, ks, s);
+    }
 }
 
 // Sparse with several token blocks (16 < M <= 64): the register kernel with each weight

@@ -240,8 +240,10 @@ def test_decode_dense_ksplit_two_streams(dev, orc):
         assert np.array_equal(to_host(outs[i]), orc.gemm_s32(xs[i], B))
 
 
-# Sparse register kernel (M <= 8) at K = 8192 with narrow N: 2 or 4 K parts.
-KSPLIT_SPARSE = [(8, 8192, 1008), (1, 8192, 4096), (5, 8192, 2000), (3, 8192, 48)]
+# Sparse register kernel (M <= 8) at K = 8192 with narrow N: 2 or 4 K parts; the LDS-ring kernel
+# (9-16 tokens) from K = 6144 on: 2 or 4 parts.
+KSPLIT_SPARSE = [(8, 8192, 1008), (1, 8192, 4096), (5, 8192, 2000), (3, 8192, 48),
+                 (16, 8192, 4096), (12, 8192, 1008), (9, 6144, 2048), (16, 6144, 48)]
 
 
 @pytest.mark.parametrize("M,K,N", KSPLIT_SPARSE)
