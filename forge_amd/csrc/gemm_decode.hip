@@ -1054,6 +1054,135 @@ static int launch_decode_sparse_reg(const int8_t* W, const uint32_t* meta, const
     }
 }
 
+// Dense with several 16-token blocks (16 < M <= 64) at narrow N and deep K, where the tile
+// engine has too few tiles to fill the chip: one 16-row weight block per workgroup, each weight
+// fragment reused for TB token blocks (the dense decode kernel's loads, swap and
+// v_mfma_i32_16x16x64_i8), K split over KP workgroups per row block with the exact hand-off.
+template <bool DEQUANT, int S, int WV, int AH, int TB, int KP>
+__global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void decode_dense_tb_kernel(
+    const int8_t* __restrict__ W, const int8_t* __restrict__ X, GemmEpilogue ep, int K, KSplit ks)
+{
+    __shared__ v4i red[WV * TB * kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int n0 = blockIdx.x * 16;
+    const int M = ep.M, N = ep.N;
+    const int r16 = lane & 15;
+    const bool hi = (lane >> 3) & 1;
+    const int kp = KP > 1 ? static_cast<int>(blockIdx.y) : 0;
+    const int k0 = kp * (K / KP);
+    const int nst = K / KP / 128;
+    const int s0 = wave * S < nst ? wave * S : nst;
+    const int ns = (s0 + S < nst ? s0 + S : nst) - s0;
+
+    const int8_t* pw[2];
+    const int8_t* px[TB][2];
+    bool tok[TB];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int r = n0 + 8 * j + (lane & 7);
+        pw[j] = W + static_cast<size_t>(r < N ? r : N - 1) * K + k0 + 16 * (lane >> 3);
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++) {
+        tok[tb] = 16 * tb + r16 < M;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int r = 16 * tb + 8 * j + (lane & 7);
+            px[tb][j] = X + static_cast<size_t>(r < M ? r : M - 1) * K + k0 + 16 * (lane >> 3);
+        }
+    }
+
+    struct Stage { v4i w[2], x[TB][2]; };
+    auto load = [&](int t, Stage& f) {
+        const int st = s0 + (t < ns ? t : ns - 1);
+#pragma unroll
+        for (int j = 0; j < 2; j++) f.w[j] = ld_stream<v4i>(pw[j] + st * 128);
+#pragma unroll
+        for (int tb = 0; tb < TB; tb++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) f.x[tb][j] = *reinterpret_cast<const v4i*>(px[tb][j] + st * 128);
+    };
+    v4i acc[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++) acc[tb] = v4i{0, 0, 0, 0};
+    auto compute = [&](Stage& f, bool real) {
+        v4i a0, a1;
+        swap8_rows(f.w[0], f.w[1], hi, a0, a1);
+#pragma unroll
+        for (int tb = 0; tb < TB; tb++) {
+            v4i x0, x1;
+            swap8_rows(f.x[tb][0], f.x[tb][1], hi, x0, x1);
+            if (!(tok[tb] && real)) {
+                x0 = v4i{0, 0, 0, 0};
+                x1 = v4i{0, 0, 0, 0};
+            }
+            acc[tb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, x0, acc[tb], 0, 0, 0);
+            acc[tb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, x1, acc[tb], 0, 0, 0);
+        }
+    };
+    constexpr int A = AH < S ? AH : S;
+    Stage f[S];
+    if (ns > 0) {
+#pragma unroll
+        for (int t = 0; t < A; t++) load(t, f[t]);
+#pragma unroll
+        for (int t = 0; t < S; t++) {
+            if (t + A < S) load(t + A, f[t + A]);
+            compute(f[t], t < ns);
+        }
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; tb++) red[(wave * TB + tb) * kWave + lane] = acc[tb];
+    __syncthreads();
+    if constexpr (KP == 1) {
+        decode_epilogue_blocks<DEQUANT, 1, TB, WV>(red, ep, n0, wave, lane);
+    } else {
+        constexpr int NQ = (TB + WV - 1) / WV;
+        v4i sums[NQ];
+        bool has[NQ];
+        int blk[NQ];
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            const int q = wave + i * WV;
+            has[i] = q < TB;
+            blk[i] = static_cast<int>(blockIdx.x) * TB + q;
+            sums[i] = has[i] ? decode_block_sum<1, TB, WV>(red, q, lane) : v4i{0, 0, 0, 0};
+        }
+        if (!ksplit_handoff<KP, NQ>(ks, sums, has, blk, lane)) return;
+#pragma unroll
+        for (int i = 0; i < NQ; i++)
+            if (has[i]) decode_store_block<DEQUANT, TB>(ep, sums[i], n0, wave + i * WV, lane);
+    }
+}
+
+constexpr int kDenseTbWaves = 4;
+constexpr int kDenseTbAhead = 2;
+
+template <bool DEQUANT, int TB, int KP>
+static int launch_dense_tb_kp(const int8_t* W, const int8_t* X, const GemmEpilogue& ep, int K, const KSplit& ks,
+                              hipStream_t s)
+{
+    constexpr int WV = kDenseTbWaves;
+    const dim3 grid(static_cast<unsigned>(divup(ep.N, 16)), KP);
+    const int per = divup(K / KP / 128, WV);
+    constexpr int SM = kDecodeMaxK / 128 / KP / WV;
+#define FORGE_DENSE_TB(SS) \
+    decode_dense_tb_kernel<DEQUANT, (SS <= SM ? SS : SM), WV, kDenseTbAhead, TB, KP><<<grid, WV * kWave, 0, s>>>(W, X, ep, K, ks)
+    if (per <= 1) FORGE_DENSE_TB(1);
+    else if (per <= 2) FORGE_DENSE_TB(2);
+    else if (per <= 4) FORGE_DENSE_TB(4);
+    else if (per <= 8) FORGE_DENSE_TB(8);
+    else FORGE_DENSE_TB(16);
+#undef FORGE_DENSE_TB
+    return launch_status();
+}
+
+// kp: 0 = as skinny_tb_kparts (defined with the sparse token-block path), else 1, 2 or 4.
+template <bool DEQUANT, int TB>
+static int launch_dense_tb_tb(const int8_t* W, const int8_t* X, const GemmEpilogue& ep, int K, int cu, hipStream_t s,
+                              int kp);
+
 template <bool DEQUANT, int KP>
 static int launch_decode_sparse_kp(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep,
                                    int K, const KSplit& ks, hipStream_t s)
@@ -1204,6 +1333,38 @@ int launch_skinny_tb(const int8_t* W, const uint32_t* meta, const int8_t* X, con
                   : launch_tb_sparse<false, 2, 4, 1>(W, meta, X, ep, K, KSplit{}, s);
     return dq ? launch_tb_sparse_narrow<true, 4>(W, meta, X, ep, K, cu, s, kp)
               : launch_tb_sparse_narrow<false, 4>(W, meta, X, ep, K, cu, s, kp);
+}
+
+template <bool DEQUANT, int TB>
+static int launch_dense_tb_tb(const int8_t* W, const int8_t* X, const GemmEpilogue& ep, int K, int cu, hipStream_t s,
+                              int kp)
+{
+    if (kp == 0) kp = skinny_tb_kparts(ep.N, K, TB, cu);
+    KSplit ks{};
+    if (kp > 1) {
+        ks = ksplit_slot(s);
+        if (!ks.acc) kp = 1;
+    }
+    switch (kp) {
+    case 2: return launch_dense_tb_kp<DEQUANT, TB, 2>(W, X, ep, K, ks, s);
+    case 4: return launch_dense_tb_kp<DEQUANT, TB, 4>(W, X, ep, K, ks, s);
+    default: return launch_dense_tb_kp<DEQUANT, TB, 1>(W, X, ep, K, ks, s);
+    }
+}
+
+bool dense_tb_supported(int M, int K, int N, int cu)
+{
+    return M > kDecodeMaxM && M <= kSkinnyTbMaxM && K >= kKSplitMinK && K <= kDecodeMaxK && K % 256 == 0 &&
+           divup(N, 16) < cu;
+}
+
+int launch_dense_tb(const int8_t* W, const int8_t* X, const GemmEpilogue& ep, int K, int cu, hipStream_t s, int kp)
+{
+    if (!dense_tb_supported(ep.M, K, ep.N, cu)) return FORGE_EINVAL;
+    const bool dq = ep.c16 != nullptr;
+    if (ep.M <= 32)
+        return dq ? launch_dense_tb_tb<true, 2>(W, X, ep, K, cu, s, kp) : launch_dense_tb_tb<false, 2>(W, X, ep, K, cu, s, kp);
+    return dq ? launch_dense_tb_tb<true, 4>(W, X, ep, K, cu, s, kp) : launch_dense_tb_tb<false, 4>(W, X, ep, K, cu, s, kp);
 }
 
 bool decode_supported(int M, int K) { return M <= kDecodeMaxM && K % 128 == 0 && K <= kDecodeMaxK; }

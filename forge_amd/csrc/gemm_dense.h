@@ -55,6 +55,11 @@ int launch_decode(const int8_t* W, const uint32_t* meta, const int8_t* X, const 
 // row block (exact INT32 hand-off); kp forces the parts (1, 2, 4; 0 = chosen by shape).
 constexpr int kSkinnyTbMaxM = 64;
 bool skinny_tb_supported(int M, int K);
+// Dense 16 < M <= 64 with K >= 4096 (K % 256 == 0, K <= kDecodeMaxK) and N narrow enough that
+// 16-row workgroups are fewer than the CUs: token blocks + K split (kp as launch_skinny_tb).
+bool dense_tb_supported(int M, int K, int N, int cu);
+int launch_dense_tb(const int8_t* W, const int8_t* X, const GemmEpilogue& ep, int K, int cu, hipStream_t s,
+                    int kp = 0);
 int launch_skinny_tb(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep, int K, int cu,
                      hipStream_t s, int kp = 0);
 

@@ -243,6 +243,14 @@ int gemm_dense(const int8_t* A, const int8_t* B, const float* act_scale, const u
         return launch_decode(B, nullptr, A, ep, K, false, s);
     if (M <= kSkinnyMaxM && vec)
         return launch_gemm_skinny(A, B, ep, M, K, N, s);
+    if (vec && M <= kSkinnyTbMaxM) {
+        // 16 < M <= 64, narrow N, deep K: the tile engine has too few tiles (M = 64, K = 6144,
+        // N = 1536: 29.4 us on 64 x 64 tiles, 11.6 us on token blocks with K split in two).
+        int st = FORGE_OK;
+        const DeviceInfo& di = device_info(&st);
+        if (st != FORGE_OK) return st;
+        if (dense_tb_supported(M, K, N, di.cu_count)) return launch_dense_tb(B, A, ep, K, di.cu_count, s);
+    }
     return gemm_tiles(A, B, ep, M, K, N, s);
 }
 

@@ -108,8 +108,13 @@ def test_config4_full_size_sampled(dev, orc, M):
 # 16 < M <= 64: two (M <= 32) or four token blocks, partial last block; K covering every padded
 # per-wave stage count (idle waves at small K, padding stages at 640 / 1152 / 5120); N ragged,
 # odd (element stores), and >= 4096 (32-row workgroups instead of 16).
+# Dense from K = 4096 on (K % 256 == 0, 16-row workgroups fewer than the CUs) runs the dense
+# token-block kernel, with 2 or 4 K parts where N is narrow enough: (40, 5120, 64), (64, 8192, 32),
+# (64, 6144, 1536), (33, 8192, 1000), (20, 4096, 2047) (odd N: element stores), and unsplit at
+# (64, 8192, 4000) and (48, 4352, 300) (17 segments); the rest run the tile engine.
 TB_DENSE = [(17, 128, 48), (32, 384, 200), (33, 640, 201), (48, 1152, 96), (64, 1536, 4160),
-            (40, 5120, 64), (64, 8192, 32), (25, 2048, 4112)]
+            (40, 5120, 64), (64, 8192, 32), (25, 2048, 4112), (64, 6144, 1536), (33, 8192, 1000),
+            (20, 4096, 2047), (64, 8192, 4000), (48, 4352, 300)]
 # From K = 4096 on, narrow N (16-row workgroups fewer than the CUs) splits K over 2 or 4
 # workgroups per row block: (40, 5120, 64), (64, 8192, 32), (64, 6144, 1536), (64, 8192, 1024),
 # (30, 4096, 1008).
