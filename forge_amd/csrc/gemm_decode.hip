@@ -887,48 +887,74 @@ constexpr int kKSplitMaxParts = 8;
 static __device__ int g_ksplit_acc[kKSplitSlots * kKSplitMaxBlocks * 4 * kWave];
 static __device__ unsigned g_ksplit_cnt[kKSplitSlots * kKSplitMaxBlocks];
 
+namespace {
+constexpr int kKSplitMaxDev = 64;
+std::mutex g_ks_mu;
+int* g_ks_acc_dev[kKSplitMaxDev];
+unsigned* g_ks_cnt_dev[kKSplitMaxDev];
+hipStream_t g_ks_owner[kKSplitMaxDev][kKSplitSlots];
+int g_ks_used[kKSplitMaxDev];
+
+// Resolves the slot arrays of device dev (g_ks_mu held); false if they cannot be resolved.
+bool ksplit_resolve(int dev)
+{
+    if (g_ks_acc_dev[dev]) return true;
+    void* a = nullptr;
+    void* c = nullptr;
+    if (hipGetSymbolAddress(&a, HIP_SYMBOL(g_ksplit_acc)) != hipSuccess ||
+        hipGetSymbolAddress(&c, HIP_SYMBOL(g_ksplit_cnt)) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    g_ks_acc_dev[dev] = static_cast<int*>(a);
+    g_ks_cnt_dev[dev] = static_cast<unsigned*>(c);
+    return true;
+}
+}  // namespace
+
+int ksplit_prepare()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kKSplitMaxDev) {
+        (void)hipGetLastError();
+        return FORGE_ENODEV;
+    }
+    std::lock_guard<std::mutex> lock(g_ks_mu);
+    return ksplit_resolve(dev) ? FORGE_OK : FORGE_ENODEV;
+}
+
 // The K-split slot of stream s on the current device, or {} (no split) when every slot is held
 // by another stream, for hipStreamPerThread (one handle for many host threads' streams), or
-// when the slot symbols cannot be resolved. A slot stays with its stream until the process ends.
+// when the slot arrays are not resolved yet and s is capturing a graph (forge_init resolves
+// them outside any capture) or cannot be resolved. A slot stays with its stream until the
+// process ends.
 static KSplit ksplit_slot(hipStream_t s)
 {
-    constexpr int kMaxDev = 64;
-    static std::mutex mu;
-    static int* acc[kMaxDev];
-    static unsigned* cnt[kMaxDev];
-    static bool failed[kMaxDev];
-    static hipStream_t owner[kMaxDev][kKSplitSlots];
-    static int used[kMaxDev];
     if (s == hipStreamPerThread) return {};
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kKSplitMaxDev) {
         (void)hipGetLastError();
         return {};
     }
-    std::lock_guard<std::mutex> lock(mu);
-    if (!acc[dev] && !failed[dev]) {
-        void* a = nullptr;
-        void* c = nullptr;
-        if (hipGetSymbolAddress(&a, HIP_SYMBOL(g_ksplit_acc)) != hipSuccess ||
-            hipGetSymbolAddress(&c, HIP_SYMBOL(g_ksplit_cnt)) != hipSuccess) {
+    std::lock_guard<std::mutex> lock(g_ks_mu);
+    if (!g_ks_acc_dev[dev]) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
             (void)hipGetLastError();
-            failed[dev] = true;
-        } else {
-            acc[dev] = static_cast<int*>(a);
-            cnt[dev] = static_cast<unsigned*>(c);
+            return {};
         }
+        if (cs != hipStreamCaptureStatusNone || !ksplit_resolve(dev)) return {};
     }
-    if (failed[dev]) return {};
     int slot = -1;
-    for (int i = 0; i < used[dev]; i++)
-        if (owner[dev][i] == s) slot = i;
+    for (int i = 0; i < g_ks_used[dev]; i++)
+        if (g_ks_owner[dev][i] == s) slot = i;
     if (slot < 0) {
-        if (used[dev] == kKSplitSlots) return {};
-        slot = used[dev]++;
-        owner[dev][slot] = s;
+        if (g_ks_used[dev] == kKSplitSlots) return {};
+        slot = g_ks_used[dev]++;
+        g_ks_owner[dev][slot] = s;
     }
-    return {acc[dev] + static_cast<size_t>(slot) * kKSplitMaxBlocks * 4 * kWave,
-            cnt[dev] + static_cast<size_t>(slot) * kKSplitMaxBlocks};
+    return {g_ks_acc_dev[dev] + static_cast<size_t>(slot) * kKSplitMaxBlocks * 4 * kWave,
+            g_ks_cnt_dev[dev] + static_cast<size_t>(slot) * kKSplitMaxBlocks};
 }
 
 // K parts for a dense decode launch: doubled while twice the workgroups still fit 1.25 waves

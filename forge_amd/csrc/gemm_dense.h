@@ -53,6 +53,10 @@ int launch_decode(const int8_t* W, const uint32_t* meta, const int8_t* X, const 
 // several 16-token blocks per weight fragment: K % 256 == 0, K <= kDecodeMaxK, 16-byte aligned
 // operands (W_comp, gfx950 index words, tokens). Narrow N splits K over 2 or 4 workgroups per
 // row block (exact INT32 hand-off); kp forces the parts (1, 2, 4; 0 = chosen by shape).
+// Resolves the decode K-split slot arrays on the current device (forge_init calls it, so that a
+// first split launch inside a graph capture needs no symbol lookup).
+int ksplit_prepare();
+
 constexpr int kSkinnyTbMaxM = 64;
 bool skinny_tb_supported(int M, int K);
 // Dense 16 < M <= 64 with K >= 4096 (K % 256 == 0, K <= kDecodeMaxK) and N narrow enough that

@@ -6,6 +6,7 @@
 // std::call_once, so concurrent first calls are safe and a call made before graph
 // capture (forge_init) keeps captured calls free of device queries.
 #include "common.h"
+#include "gemm_dense.h"
 
 #include <mutex>
 
@@ -61,7 +62,8 @@ extern "C" const char* forge_status_string(int status) {
 extern "C" int forge_init(void) {
     int st = FORGE_OK;
     device_info(&st);
-    return st;
+    if (st != FORGE_OK) return st;
+    return ksplit_prepare();
 }
 
 extern "C" int forge_get_compute_capability(int device, int* out_cc) {

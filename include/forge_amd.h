@@ -56,8 +56,10 @@ extern "C" {
 /* Human-readable text for a status code. */
 const char* forge_status_string(int status);
 
-/* One-time per-device setup (device properties). Called implicitly by every entry
- * point; calling it before graph capture keeps captured calls free of device queries. */
+/* One-time per-device setup (device properties, the device addresses of the decode K-split
+ * sum slots). Called implicitly by every entry point; calling it before graph capture keeps
+ * captured calls free of device queries (a capture that starts before any split launch on
+ * the device otherwise records the decode launches unsplit: same bits, slower). */
 int forge_init(void);
 
 /* Replaces forge::gemm::get_compute_capability / has_wmma_int8

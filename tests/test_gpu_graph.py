@@ -47,11 +47,12 @@ def _replay_check(dev, calls, outputs, replays=4):
 
 
 def test_graph_int8_linear(dev):
-    """configs[1]-style fused linear (quantize + dequantizing GEMM), plus the decode shape."""
+    """configs[1]-style fused linear (quantize + dequantizing GEMM), plus decode shapes; (16, 4096,
+    1024) and (40, 8192, 512) split K across workgroups (the sum slots of the capture stream)."""
     import torch
     from forge_amd import ops
     rng = np.random.default_rng(21)
-    for (M, K, N) in [(512, 1024, 768), (16, 4096, 1024), (3, 1152, 96)]:
+    for (M, K, N) in [(512, 1024, 768), (16, 4096, 1024), (3, 1152, 96), (40, 8192, 512)]:
         say(f"graph int8_linear M={M} K={K} N={N}")
         x = to_dev(fp16_normal(rng, (M, K)), dev)
         w = to_dev(int8_uniform(rng, (N, K)), dev)
