@@ -17,13 +17,13 @@ roofline.traffic: HBM bytes per launch of the GEMM, read from TRAFFIC_FILE, whic
 rocprofv3 --pmc runs of `bench.py --traffic-probe` (FETCH_SIZE, then WRITE_SIZE) scaled by
 what the same counters read for a device copy of known size in the same runs.
 extra: configs[2] (2:4 sparse vs dense at 4096x11008x4096), configs[3] (decode
-M = 1/4/16, N = K = 8192, dense and 2:4, HBM GB/s with 6 rotating weight copies so the
-256 MB MALL cannot hold them; calls captured into a HIP graph and replayed so host launch
+M = 1/4/16, N = K = 8192, dense and 2:4, HBM GB/s with 8 dense / 10 sparse rotating weight
+copies so the 256 MB MALL cannot hold them; calls captured into a HIP graph and replayed so host launch
 overhead is not timed; the whole int8_linear / sparse_int8_linear, and the GEMM alone on
 pre-quantized tokens, *_gemm_*), configs[4] (INT8 NHWC 3x3 conv, INT32 and dequant outputs), and
 the rest of the INT8 conv family on NCHW FP16 maps: depthwise 3x3 (1, 64, 540, 960) and
 ConvTranspose2d k2s2 (1, 64, 270, 480) -> (1, 32, 540, 960), as time and HBM GB/s of
-input + output bytes; and SparseLinear's weight preparation at 11008 x 4096 fp32, one pass
+input + output bytes (rotating over more than 256 MB of inputs and outputs, graph-replayed); and SparseLinear's weight preparation at 11008 x 4096 fp32, one pass
 against the reference's separate quantize / prune+compress / pack steps; and
 extra.reference_sweep: the reference's own sparse benchmark (bench_int8_sparse.cu shapes and
 protocol) with the dense path beside it.
@@ -55,6 +55,19 @@ def measured_traffic():
         with open(TRAFFIC_FILE) as f:
             return int(json.load(f)["gemm_bytes_per_launch"])
     except (OSError, ValueError, KeyError):
+        return None
+
+
+COUNTERS_FILE = os.path.join(ROOT, "profiles", "int8_linear_c2_gemm_counters.json")
+
+
+def measured_mfma_busy():
+    """MFMA-busy fraction of the configs[1] GEMM from the committed counter run
+    (SQ_VALU_MFMA_BUSY_CYCLES over SQ_BUSY_CYCLES x 4 SIMDs ... see the file), or None."""
+    try:
+        with open(COUNTERS_FILE) as f:
+            return float(json.load(f)["gemm"]["mfma_busy"])
+    except (OSError, ValueError, KeyError, TypeError):
         return None
 
 
@@ -164,6 +177,20 @@ def graph_median_ms(fn, min_sample_ms: float = 0.2, warmup: int = 50, reps: int 
     return ts[len(ts) // 2] / n
 
 
+def spin(fn, seconds: float) -> None:
+    """Runs fn back to back for `seconds` of GPU time (clocks up before a measurement)."""
+    import torch
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    while True:
+        for _ in range(50):
+            fn()
+        e.record()
+        e.synchronize()
+        if s.elapsed_time(e) >= seconds * 1e3:
+            return
+
+
 def bench_reference_sweep(dev):
     """The reference's own sparse benchmark (benchmarks/bench_int8_sparse.cu:113-114, 235-236):
     sparse_int8_gemm with the dequant epilogue, automatic plan and a split-K workspace, on
@@ -175,6 +202,7 @@ def bench_reference_sweep(dev):
     g = torch.Generator(device=dev)
     g.manual_seed(0)
     gemm, layers, best = {}, {}, 0.0
+    spun = False
     for K, N in ((1536, 6144), (6144, 1536), (1280, 5120), (5120, 1280)):
         W = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
         comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
@@ -191,14 +219,27 @@ def bench_reference_sweep(dev):
             xs = torch.empty((M,), dtype=torch.float32, device=dev)
             out = torch.empty((M, N), dtype=torch.float16, device=dev)
             wsp = torch.empty((M, N), dtype=torch.float32, device=dev)
-            ops.fused_quantize_activation(xh[:M], M, K, out=xq, scales=xs)
-            t_sp = graph_median_ms(lambda: ops.sparse_int8_gemm(comp, xq, meta, xs, ws, b, splitk_workspace=wsp,
-                                                                split_k=0, out=out))
-            t_de = graph_median_ms(lambda: ops.int8_gemm_dequant(xq, W, xs, ws, b, out=out))
+            quant = lambda: ops.fused_quantize_activation(xh[:M], M, K, out=xq, scales=xs)
+            quant()
+            sp = lambda: ops.sparse_int8_gemm(comp, xq, meta, xs, ws, b, splitk_workspace=wsp, split_k=0, out=out)
+            de = lambda: ops.int8_gemm_dequant(xq, W, xs, ws, b, out=out)
+            if not spun:   # the reference spins >= 1 s of GEMMs before its first measurement
+                spin(sp, 1.0)
+                spun = True
+            sp()
+            plan = ops.sparse_int8_gemm_plan(M, K, N, 0, True)
+            route_sp = ops.last_route()
+            de()
+            route_de = ops.last_route()
+            t_sp = graph_median_ms(sp)
+            t_de = graph_median_ms(de)
+            t_q = graph_median_ms(quant)
             tops = 2.0 * M * N * K / t_sp / 1e9
             best = max(best, tops)
             row[str(M)] = {"sparse_us": round(t_sp * 1e3, 2), "sparse_tops": round(tops, 1),
-                           "dense_us": round(t_de * 1e3, 2)}
+                           "dense_us": round(t_de * 1e3, 2), "quant_us": round(t_q * 1e3, 2),
+                           "plan": f"tile{plan[0]} s{plan[1]}", "sparse_engine": route_sp,
+                           "dense_engine": route_de}
         gemm[f"{K}x{N}"] = row
         del W, comp, raw, meta, xh
     for K, N, M in ((1280, 320, 147456), (640, 320, 147456), (640, 640, 36864), (1024, 640, 37008),
@@ -217,12 +258,15 @@ def bench_reference_sweep(dev):
         wsp = torch.empty((M, N), dtype=torch.float32, device=dev)
         t = [graph_median_ms(lambda p=p: ops.sparse_int8_linear(x, comp, meta, ws, b, sq, ss, wsp, 0, p))
              for p in (0, 1, -1)]
+        ops.sparse_int8_linear(x, comp, meta, ws, b, sq, ss, wsp, 0, -1)
         layers[f"{K}x{N}@{M}"] = {"two_pass_us": round(t[0] * 1e3, 2), "fused_us": round(t[1] * 1e3, 2),
-                                  "auto_us": round(t[2] * 1e3, 2)}
+                                  "auto_us": round(t[2] * 1e3, 2), "auto_engine": ops.last_route()}
         del W, comp, raw, meta, x, sq, ss, wsp
     torch.cuda.empty_cache()
-    return {"protocol": "bench_int8_sparse.cu: graph of n calls >= 0.2 ms, 50 warm-up + 100 timed replays, "
-                        "median / n, L2-resident inputs",
+    return {"protocol": "bench_int8_sparse.cu: >= 1 s of GEMMs to reach clock, then per call a graph of n "
+                        "calls >= 0.2 ms, 50 warm-up + 100 timed replays, median / n, L2-resident inputs; "
+                        "quant_us = the per-token quantize of the M x K activations on the same protocol; "
+                        "plan = sparse_int8_gemm_plan (kSparseTile index, split); *_engine = the kernel that ran",
             "gemm": gemm, "layers": layers, "peak_sparse_tops": round(best, 1)}
 
 
@@ -243,9 +287,9 @@ def make_c2(dev, seed=2):
 
 def cpu_baseline(target_s: float = 12.0):
     """The oracle's INT32 loop + dequant epilogue (oracle/) on configs[1] (M = N = K = 4096),
-    split over output rows on up to 16 POSIX threads (the GPU box's CPU share per GPU), over
-    the whole workload; the single-threaded rate over as many rows as fit in about target_s
-    seconds is recorded in the sample text."""
+    split over output rows on the host's cores up to 16 POSIX threads (the GPU box's CPU share
+    per GPU; nproc is recorded), over the whole workload; the single-threaded rate over as many
+    rows as fit in about target_s seconds is recorded in the sample text."""
     from oracle import oracle
     oracle.build()
     rng = np.random.default_rng(2)
@@ -261,7 +305,8 @@ def cpu_baseline(target_s: float = 12.0):
     rows = int(max(32, min(M, target_s / max(t, 1e-6) * rows)))
     t1, _ = oracle.time_gemm_dequant_rows(q, W, s, ws, b, rows)
     tops1 = 2.0 * rows * N * K / t1 / 1e12
-    threads = max(1, min(16, os.cpu_count() or 1))
+    nproc = os.cpu_count() or 1
+    threads = oracle.cpu_threads()
     tm, _ = oracle.time_gemm_dequant_rows_mt(q, W, s, ws, b, M, threads)
     tops = 2.0 * M * N * K / tm / 1e12
     model = "unknown"
@@ -275,7 +320,8 @@ def cpu_baseline(target_s: float = 12.0):
     return {"value": tops, "unit": "TOPS", "cores": threads, "kind": "port",
             "sample": f"oracle INT32 loop + dequant epilogue over all 4096 rows of configs[1] (N=K=4096) split "
                       f"over output rows on {threads} threads: {tm:.2f} s; one thread over {rows} rows: "
-                      f"{t1:.2f} s = {tops1:.4f} TOPS; gcc -O3, host CPU '{model}'"}
+                      f"{t1:.2f} s = {tops1:.4f} TOPS; gcc -O3, host CPU '{model}', nproc {nproc} (threads capped "
+                      f"at 16, the box's CPU share per GPU)"}
 
 
 def bench_extra(dev):
@@ -306,10 +352,11 @@ def bench_extra(dev):
     del W, x, comp, raw, meta, C
     torch.cuda.empty_cache()
 
-    # decode, N = K = 8192, 6 rotating weight copies (384 MB dense)
+    # decode, N = K = 8192; rotating weight copies so that the 256 MB MALL cannot
+    # serve them: 8 dense copies (537 MB), 10 sparse copies (W_comp + index words, 420 MB).
     N = K = 8192
-    copies = 6
-    Ws = [torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8) for _ in range(copies)]
+    copies, sp_copies = 8, 10
+    Ws = [torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8) for _ in range(sp_copies)]
     comps, metas = [], []
     for Wc in Ws:
         cp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
@@ -319,6 +366,7 @@ def bench_extra(dev):
         ops.pack_metadata(rw, mt, N, K)
         comps.append(cp)
         metas.append(mt)
+    del Ws[copies:]
     ws = (torch.rand((N,), generator=g, device=dev) * 9e-3 + 1e-3).half()
     b = (torch.randn((N,), generator=g, device=dev) * 0.1).half()
     for M in (1, 4, 16):
@@ -326,9 +374,9 @@ def bench_extra(dev):
         sq = torch.empty((M, K), dtype=torch.int8, device=dev)
         ss = torch.empty((M,), dtype=torch.float32, device=dev)
         dense = [lambda c=c: ops.int8_linear(xh, Ws[c], ws, b, sq, ss) for c in range(copies)]
-        sparse = [lambda c=c: ops.sparse_int8_linear(xh, comps[c], metas[c], ws, b, sq, ss) for c in range(copies)]
+        sparse = [lambda c=c: ops.sparse_int8_linear(xh, comps[c], metas[c], ws, b, sq, ss) for c in range(sp_copies)]
         td = graph_time_ms(dense * 6)
-        ts = graph_time_ms(sparse * 6)
+        ts = graph_time_ms(sparse * 5)
         bytes_d = N * K + M * K * 2 + M * N * 2 + N * 2 + N * 2
         bytes_s = N * K // 2 + N * K // 8 + M * K * 2 + M * N * 2 + N * 2 + N * 2
         out[f"c4_M{M}_dense_GBs"] = bytes_d / td / 1e6
@@ -340,9 +388,9 @@ def bench_extra(dev):
         ops.fused_quantize_activation(xh, M, K, out=sq, scales=ss)
         y = torch.empty((M, N), dtype=torch.float16, device=dev)
         gd = [lambda c=c: ops.int8_gemm_dequant(sq, Ws[c], ss, ws, b, out=y) for c in range(copies)]
-        gs = [lambda c=c: ops.sparse_int8_gemm(comps[c], sq, metas[c], ss, ws, b, out=y) for c in range(copies)]
+        gs = [lambda c=c: ops.sparse_int8_gemm(comps[c], sq, metas[c], ss, ws, b, out=y) for c in range(sp_copies)]
         tgd = graph_time_ms(gd * 6)
-        tgs = graph_time_ms(gs * 6)
+        tgs = graph_time_ms(gs * 5)
         gbytes_d = N * K + M * K + M * N * 2 + N * 4 + M * 4
         gbytes_s = N * K // 2 + N * K // 8 + M * K + M * N * 2 + N * 4 + M * 4
         out[f"c4_M{M}_dense_gemm_us"] = tgd * 1e3
@@ -381,30 +429,32 @@ def bench_extra(dev):
     # The rest of the INT8 conv family (NCHW FP16 in and out), HBM-bound:
     # depthwise 3x3, pad 1: (1, 64, 540, 960) -> same shape; bytes = input + output;
     # ConvTranspose2d k2s2: (1, 64, 270, 480) -> (1, 32, 540, 960); bytes = input + output + weights.
-    xd = (torch.rand((1, 64, 540, 960), generator=g, device=dev) * 2 - 1).half()
+    # Each leg rotates over enough input/output pairs that the 256 MB MALL cannot hold them
+    # (depthwise: 3 x 133 MB, transposed conv: 6 x 50 MB), graph-replayed.
+    nd, nt = 3, 6
+    xds = [(torch.rand((1, 64, 540, 960), generator=g, device=dev) * 2 - 1).half() for _ in range(nd)]
     wd = torch.randint(-127, 128, (64, 9), generator=g, device=dev, dtype=torch.int8)
     wsd = (torch.rand((64,), generator=g, device=dev) * 0.045 + 0.005).half()
     bd = (torch.rand((64,), generator=g, device=dev) - 0.5).half()
-    yd = torch.empty_like(xd)
-    dw = lambda: ops.int8_depthwise_conv2d_forward(xd, wd, wsd, bd, 3, 3, (1, 1), out=yd)
-    xt = (torch.rand((1, 64, 270, 480), generator=g, device=dev) * 2 - 1).half()
+    yds = [torch.empty_like(xds[0]) for _ in range(nd)]
+    dws = [lambda i=i: ops.int8_depthwise_conv2d_forward(xds[i], wd, wsd, bd, 3, 3, (1, 1), out=yds[i])
+           for i in range(nd)]
+    xts = [(torch.rand((1, 64, 270, 480), generator=g, device=dev) * 2 - 1).half() for _ in range(nt)]
     wt = torch.randint(-127, 128, (4 * 32, 64), generator=g, device=dev, dtype=torch.int8)
     wst = (torch.rand((32,), generator=g, device=dev) * 0.045 + 0.005).half()
     bt = (torch.rand((32,), generator=g, device=dev) - 0.5).half()
-    yt = torch.empty((1, 32, 540, 960), dtype=torch.float16, device=dev)
+    yts = [torch.empty((1, 32, 540, 960), dtype=torch.float16, device=dev) for _ in range(nt)]
     wsp = torch.empty((ops.int8_conv_transpose2d_k2s2_workspace_size(64, 270, 480, 32),), dtype=torch.uint8,
                       device=dev)
-    ct = lambda: ops.int8_conv_transpose2d_k2s2_forward(xt, wt, wst, bt, workspace=wsp, out=yt)
-    for _ in range(3):
-        dw()
-        ct()
-    t_dw = events_time_ms(dw, 20)
-    t_ct = events_time_ms(ct, 20)
+    cts = [lambda i=i: ops.int8_conv_transpose2d_k2s2_forward(xts[i], wt, wst, bt, workspace=wsp, out=yts[i])
+           for i in range(nt)]
+    t_dw = graph_time_ms(dws * 6)
+    t_ct = graph_time_ms(cts * 4)
     out["f2_depthwise_us"] = t_dw * 1e3
-    out["f2_depthwise_GBs"] = (xd.numel() * 2 + yd.numel() * 2) / t_dw / 1e6
+    out["f2_depthwise_GBs"] = (xds[0].numel() * 2 + yds[0].numel() * 2) / t_dw / 1e6
     out["f2_convT_us"] = t_ct * 1e3
-    out["f2_convT_GBs"] = (xt.numel() * 2 + yt.numel() * 2 + wt.numel()) / t_ct / 1e6
-    del xd, yd, xt, yt, wsp
+    out["f2_convT_GBs"] = (xts[0].numel() * 2 + yts[0].numel() * 2 + wt.numel()) / t_ct / 1e6
+    del xds, yds, xts, yts, wsp
     torch.cuda.empty_cache()
 
     # Weight preparation for SparseLinear at configs[2]'s weight (11008 x 4096, fp32): the one
@@ -538,7 +588,8 @@ def main() -> int:
         "config": {"workload": "configs[1] fused W8A8 linear, M=N=K=4096, fp16 in/out",
                    "M": M, "N": N, "K": K, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": measured_traffic(),
+                     "unit": "TOPS", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": measured_traffic(),
+                     "mfma_busy": measured_mfma_busy(),
                      "kernel": "gemm_dma_kernel<256,256,dequant>", "kernel_ms": round(t_gemm, 5),
                      "quantize_ms": round(t_q, 5)},
     }

@@ -22,6 +22,9 @@ _I = ctypes.c_int
 SIGNATURES = {
     "forge_status_string": (ctypes.c_char_p, [_I]),
     "forge_init": (_I, []),
+    "forge_ksplit_last": (_I, [_P, _P]),
+    "forge_ksplit_reset": (_I, [_P]),
+    "forge_last_route": (ctypes.c_char_p, []),
     "forge_get_compute_capability": (_I, [_I, _P]),
     "forge_has_int8_matrix_cores": (_I, [_I, _P]),
     "forge_quantize_activation": (_I, [_P, _P, _P, _I, _I, _P]),

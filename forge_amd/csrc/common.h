@@ -30,6 +30,9 @@ struct DeviceInfo {
 const DeviceInfo& device_info(int* status);
 // Host-only default used where no device exists (planner, CPU tests).
 int default_cu_count();
+// Records the engine of the calling thread's last GEMM launch ("dma256x256", "decode", ...;
+// tile/split appended when >= 0 / > 0), read back by forge_last_route.
+void note_route(const char* engine, int tile = -1, int split = 0);
 
 inline int divup(int a, int b) { return (a + b - 1) / b; }
 inline long long divupll(long long a, long long b) { return (a + b - 1) / b; }

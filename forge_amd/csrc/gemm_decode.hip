@@ -876,24 +876,37 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
 
 // K split for narrow N (row blocks fewer than CUs): the KP workgroups of a row block each take
 // K / KP and hand their sums over (ksplit_handoff). The sums and counters live in static device
-// slots, zero when the code object loads and left zero by every launch, one slot per stream, so
-// calls on different streams never share one (calls on one stream run in order) and nothing is
-// allocated. Measured at M = 16, K = 8192 (128 and 32 row blocks of 32 rows): N = 4096
+// slots, zero when the code object loads and left zero by every launch, so nothing is
+// allocated. Two launches must never use one slot at the same time, so a slot belongs to one
+// key: (stream, 0) for launches made outside graph capture, whose launches on that stream run
+// in order, and (stream, capture id) for launches recorded into a graph, which run in order
+// within each replay of that graph. No key is shared between eager work and a capture, or
+// between two captures; a graph must not be replayed while another replay of the same graph
+// is still running (as for any graph whose nodes share memory). A slot stays with its key
+// until the process ends; with every slot taken, a launch runs unsplit (same bits, no split).
+// Measured at M = 16, K = 8192 (128 and 32 row blocks of 32 rows): N = 4096
 // 13.6 -> 9.9 us, N = 1000 13.2 -> 8.8 us. Where the row blocks already fill the chip the split
 // only adds the hand-off (N = 8192: 14.4 -> 15.2 us), so it is not used there.
-constexpr int kKSplitSlots = 8;
+constexpr int kKSplitSlots = 32;
 constexpr int kKSplitMaxBlocks = 512;   // 16-row blocks per slot (N <= 8192)
 constexpr int kKSplitMaxParts = 8;
-static __device__ int g_ksplit_acc[kKSplitSlots * kKSplitMaxBlocks * 4 * kWave];
+constexpr size_t kKSplitAccPerSlot = static_cast<size_t>(kKSplitMaxBlocks) * 4 * kWave;
+static __device__ int g_ksplit_acc[kKSplitSlots * kKSplitAccPerSlot];
 static __device__ unsigned g_ksplit_cnt[kKSplitSlots * kKSplitMaxBlocks];
 
 namespace {
 constexpr int kKSplitMaxDev = 64;
+struct SlotKey {
+    hipStream_t stream;
+    unsigned long long capture;   // 0: eager launches; otherwise the capture's id
+};
 std::mutex g_ks_mu;
 int* g_ks_acc_dev[kKSplitMaxDev];
 unsigned* g_ks_cnt_dev[kKSplitMaxDev];
-hipStream_t g_ks_owner[kKSplitMaxDev][kKSplitSlots];
+SlotKey g_ks_owner[kKSplitMaxDev][kKSplitSlots];
 int g_ks_used[kKSplitMaxDev];
+thread_local int t_ks_last_slot = -1;   // the calling thread's last decode launch: slot (-1: none)
+thread_local int t_ks_last_kp = 0;      // and its K parts (1: unsplit; 0: no decode launch yet)
 
 // Resolves the slot arrays of device dev (g_ks_mu held); false if they cannot be resolved.
 bool ksplit_resolve(int dev)
@@ -910,51 +923,78 @@ bool ksplit_resolve(int dev)
     g_ks_cnt_dev[dev] = static_cast<unsigned*>(c);
     return true;
 }
+
+bool current_device(int* dev)
+{
+    if (hipGetDevice(dev) != hipSuccess || *dev < 0 || *dev >= kKSplitMaxDev) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return true;
+}
 }  // namespace
 
 int ksplit_prepare()
 {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kKSplitMaxDev) {
-        (void)hipGetLastError();
-        return FORGE_ENODEV;
-    }
+    if (!current_device(&dev)) return FORGE_ENODEV;
     std::lock_guard<std::mutex> lock(g_ks_mu);
     return ksplit_resolve(dev) ? FORGE_OK : FORGE_ENODEV;
 }
 
-// The K-split slot of stream s on the current device, or {} (no split) when every slot is held
-// by another stream, for hipStreamPerThread (one handle for many host threads' streams), or
-// when the slot arrays are not resolved yet and s is capturing a graph (forge_init resolves
-// them outside any capture) or cannot be resolved. A slot stays with its stream until the
-// process ends.
-static KSplit ksplit_slot(hipStream_t s)
+// The K-split slot of the key (s, capture id of s or 0) on the current device, or {} (no split)
+// when every slot is held by other keys, for hipStreamPerThread (one handle for many host
+// threads' streams), when the capture state of s cannot be read, or when the slot arrays are
+// not resolved yet and s is capturing a graph (forge_init resolves them outside any capture).
+static KSplit ksplit_slot(hipStream_t s, int* slot_out)
 {
+    *slot_out = -1;
     if (s == hipStreamPerThread) return {};
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kKSplitMaxDev) {
+    if (!current_device(&dev)) return {};
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    unsigned long long cid = 0;
+    if (hipStreamGetCaptureInfo(s, &cs, &cid) != hipSuccess) {
         (void)hipGetLastError();
         return {};
     }
+    if (cs == hipStreamCaptureStatusInvalidated) return {};
+    const SlotKey key{s, cs == hipStreamCaptureStatusActive ? (cid ? cid : ~0ull) : 0ull};
     std::lock_guard<std::mutex> lock(g_ks_mu);
-    if (!g_ks_acc_dev[dev]) {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
-            (void)hipGetLastError();
-            return {};
-        }
-        if (cs != hipStreamCaptureStatusNone || !ksplit_resolve(dev)) return {};
-    }
+    if (!g_ks_acc_dev[dev] && (key.capture != 0 || !ksplit_resolve(dev))) return {};
     int slot = -1;
     for (int i = 0; i < g_ks_used[dev]; i++)
-        if (g_ks_owner[dev][i] == s) slot = i;
+        if (g_ks_owner[dev][i].stream == key.stream && g_ks_owner[dev][i].capture == key.capture) slot = i;
     if (slot < 0) {
         if (g_ks_used[dev] == kKSplitSlots) return {};
         slot = g_ks_used[dev]++;
-        g_ks_owner[dev][slot] = s;
+        g_ks_owner[dev][slot] = key;
     }
-    return {g_ks_acc_dev[dev] + static_cast<size_t>(slot) * kKSplitMaxBlocks * 4 * kWave,
+    *slot_out = slot;
+    return {g_ks_acc_dev[dev] + static_cast<size_t>(slot) * kKSplitAccPerSlot,
             g_ks_cnt_dev[dev] + static_cast<size_t>(slot) * kKSplitMaxBlocks};
+}
+
+// The K split of one decode launch: kp > 1 takes the slot of the launch's key; without one
+// the launch runs unsplit (kp = 1). Records the decision for forge_ksplit_last.
+static KSplit ksplit_take(hipStream_t s, int& kp)
+{
+    KSplit ks{};
+    int slot = -1;
+    if (kp > 1) {
+        ks = ksplit_slot(s, &slot);
+        if (!ks.acc) kp = 1;
+    }
+    t_ks_last_slot = slot;
+    t_ks_last_kp = kp;
+    return ks;
+}
+
+__global__ __launch_bounds__(256) void ksplit_clear_kernel(int* acc, size_t n_acc, unsigned* cnt, size_t n_cnt)
+{
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_acc; i += stride) acc[i] = 0;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_cnt; i += stride) cnt[i] = 0;
 }
 
 // K parts for a dense decode launch: doubled while twice the workgroups still fit 1.25 waves
@@ -1007,11 +1047,7 @@ static int launch_decode_dense(const int8_t* W, const int8_t* X, const GemmEpilo
         if (st != FORGE_OK) return st;
         kp = decode_dense_kparts(ep.N, K, RB, di.cu_count);
     }
-    KSplit ks{};
-    if (kp > 1) {
-        ks = ksplit_slot(s);
-        if (!ks.acc) kp = 1;
-    }
+    const KSplit ks = ksplit_take(s, kp);
     switch (kp) {
     case 2: return launch_decode_dense_kp<DEQUANT, RB, WV, AH, 2>(W, X, ep, K, ks, s);
     case 4: return launch_decode_dense_kp<DEQUANT, RB, WV, AH, 4>(W, X, ep, K, ks, s);
@@ -1067,11 +1103,7 @@ static int launch_decode_sparse_reg(const int8_t* W, const uint32_t* meta, const
         if (st != FORGE_OK) return st;
         kp = decode_sparse_kparts(ep.N, K, RB, di.cu_count);
     }
-    KSplit ks{};
-    if (kp > 1) {
-        ks = ksplit_slot(s);
-        if (!ks.acc) kp = 1;
-    }
+    const KSplit ks = ksplit_take(s, kp);
     switch (kp) {
     case 2: return launch_decode_sparse_reg_kp<DEQUANT, RB, WV, AH, 2>(W, meta, X, ep, K, ks, s);
     case 4: return launch_decode_sparse_reg_kp<DEQUANT, RB, WV, AH, 4>(W, meta, X, ep, K, ks, s);
@@ -1250,11 +1282,7 @@ static int launch_decode_sparse(const int8_t* W, const uint32_t* meta, const int
         if (st != FORGE_OK) return st;
         kp = decode_ring_kparts(ep.N, K, di.cu_count);
     }
-    KSplit ks{};
-    if (kp > 1) {
-        ks = ksplit_slot(s);
-        if (!ks.acc) kp = 1;
-    }
+    const KSplit ks = ksplit_take(s, kp);
     switch (kp) {
     case 2: return launch_decode_sparse_kp<DEQUANT, 2>(W, meta, X, ep, K, ks, s);
     case 4: return launch_decode_sparse_kp<DEQUANT, 4>(W, meta, X, ep, K, ks, s);
@@ -1327,11 +1355,7 @@ static int launch_tb_sparse_narrow(const int8_t* W, const uint32_t* meta, const 
                                    int K, int cu, hipStream_t s, int kp)
 {
     if (kp == 0) kp = skinny_tb_kparts(ep.N, K, TB, cu);
-    KSplit ks{};
-    if (kp > 1) {
-        ks = ksplit_slot(s);
-        if (!ks.acc) kp = 1;
-    }
+    const KSplit ks = ksplit_take(s, kp);
     switch (kp) {
     case 2: return launch_tb_sparse<DEQUANT, 1, TB, 2>(W, meta, X, ep, K, ks, s);
     case 4: return launch_tb_sparse<DEQUANT, 1, TB, 4>(W, meta, X, ep, K, ks, s);
@@ -1366,11 +1390,7 @@ static int launch_dense_tb_tb(const int8_t* W, const int8_t* X, const GemmEpilog
                               int kp)
 {
     if (kp == 0) kp = skinny_tb_kparts(ep.N, K, TB, cu);
-    KSplit ks{};
-    if (kp > 1) {
-        ks = ksplit_slot(s);
-        if (!ks.acc) kp = 1;
-    }
+    const KSplit ks = ksplit_take(s, kp);
     switch (kp) {
     case 2: return launch_dense_tb_kp<DEQUANT, TB, 2>(W, X, ep, K, ks, s);
     case 4: return launch_dense_tb_kp<DEQUANT, TB, 4>(W, X, ep, K, ks, s);
@@ -1446,11 +1466,7 @@ static int launch_decode_fq_vpr(const int8_t* W, const uint32_t* meta, const Gem
     if (st != FORGE_OK) return st;
     int kp = sparse ? decode_sparse_kparts(ep.N, K, 2, di.cu_count) : decode_dense_kparts(ep.N, K, 1, di.cu_count);
     kp = kp < 4 ? kp : 4;
-    KSplit ks{};
-    if (kp > 1) {
-        ks = ksplit_slot(s);
-        if (!ks.acc) kp = 1;
-    }
+    const KSplit ks = ksplit_take(s, kp);
     switch (kp) {
     case 2: return launch_decode_fq_kp<VPR, 2>(W, meta, ep, K, sparse, fq, ks, s);
     case 4: return launch_decode_fq_kp<VPR, 4>(W, meta, ep, K, sparse, fq, ks, s);
@@ -1492,3 +1508,30 @@ int launch_decode(const int8_t* W, const uint32_t* meta, const int8_t* X, const 
 }
 
 }  // namespace forge_amd
+
+using namespace forge_amd;
+
+extern "C" int forge_ksplit_last(int* slot, int* parts)
+{
+    if (!slot || !parts) return FORGE_EINVAL;
+    *slot = t_ks_last_slot;
+    *parts = t_ks_last_kp;
+    return FORGE_OK;
+}
+
+extern "C" int forge_ksplit_reset(void* stream)
+{
+    int dev = 0;
+    if (!current_device(&dev)) return FORGE_ENODEV;
+    int* acc = nullptr;
+    unsigned* cnt = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_ks_mu);
+        if (!ksplit_resolve(dev)) return FORGE_ENODEV;
+        acc = g_ks_acc_dev[dev];
+        cnt = g_ks_cnt_dev[dev];
+    }
+    ksplit_clear_kernel<<<1024, 256, 0, as_stream(stream)>>>(acc, kKSplitSlots * kKSplitAccPerSlot, cnt,
+                                                             static_cast<size_t>(kKSplitSlots) * kKSplitMaxBlocks);
+    return launch_status();
+}

@@ -164,13 +164,17 @@ static int dispatch_dma(const OpA& opa, const DmaRowMajor& opb, const GemmEpilog
     const TileCfg t = pick_tile(M, N, cu);
     const bool out16 = ep.c16 != nullptr;
     if (t == TileCfg::k256) {
+        note_route("dma256x256+tail192");
         const int r = out16 ? launch_dma_tail_split<true>(opa, opb, ep, M, N, K, cu, s)
                             : launch_dma_tail_split<false>(opa, opb, ep, M, N, K, cu, s);
         if (r != -1) return r;
+        note_route("dma256x256");
         return out16 ? launch_dma<256, 256, true>(opa, opb, ep, M, N, K, s) : launch_dma<256, 256, false>(opa, opb, ep, M, N, K, s);
     }
-    if (t == TileCfg::k128)
+    if (t == TileCfg::k128) {
+        note_route("dma128x128");
         return out16 ? launch_dma<128, 128, true>(opa, opb, ep, M, N, K, s) : launch_dma<128, 128, false>(opa, opb, ep, M, N, K, s);
+    }
     return -1;
 }
 
@@ -184,6 +188,7 @@ static int dispatch_tiles(const OpA& opa, const OpB& opb, const GemmEpilogue& ep
     const int cu = cu_count(&st);
     if (st != FORGE_OK) return st;
     TileCfg t = pick_tile(M, N, cu);
+    note_route(t == TileCfg::k256 && MAX256 ? "regstaged256" : t == TileCfg::k64 ? "regstaged64" : "regstaged128");
     if constexpr (MAX256) {
         if (t == TileCfg::k256) return launch_tile<256, 256, EVEN_K, DEQUANT>(opa, opb, ep, M, N, K, s);
     } else {
@@ -239,17 +244,24 @@ int gemm_dense(const int8_t* A, const int8_t* B, const float* act_scale, const u
     const bool vec = (K % 16 == 0) && aligned(A, 16) && aligned(B, 16);
     GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N,
                     out16 ? out_vec(out16, N, 2) : out_vec(out32, N, 4)};
-    if (vec && decode_supported(M, K))
+    if (vec && decode_supported(M, K)) {
+        note_route("decode");
         return launch_decode(B, nullptr, A, ep, K, false, s);
-    if (M <= kSkinnyMaxM && vec)
+    }
+    if (M <= kSkinnyMaxM && vec) {
+        note_route("skinny");
         return launch_gemm_skinny(A, B, ep, M, K, N, s);
+    }
     if (vec && M <= kSkinnyTbMaxM) {
         // 16 < M <= 64, narrow N, deep K: the tile engine has too few tiles (M = 64, K = 6144,
         // N = 1536: 29.4 us on 64 x 64 tiles, 11.6 us on token blocks with K split in two).
         int st = FORGE_OK;
         const DeviceInfo& di = device_info(&st);
         if (st != FORGE_OK) return st;
-        if (dense_tb_supported(M, K, N, di.cu_count)) return launch_dense_tb(B, A, ep, K, di.cu_count, s);
+        if (dense_tb_supported(M, K, N, di.cu_count)) {
+            note_route("token-block");
+            return launch_dense_tb(B, A, ep, K, di.cu_count, s);
+        }
     }
     return gemm_tiles(A, B, ep, M, K, N, s);
 }
@@ -309,8 +321,10 @@ extern "C" int forge_int8_linear(const uint16_t* x, const int8_t* w, const uint1
     hipStream_t s = as_stream(stream);
     // Decode shapes: one kernel, the quantize fused into the decode GEMM's prologue (each
     // workgroup quantizes the few token rows itself while its first weight stages stream in).
-    if (decode_fq_supported(M, K, false) && aligned(x, 16) && aligned(w, 16) && aligned(scratch_q, 8))
+    if (decode_fq_supported(M, K, false) && aligned(x, 16) && aligned(w, 16) && aligned(scratch_q, 8)) {
+        note_route("decode+quantize");
         return launch_decode_fq(x, w, nullptr, w_scale, bias, out, scratch_q, scratch_scale, M, K, N, false, s);
+    }
     int st = launch_quantize(x, scratch_q, scratch_scale, M, K, s);
     if (st != FORGE_OK) return st;
     return gemm_dense(scratch_q, w, scratch_scale, w_scale, bias, out, nullptr, M, K, N, s);

@@ -999,6 +999,7 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
     if (decode_supported(M, K)) {
         void* o = out16 ? static_cast<void*>(out16) : static_cast<void*>(out32);
         GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N, aligned(o, 16) ? 1 : 0};
+        note_route("decode");
         return launch_decode(W_comp, meta, x, ep, K, true, s);
     }
     // 16 < M <= 64 in automatic mode: the same weight-streaming kernel with several token blocks
@@ -1006,6 +1007,7 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
     if (skinny_tb_supported(M, K) && tile == FORGE_SPARSE_TILE_AUTO && split_k <= 1) {
         void* o = out16 ? static_cast<void*>(out16) : static_cast<void*>(out32);
         GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N, aligned(o, 16) ? 1 : 0};
+        note_route("token-block");
         return launch_skinny_tb(W_comp, meta, x, ep, K, cu_count_or_default(), s);
     }
     int pt = 1, ps = 1;
@@ -1026,6 +1028,7 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
         zero_i32_kernel<<<blocks, 256, 0, s>>>(reinterpret_cast<int4*>(ws), total / 4, ws + (total / 4) * 4,
                                                static_cast<int>(total % 4));
         if ((st = launch_status()) != FORGE_OK) return st;
+        note_route("regstaged", pt, ps);
         if ((st = sparse_launch(pt, p, s)) != FORGE_OK) return st;
         const int fblocks = static_cast<int>(std::min<long long>(divupll(total, 256), 8192));
         splitk_finalize_kernel<<<fblocks, 256, 0, s>>>(ws, act_scale, w_scale, bias, out16, N, total);
@@ -1039,6 +1042,7 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
         GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N, aligned(o, 16) ? 1 : 0};
         const SpEngine e = tile == FORGE_SPARSE_TILE_AUTO ? sparse_pick_engine(M, N, K, cu_count_or_default())
                                                           : SpEngine::k256x128;
+        note_route(e == SpEngine::k256x256 ? "dma256x256" : e == SpEngine::kRing ? "ring128x64" : "dma256x128");
         if (e == SpEngine::k256x256)
             return out16 ? launch_sparse_dma32<true>(W_comp, x, meta, ep, K, s)
                          : launch_sparse_dma32<false>(W_comp, x, meta, ep, K, s);
@@ -1053,6 +1057,7 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
     p.out16 = out16;
     p.out32 = out32;
     p.atomic = 0;
+    note_route("regstaged", pt, 1);
     return sparse_launch(pt, p, s);
 }
 
@@ -1485,11 +1490,15 @@ extern "C" int forge_sparse_int8_linear(const uint16_t* x, const int8_t* W_comp,
     // prologue (one kernel instead of two); like the reference's fused path it leaves the scratch
     // buffers untouched (int8_sparse.cuh:87-89).
     if ((path == 1 || (path == -1 && split_k <= 1)) && decode_fq_supported(M, K, true) && aligned(x, 16) &&
-        aligned(W_comp, 16) && aligned(w_meta, 16))
+        aligned(W_comp, 16) && aligned(w_meta, 16)) {
+        note_route("decode+quantize");
         return launch_decode_fq(x, W_comp, w_meta, w_scale, bias, out, nullptr, nullptr, M, K, N_out, true, s);
+    }
     if (fq_fits(x, W_comp, out, K, N_out) &&
-        (path == 1 || (path == -1 && split_k <= 1 && fq_pays(M, K, N_out))))
+        (path == 1 || (path == -1 && split_k <= 1 && fq_pays(M, K, N_out)))) {
+        note_route("fused-quantize");
         return launch_sparse_fq(x, W_comp, w_meta, w_scale, bias, out, M, K, N_out, s);
+    }
     int st = launch_quantize(x, scratch_q, scratch_scale, M, K, s);
     if (st != FORGE_OK) return st;
     return sparse_gemm(W_comp, scratch_q, w_meta, scratch_scale, w_scale, bias, out, nullptr, M, K, N_out,

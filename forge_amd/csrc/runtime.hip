@@ -8,6 +8,7 @@
 #include "common.h"
 #include "gemm_dense.h"
 
+#include <cstdio>
 #include <mutex>
 
 namespace forge_amd {
@@ -30,6 +31,19 @@ void query(int dev) {
 }  // namespace
 
 int default_cu_count() { return 256; }
+
+namespace {
+thread_local char t_route[48] = "none";
+}
+
+void note_route(const char* engine, int tile, int split)
+{
+    if (tile >= 0 && split > 0) snprintf(t_route, sizeof t_route, "%s tile%d s%d", engine, tile, split);
+    else if (tile >= 0) snprintf(t_route, sizeof t_route, "%s tile%d", engine, tile);
+    else snprintf(t_route, sizeof t_route, "%s", engine);
+}
+
+const char* last_route() { return t_route; }
 
 const DeviceInfo& device_info(int* status) {
     static DeviceInfo none;
@@ -58,6 +72,8 @@ extern "C" const char* forge_status_string(int status) {
     if (status == FORGE_ENODEV) return "no HIP device";
     return hipGetErrorString(static_cast<hipError_t>(status));
 }
+
+extern "C" const char* forge_last_route(void) { return last_route(); }
 
 extern "C" int forge_init(void) {
     int st = FORGE_OK;

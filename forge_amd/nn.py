@@ -1,13 +1,17 @@
 """PyTorch modules of the INT8 path, shaped like the reference's python/forge/nn/linear.py:115-254.
 
 QuantizedLinear and SparseLinear keep the reference's parameter and buffer names, shapes and
-dtypes, so a reference state_dict loads as is:
+dtypes:
 - QuantizedLinear: w_int8 (N, K) int8 buffer, w_scale (N) fp16, bias (N) fp16 or None;
 - SparseLinear: W_comp (N, K/2) int8 buffer, w_meta (N, K/32) int32 buffer, w_scale, bias.
 The one stored difference is the order of the 2:4 index words in w_meta: here the gfx950 SMFMAC
-order (forge_pack_metadata). w_meta_from_reference / w_meta_to_reference convert a whole tensor
-between the reference's row-major words (pack_metadata.cu:23-29) and this layout; the word values
-and the raw nibbles are the same.
+order (forge_pack_metadata), in the reference the row-major order (pack_metadata.cu:23-29); the
+word values and the raw nibbles are the same. SparseLinear's state_dict carries layout version 2
+in its metadata (torch's per-module `version`); load_state_dict converts w_meta from the
+reference order when the version is lower or absent (a reference checkpoint: the reference
+module has torch's default version 1), so a reference state_dict loads as is and computes the
+reference's outputs. w_meta_from_reference / w_meta_to_reference convert a whole tensor on any
+device.
 
 Forward runs the library (forge_int8_linear / forge_sparse_int8_linear); there is no other path.
 """
@@ -109,7 +113,13 @@ class _SparseInt8LinearFn(torch.autograd.Function):
 
 class SparseLinear(nn.Module):
     """2:4 structured-sparse INT8 linear layer (linear.py:206-254). in_features % 64 == 0 and
-    out_features % 16 == 0."""
+    out_features % 16 == 0.
+
+    State-dict layout version 2: w_meta in the gfx950 word order. Loading a state_dict whose
+    metadata says version 1 or nothing (the reference's own modules save version 1) converts
+    w_meta from the reference's row-major order first."""
+
+    _version = 2
 
     def __init__(self, in_features: int, out_features: int, bias: bool = True):
         super().__init__()
@@ -139,6 +149,21 @@ class SparseLinear(nn.Module):
         q, s = self._scratch(M, K, x.device)
         return _SparseInt8LinearFn.apply(x, self.W_comp, self.w_meta, self.w_scale, self.bias, q, s)
 
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                              error_msgs):
+        version = local_metadata.get("version", None) if local_metadata else None
+        key = prefix + "w_meta"
+        if (version is None or version < 2) and key in state_dict:
+            meta = state_dict[key]
+            if meta.dim() != 2 or meta.shape[1] * 32 != self.in_features or meta.shape[0] != self.out_features:
+                error_msgs.append(f"{key}: expected a ({self.out_features}, {self.in_features // 32}) tensor of the "
+                                  f"reference's index words, got {tuple(meta.shape)}")
+                return
+            state_dict = dict(state_dict)
+            state_dict[key] = w_meta_from_reference(meta.to(torch.int32))
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                                      error_msgs)
+
     @torch.no_grad()
     def from_dense_weight(self, weight_fp: torch.Tensor) -> None:
         """linear.py:231-249 in one device pass (forge_prepare_sparse_weight): quantize per row
@@ -154,26 +179,29 @@ class SparseLinear(nn.Module):
                 f"bias={self.bias is not None}, sparse=2:4")
 
 
+def _gfx950_word_positions(N: int, W: int, device) -> torch.Tensor:
+    """Position in the gfx950 layout of reference word (n, c) (row-major index n * W + c):
+    (n / 16) * W * 16 + c * R + n % 16, R = the rows of n's 16-row block (16, or fewer in a
+    ragged last block), as forge_pack_metadata stores them."""
+    n = torch.arange(N, device=device, dtype=torch.int64).unsqueeze(1)
+    c = torch.arange(W, device=device, dtype=torch.int64).unsqueeze(0)
+    blk = n // 16
+    rows = torch.clamp(N - 16 * blk, max=16)
+    return (blk * W * 16 + c * rows + n % 16).reshape(-1)
+
+
 def w_meta_from_reference(w_meta_ref: torch.Tensor) -> torch.Tensor:
     """The reference's (N, K/32) int32 index words (word (n, c) = sum_g nib[n, 8c+g] << 4g,
     pack_metadata.cu:23-29) -> the same words in the gfx950 order, on the tensor's device."""
     N, W = w_meta_ref.shape
-    K = W * 32
-    words = w_meta_ref.contiguous().view(torch.int32)
-    shifts = torch.arange(0, 32, 4, device=words.device, dtype=torch.int32)
-    nibs = torch.bitwise_and(torch.bitwise_right_shift(words.unsqueeze(-1), shifts), 0xF).to(torch.uint8)
-    raw = nibs.reshape(-1).contiguous()
-    out = torch.empty(N, W, dtype=torch.int32, device=words.device)
-    ops.pack_metadata(raw, out, N, K)
-    return out
+    src = w_meta_ref.contiguous().view(torch.int32).reshape(-1)
+    out = torch.empty(N * W, dtype=torch.int32, device=src.device)
+    out[_gfx950_word_positions(N, W, src.device)] = src
+    return out.view(N, W)
 
 
 def w_meta_to_reference(w_meta: torch.Tensor) -> torch.Tensor:
     """Inverse of w_meta_from_reference: gfx950-order words -> the reference's row-major words."""
     N, W = w_meta.shape
-    K = W * 32
-    raw = torch.empty(N * K // 4, dtype=torch.uint8, device=w_meta.device)
-    ops.unpack_metadata(w_meta.contiguous(), raw, N, K)
-    nibs = raw.view(N, W, 8).to(torch.int32)
-    shifts = torch.arange(0, 32, 4, device=w_meta.device, dtype=torch.int32)
-    return torch.bitwise_left_shift(nibs, shifts).sum(dim=-1, dtype=torch.int64).to(torch.int32)
+    src = w_meta.contiguous().view(torch.int32).reshape(-1)
+    return src[_gfx950_word_positions(N, W, src.device)].view(N, W).clone()

@@ -80,6 +80,44 @@ def fused_dequantize_bias(input: torch.Tensor, act_scale: torch.Tensor, w_scale:
     return out
 
 
+# ---- decode K-split slots (extension) ---------------------------------------------
+
+def ksplit_last() -> Tuple[int, int]:
+    """(slot, K parts) of this thread's last decode launch: slot -1 = no slot (unsplit)."""
+    import ctypes
+    slot, parts = ctypes.c_int(), ctypes.c_int()
+    _call("forge_ksplit_last", ctypes.addressof(slot), ctypes.addressof(parts))
+    return slot.value, parts.value
+
+
+def last_route() -> str:
+    """The engine of this thread's last GEMM launch (forge_last_route)."""
+    return _lib.load().forge_last_route().decode()
+
+
+def ksplit_reset() -> None:
+    """Zeroes every decode K-split slot of the current device on torch's current stream."""
+    _call("forge_ksplit_reset", _stream())
+
+
+# ---- device queries (int8_gemm.cuh:18-24) ----------------------------------------
+
+def get_compute_capability(device: int = 0) -> int:
+    """forge_get_compute_capability: 100 * major + 10 * minor of the HIP device (gfx950 -> 950)."""
+    import ctypes
+    v = ctypes.c_int()
+    _call("forge_get_compute_capability", device, ctypes.addressof(v))
+    return v.value
+
+
+def has_int8_matrix_cores(device: int = 0) -> bool:
+    """forge_has_int8_matrix_cores (the reference's has_wmma_int8): INT8 MFMA / SMFMAC present."""
+    import ctypes
+    v = ctypes.c_int()
+    _call("forge_has_int8_matrix_cores", device, ctypes.addressof(v))
+    return bool(v.value)
+
+
 # ---- dense GEMM (bindings.cpp:498-519) -------------------------------------------
 
 def int8_linear(x: torch.Tensor, w_int8: torch.Tensor, w_scale: torch.Tensor, bias: Optional[torch.Tensor],
@@ -118,6 +156,25 @@ def int8_gemm_dequant(A: torch.Tensor, B: torch.Tensor, act_scale: torch.Tensor,
     _need(out, torch.float16, "out", M * N)
     _call("forge_int8_gemm_dequant", _p(A), _p(B), _p(act_scale), _p(w_scale), _p(bias), _p(out),
           M, K, N, _stream())
+    return out
+
+
+def int8_gemm(A: torch.Tensor, B: torch.Tensor, act_scale: torch.Tensor, w_scale: torch.Tensor,
+              bias: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The reference's capability-dispatching int8_gemm (int8_gemm.cu:26-46): on gfx950 always the
+    matrix-core GEMM, so it equals int8_gemm_dequant."""
+    M, K = A.shape
+    N = B.shape[0]
+    _need(A, torch.int8, "A")
+    _need(B, torch.int8, "B", N * K)
+    _need(act_scale, torch.float32, "act_scale", M)
+    _need(w_scale, torch.float16, "w_scale", N)
+    if bias is not None:
+        _need(bias, torch.float16, "bias", N)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=A.device)
+    _need(out, torch.float16, "out", M * N)
+    _call("forge_int8_gemm", _p(A), _p(B), _p(act_scale), _p(w_scale), _p(bias), _p(out), M, K, N, _stream())
     return out
 
 
@@ -213,7 +270,8 @@ def sparse_int8_linear_fused(M: int, K: int, N_out: int) -> bool:
 def sparse_int8_linear(x: torch.Tensor, W_comp: torch.Tensor, w_meta: torch.Tensor, w_scale: torch.Tensor,
                        bias: Optional[torch.Tensor], scratch_x_int8: torch.Tensor, scratch_x_scale: torch.Tensor,
                        splitk_workspace: Optional[torch.Tensor] = None, split_k: int = 1,
-                       path: int = -1) -> torch.Tensor:
+                       path: int = -1, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """int8_sparse.cuh:92-105; `out` may be passed to reuse an (M, N) FP16 buffer."""
     M, K = x.shape
     N = W_comp.shape[0]
     _need(x, torch.float16, "x")
@@ -231,17 +289,23 @@ def sparse_int8_linear(x: torch.Tensor, W_comp: torch.Tensor, w_meta: torch.Tens
         ws = torch.empty((M, N), dtype=torch.float32, device=x.device)
     if ws is not None:
         _need(ws, torch.float32, "splitk_workspace", M * N)
-    out = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    _need(out, torch.float16, "out", M * N)
     _call("forge_sparse_int8_linear", _p(x), _p(W_comp), _p(w_meta), _p(w_scale), _p(bias), _p(out), M, K, N,
           _p(scratch_x_int8), _p(scratch_x_scale), _p(ws), split_k, _stream(), path)
     return out
 
 
-def splitk_reduce(workspace: torch.Tensor, bias: Optional[torch.Tensor], M: int, N: int) -> torch.Tensor:
+def splitk_reduce(workspace: torch.Tensor, bias: Optional[torch.Tensor], M: int, N: int,
+                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """int8_sparse.cuh:107-114: FP32 (M, N) workspace [+ bias] -> FP16."""
     _need(workspace, torch.float32, "workspace", M * N)
     if bias is not None:
         _need(bias, torch.float16, "bias", N)
-    out = torch.empty((M, N), dtype=torch.float16, device=workspace.device)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=workspace.device)
+    _need(out, torch.float16, "out", M * N)
     _call("forge_splitk_reduce", _p(workspace), _p(bias), _p(out), M, N, _stream())
     return out
 

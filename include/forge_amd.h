@@ -62,6 +62,25 @@ const char* forge_status_string(int status);
  * the device otherwise records the decode launches unsplit: same bits, slower). */
 int forge_init(void);
 
+/* Decode K-split slots (no counterpart in the reference, whose split-K takes a caller
+ * workspace). Decode launches for narrow N split K over several workgroups that hand exact
+ * INT32 partial sums over through static device slots, one slot per (stream, graph capture)
+ * key. forge_ksplit_last reports the calling thread's last decode launch: the slot it used
+ * (-1: none) and its K parts (1: unsplit; 0: no decode launch yet on this thread).
+ * forge_ksplit_reset zeroes every slot of the current device, in stream order on `stream`;
+ * call it only when no decode launch is in flight on the device (a launch is left
+ * unfinished only by a device fault or an aborted graph). */
+int forge_ksplit_last(int* slot, int* parts);
+int forge_ksplit_reset(void* stream);
+
+/* The engine of the calling thread's last GEMM launch made through this library (no
+ * counterpart in the reference; its benchmark prints the plan it computes itself,
+ * benchmarks/bench_int8_sparse.cu:164-170): e.g. "dma256x256", "ring128x64", "decode",
+ * "decode+quantize", "token-block", "fused-quantize", "regstaged tile1 s3"
+ * (tile = the reference's kSparseTile* index, s = split-K parts). "none" before any launch.
+ * The string belongs to the library and stays valid until the thread's next GEMM call. */
+const char* forge_last_route(void);
+
 /* Replaces forge::gemm::get_compute_capability / has_wmma_int8
  * (include/forge/gemm/int8_gemm.cuh:18-23). On gfx950 the "compute capability"
  * is the gfx IP version 950 and INT8 matrix cores are always present. */

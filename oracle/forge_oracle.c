@@ -123,6 +123,18 @@ void orc_dequantize_bias(const int32_t* acc, const float* act_scale, const uint1
     }
 }
 
+/* Split-K finalize, src/gemm/int8_sparse.cu:99-111: out = half(ws [+ float(bias[n])]), one
+ * fp32 addition then fp16 RNE. */
+void orc_splitk_reduce(const float* ws, const uint16_t* bias, uint16_t* out, int M, int N)
+{
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            float v = ws[(size_t)m * N + n];
+            if (bias) v += orc_f16_to_f32(bias[n]);
+            out[(size_t)m * N + n] = orc_f32_to_f16(v);
+        }
+}
+
 /* ------------------------------------------------------------------------- */
 /* Dense INT8 GEMM, C = A (M,K) x B (N,K)^T with INT32 accumulation           */
 /* tests/test_int8_dense_gemm.cu:35-39; tests/test_int8_dp4a_gemm.cu:15-30    */
@@ -303,30 +315,42 @@ int orc_conv_out_size(int in, int pad, int dil, int k, int stride)
     return (in + 2 * pad - dil * (k - 1) - 1) / stride + 1;
 }
 
+/* Output pixel rows r0 <= r < r1 (r = n * Ho + ho) of the direct convolution. */
+static void conv2d_nhwc_s32_rows(const int8_t* x, const int8_t* w, int32_t* out,
+                                 int H, int W, int C, int Co, int kH, int kW,
+                                 int padH, int padW, int strideH, int strideW, int dilH, int dilW,
+                                 int Ho, int Wo, int r0, int r1)
+{
+    for (int r = r0; r < r1; r++) {
+        const int n = r / Ho, ho = r % Ho;
+        for (int wo = 0; wo < Wo; wo++)
+            for (int co = 0; co < Co; co++) {
+                int32_t acc = 0;
+                for (int kh = 0; kh < kH; kh++) {
+                    const int hi = ho * strideH + kh * dilH - padH;
+                    if (hi < 0 || hi >= H) continue;
+                    for (int kw = 0; kw < kW; kw++) {
+                        const int wi = wo * strideW + kw * dilW - padW;
+                        if (wi < 0 || wi >= W) continue;
+                        const int8_t* xp = x + (((size_t)n * H + hi) * W + wi) * C;
+                        const int8_t* wp = w + (((size_t)co * kH + kh) * kW + kw) * C;
+                        for (int c = 0; c < C; c++) acc += (int32_t)xp[c] * (int32_t)wp[c];
+                    }
+                }
+                out[(((size_t)n * Ho + ho) * Wo + wo) * Co + co] = acc;
+            }
+    }
+}
+
 void orc_conv2d_nhwc_s32(const int8_t* x, const int8_t* w, int32_t* out,
                          int N, int H, int W, int C, int Co, int kH, int kW,
                          int padH, int padW, int strideH, int strideW, int dilH, int dilW)
 {
     const int Ho = orc_conv_out_size(H, padH, dilH, kH, strideH);
     const int Wo = orc_conv_out_size(W, padW, dilW, kW, strideW);
-    for (int n = 0; n < N; n++)
-        for (int ho = 0; ho < Ho; ho++)
-            for (int wo = 0; wo < Wo; wo++)
-                for (int co = 0; co < Co; co++) {
-                    int32_t acc = 0;
-                    for (int kh = 0; kh < kH; kh++) {
-                        const int hi = ho * strideH + kh * dilH - padH;
-                        if (hi < 0 || hi >= H) continue;
-                        for (int kw = 0; kw < kW; kw++) {
-                            const int wi = wo * strideW + kw * dilW - padW;
-                            if (wi < 0 || wi >= W) continue;
-                            const int8_t* xp = x + (((size_t)n * H + hi) * W + wi) * C;
-                            const int8_t* wp = w + (((size_t)co * kH + kh) * kW + kw) * C;
-                            for (int c = 0; c < C; c++) acc += (int32_t)xp[c] * (int32_t)wp[c];
-                        }
-                    }
-                    out[(((size_t)n * Ho + ho) * Wo + wo) * Co + co] = acc;
-                }
+    if (Ho <= 0 || Wo <= 0) return;
+    conv2d_nhwc_s32_rows(x, w, out, H, W, C, Co, kH, kW, padH, padW, strideH, strideW, dilH, dilW,
+                         Ho, Wo, 0, N * Ho);
 }
 
 /* ------------------------------------------------------------------------- */
@@ -536,4 +560,102 @@ double orc_time_gemm_dequant_rows(const int8_t* A, const int8_t* B, const float*
     clock_gettime(CLOCK_MONOTONIC, &t1);
     free(acc);
     return (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Threaded forms of the GEMM and conv loops (for whole-output comparisons at  */
+/* full size). Each thread runs the single-threaded code on a contiguous range */
+/* of output rows, so every output has the same bits as the plain function.    */
+/* ------------------------------------------------------------------------- */
+
+typedef struct {
+    int kind; /* 0 gemm_s32, 1 gemm_dequant, 2 conv */
+    const int8_t *A, *B;
+    const float* act_scale;
+    const uint16_t *w_scale, *bias;
+    uint16_t* out16;
+    int32_t* C;
+    int r0, r1, K, N;
+    /* conv geometry */
+    int H, W, Cc, Co, kH, kW, padH, padW, sH, sW, dH, dW, Ho, Wo;
+} orc_range_job;
+
+static void* orc_range_worker(void* p)
+{
+    const orc_range_job* j = (const orc_range_job*)p;
+    if (j->r1 <= j->r0) return NULL;
+    if (j->kind == 2) {
+        conv2d_nhwc_s32_rows(j->A, j->B, j->C, j->H, j->W, j->Cc, j->Co, j->kH, j->kW, j->padH, j->padW,
+                             j->sH, j->sW, j->dH, j->dW, j->Ho, j->Wo, j->r0, j->r1);
+        return NULL;
+    }
+    orc_gemm_s32_rows(j->A, j->B, j->C, j->r0, j->r1, j->K, j->N);
+    if (j->kind == 1)
+        orc_dequant_epilogue(j->C + (size_t)j->r0 * j->N, j->act_scale + j->r0, j->w_scale, j->bias,
+                             j->out16 + (size_t)j->r0 * j->N, j->r1 - j->r0, j->N);
+    return NULL;
+}
+
+static void orc_run_rows(const orc_range_job* proto, int rows, int threads)
+{
+    if (threads < 1) threads = 1;
+    if (threads > 256) threads = 256;
+    if (threads > rows) threads = rows > 0 ? rows : 1;
+    pthread_t tid[256];
+    orc_range_job jobs[256];
+    int started[256];
+    for (int t = 0; t < threads; t++) {
+        jobs[t] = *proto;
+        jobs[t].r0 = (int)((long long)rows * t / threads);
+        jobs[t].r1 = (int)((long long)rows * (t + 1) / threads);
+        started[t] = pthread_create(&tid[t], NULL, orc_range_worker, &jobs[t]) == 0;
+        if (!started[t]) orc_range_worker(&jobs[t]);   /* no thread: run the range here */
+    }
+    for (int t = 0; t < threads; t++)
+        if (started[t]) pthread_join(tid[t], NULL);
+}
+
+void orc_gemm_s32_mt(const int8_t* A, const int8_t* B, int32_t* C, int M, int K, int N, int threads)
+{
+    orc_range_job j;
+    memset(&j, 0, sizeof j);
+    j.kind = 0; j.A = A; j.B = B; j.C = C; j.K = K; j.N = N;
+    orc_run_rows(&j, M, threads);
+}
+
+void orc_gemm_dequant_mt(const int8_t* A, const int8_t* B, const float* act_scale,
+                         const uint16_t* w_scale, const uint16_t* bias, uint16_t* out,
+                         int M, int K, int N, int threads)
+{
+    int32_t* acc = (int32_t*)malloc((size_t)M * N * sizeof(int32_t));
+    orc_range_job j;
+    memset(&j, 0, sizeof j);
+    j.kind = 1; j.A = A; j.B = B; j.C = acc; j.K = K; j.N = N;
+    j.act_scale = act_scale; j.w_scale = w_scale; j.bias = bias; j.out16 = out;
+    orc_run_rows(&j, M, threads);
+    free(acc);
+}
+
+void orc_sparse_gemm_s32_mt(const int8_t* W_comp, const int8_t* x, const uint8_t* meta_raw,
+                            int32_t* C, int M, int K, int N, int threads)
+{
+    int8_t* wd = (int8_t*)malloc((size_t)N * K);
+    orc_decompress_24(W_comp, meta_raw, wd, N, K);
+    orc_gemm_s32_mt(x, wd, C, M, K, N, threads);
+    free(wd);
+}
+
+void orc_conv2d_nhwc_s32_mt(const int8_t* x, const int8_t* w, int32_t* out,
+                            int N, int H, int W, int C, int Co, int kH, int kW,
+                            int padH, int padW, int strideH, int strideW, int dilH, int dilW, int threads)
+{
+    const int Ho = orc_conv_out_size(H, padH, dilH, kH, strideH);
+    const int Wo = orc_conv_out_size(W, padW, dilW, kW, strideW);
+    if (Ho <= 0 || Wo <= 0) return;
+    orc_range_job j;
+    memset(&j, 0, sizeof j);
+    j.kind = 2; j.A = x; j.B = w; j.C = out;
+    j.H = H; j.W = W; j.Cc = C; j.Co = Co; j.kH = kH; j.kW = kW; j.padH = padH; j.padW = padW;
+    j.sH = strideH; j.sW = strideW; j.dH = dilH; j.dW = dilW; j.Ho = Ho; j.Wo = Wo;
+    orc_run_rows(&j, N * Ho, threads);
 }

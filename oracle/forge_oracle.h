@@ -13,6 +13,8 @@
  *                                     .5 ties with scale 1.0 / 2.0), invariants (|q|<=127, absmax
  *                                     element -> +-127, |x - q*scale| <= scale/2), numpy fp32 path
  *   orc_dequantize_bias               float64 evaluation of the same expression (<= 1 fp16 ulp)
+ *   orc_splitk_reduce                 numpy float32 addition + float16 conversion; the bias-less
+ *                                     case as a plain RNE conversion
  *   orc_gemm_s32                      numpy int64 matmul; all-ones and identity closed forms
  *   orc_gemm_dequant                  float64 evaluation (<= 1 fp16 ulp)
  *   orc_prune_compress_24             hand-derived known answers; exhaustive brute force over all
@@ -36,6 +38,8 @@
  *                                     float64 dequantized conv_transpose2d (<= 2 fp16 ulps);
  *                                     the quantize stage is orc_quantize_rows (pinned above)
  *   orc_mt19937                       the C++ standard's 10000th-output check (4123659995)
+ *   orc_*_mt (threaded forms)         bit-identical to the single-threaded functions above on
+ *                                     shapes whose row count does not divide the thread count
  */
 #ifndef FORGE_ORACLE_H
 #define FORGE_ORACLE_H
@@ -52,6 +56,7 @@ uint16_t orc_f32_to_f16(float f);
 void orc_quantize_rows(const uint16_t* x, int8_t* q, float* scales, int M, int K);
 void orc_dequantize_bias(const int32_t* acc, const float* act_scale, const uint16_t* w_scale,
                          const uint16_t* bias, uint16_t* out, int M, int N);
+void orc_splitk_reduce(const float* ws, const uint16_t* bias, uint16_t* out, int M, int N);
 void orc_gemm_s32(const int8_t* A, const int8_t* B, int32_t* C, int M, int K, int N);
 void orc_gemm_s32_rows(const int8_t* A, const int8_t* B, int32_t* C, int m0, int m1, int K, int N);
 void orc_dequant_epilogue(const int32_t* acc, const float* act_scale, const uint16_t* w_scale,
@@ -94,6 +99,19 @@ double orc_time_gemm_dequant_rows_mt(const int8_t* A, const int8_t* B, const flo
 double orc_time_gemm_dequant_rows(const int8_t* A, const int8_t* B, const float* act_scale,
                                   const uint16_t* w_scale, const uint16_t* bias, uint16_t* out,
                                   int rows, int K, int N);
+
+/* The same functions split over output rows (conv: output pixel rows) on `threads` POSIX
+ * threads, so full-size results can be compared whole; each output is computed by exactly
+ * the single-threaded code on its own row range, so the bits are those of the functions above. */
+void orc_gemm_s32_mt(const int8_t* A, const int8_t* B, int32_t* C, int M, int K, int N, int threads);
+void orc_gemm_dequant_mt(const int8_t* A, const int8_t* B, const float* act_scale,
+                         const uint16_t* w_scale, const uint16_t* bias, uint16_t* out,
+                         int M, int K, int N, int threads);
+void orc_sparse_gemm_s32_mt(const int8_t* W_comp, const int8_t* x, const uint8_t* meta_raw,
+                            int32_t* C, int M, int K, int N, int threads);
+void orc_conv2d_nhwc_s32_mt(const int8_t* x, const int8_t* w, int32_t* out,
+                            int N, int H, int W, int C, int Co, int kH, int kW,
+                            int padH, int padW, int strideH, int strideW, int dilH, int dilW, int threads);
 
 #ifdef __cplusplus
 }

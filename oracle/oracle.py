@@ -43,6 +43,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_quantize_rows.argtypes = [_P, _P, _P, _I, _I]
     L.orc_dequantize_bias.argtypes = [_P, _P, _P, _P, _P, _I, _I]
     L.orc_gemm_s32.argtypes = [_P, _P, _P, _I, _I, _I]
+    L.orc_splitk_reduce.argtypes = [_P, _P, _P, _I, _I]
     L.orc_gemm_s32_rows.argtypes = [_P, _P, _P, _I, _I, _I, _I]
     L.orc_dequant_epilogue.argtypes = [_P, _P, _P, _P, _P, _I, _I]
     L.orc_gemm_dequant.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I]
@@ -66,6 +67,20 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_time_gemm_dequant_rows.restype = ctypes.c_double
     L.orc_time_gemm_dequant_rows_mt.argtypes = [_P] * 6 + [_I] * 4
     L.orc_time_gemm_dequant_rows_mt.restype = ctypes.c_double
+    L.orc_gemm_s32_mt.argtypes = [_P, _P, _P, _I, _I, _I, _I]
+    L.orc_gemm_dequant_mt.argtypes = [_P] * 6 + [_I] * 4
+    L.orc_sparse_gemm_s32_mt.argtypes = [_P] * 4 + [_I] * 4
+    L.orc_conv2d_nhwc_s32_mt.argtypes = [_P, _P, _P] + [_I] * 14
+
+
+def cpu_threads() -> int:
+    """Threads for the oracle's threaded loops: the host's cores, at most 16 (a GPU box's
+    CPU share per GPU)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
 
 
 def _p(a):
@@ -106,13 +121,26 @@ def dequantize_bias(acc, act_scale, w_scale16, bias16=None):
     return out.view(np.float16)
 
 
-def gemm_s32(A, B):
+def splitk_reduce(ws, bias16=None):
+    """fp32 (M, N) split-K workspace [+ fp16 bias] -> fp16 (int8_sparse.cu:99-111)."""
+    ws = np.ascontiguousarray(ws, np.float32)
+    M, N = ws.shape
+    b = None if bias16 is None else _u16(bias16)
+    out = np.empty((M, N), np.uint16)
+    lib().orc_splitk_reduce(_p(ws), _p(b), _p(out), M, N)
+    return out.view(np.float16)
+
+
+def gemm_s32(A, B, threads: int = 1):
     A = np.ascontiguousarray(A, np.int8)
     B = np.ascontiguousarray(B, np.int8)
     M, K = A.shape
     N = B.shape[0]
     C = np.empty((M, N), np.int32)
-    lib().orc_gemm_s32(_p(A), _p(B), _p(C), M, K, N)
+    if threads > 1:
+        lib().orc_gemm_s32_mt(_p(A), _p(B), _p(C), M, K, N, threads)
+    else:
+        lib().orc_gemm_s32(_p(A), _p(B), _p(C), M, K, N)
     return C
 
 
@@ -127,13 +155,24 @@ def dequant_epilogue(acc, act_scale, w_scale16, bias16=None):
     return out.view(np.float16)
 
 
-def gemm_dequant(A, B, act_scale, w_scale16, bias16=None):
-    return dequant_epilogue(gemm_s32(A, B), act_scale, w_scale16, bias16)
+def gemm_dequant(A, B, act_scale, w_scale16, bias16=None, threads: int = 1):
+    if threads <= 1:
+        return dequant_epilogue(gemm_s32(A, B), act_scale, w_scale16, bias16)
+    A = np.ascontiguousarray(A, np.int8)
+    B = np.ascontiguousarray(B, np.int8)
+    M, K = A.shape
+    N = B.shape[0]
+    as_ = np.ascontiguousarray(act_scale, np.float32)
+    ws = _u16(w_scale16)
+    b = None if bias16 is None else _u16(bias16)
+    out = np.empty((M, N), np.uint16)
+    lib().orc_gemm_dequant_mt(_p(A), _p(B), _p(as_), _p(ws), _p(b), _p(out), M, K, N, threads)
+    return out.view(np.float16)
 
 
-def linear(x16, W, w_scale16, bias16=None):
+def linear(x16, W, w_scale16, bias16=None, threads: int = 1):
     q, s = quantize_rows(x16)
-    return gemm_dequant(q, W, s, w_scale16, bias16), q, s
+    return gemm_dequant(q, W, s, w_scale16, bias16, threads=threads), q, s
 
 
 def prune_compress_24(w):
@@ -174,13 +213,16 @@ def unpack_metadata_gfx950(packed, N, K):
     return out
 
 
-def sparse_gemm_s32(W_comp, x, meta_raw, N, K):
+def sparse_gemm_s32(W_comp, x, meta_raw, N, K, threads: int = 1):
     W_comp = np.ascontiguousarray(W_comp, np.int8)
     x = np.ascontiguousarray(x, np.int8)
     meta = np.ascontiguousarray(meta_raw, np.uint8)
     M = x.shape[0]
     C = np.empty((M, N), np.int32)
-    lib().orc_sparse_gemm_s32(_p(W_comp), _p(x), _p(meta), _p(C), M, K, N)
+    if threads > 1:
+        lib().orc_sparse_gemm_s32_mt(_p(W_comp), _p(x), _p(meta), _p(C), M, K, N, threads)
+    else:
+        lib().orc_sparse_gemm_s32(_p(W_comp), _p(x), _p(meta), _p(C), M, K, N)
     return C
 
 
@@ -188,7 +230,7 @@ def conv_out_size(i, pad, dil, k, stride):
     return lib().orc_conv_out_size(i, pad, dil, k, stride)
 
 
-def conv2d_nhwc_s32(x, w, pad=(0, 0), stride=(1, 1), dil=(1, 1)):
+def conv2d_nhwc_s32(x, w, pad=(0, 0), stride=(1, 1), dil=(1, 1), threads: int = 1):
     x = np.ascontiguousarray(x, np.int8)
     w = np.ascontiguousarray(w, np.int8)
     N, H, W, C = x.shape
@@ -197,8 +239,11 @@ def conv2d_nhwc_s32(x, w, pad=(0, 0), stride=(1, 1), dil=(1, 1)):
     Ho = conv_out_size(H, pad[0], dil[0], kH, stride[0])
     Wo = conv_out_size(W, pad[1], dil[1], kW, stride[1])
     out = np.empty((N, Ho, Wo, Co), np.int32)
-    lib().orc_conv2d_nhwc_s32(_p(x), _p(w), _p(out), N, H, W, C, Co, kH, kW,
-                              pad[0], pad[1], stride[0], stride[1], dil[0], dil[1])
+    args = (N, H, W, C, Co, kH, kW, pad[0], pad[1], stride[0], stride[1], dil[0], dil[1])
+    if threads > 1:
+        lib().orc_conv2d_nhwc_s32_mt(_p(x), _p(w), _p(out), *args, threads)
+    else:
+        lib().orc_conv2d_nhwc_s32(_p(x), _p(w), _p(out), *args)
     return out
 
 

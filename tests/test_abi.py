@@ -165,3 +165,16 @@ def test_nn_modules_match_reference_state_dict_layout():
     import pytest
     with pytest.raises(ValueError):
         SparseLinear(100, 96)
+
+
+def test_cpp_caller_links_and_reports_errors(lib):
+    """The test suite's C++ caller of include/forge/**.h (tests/cpp) loads against the library
+    (every forge:: symbol it uses resolves) and sees forge::last_error() = FORGE_EINVAL for a
+    call with null operands, which the C ABI rejects before any device work."""
+    from forge_amd import _lib
+    path = os.path.join(ROOT, "tests", "cpp", "lib", "libforge_caller.so")
+    if not os.path.exists(path):
+        pytest.skip("tests/cpp caller not built (python tests/cpp/build.py)")
+    caller = ctypes.CDLL(path)
+    caller.caller_last_error_after_bad_call.restype = ctypes.c_int
+    assert caller.caller_last_error_after_bad_call() == _lib.FORGE_EINVAL

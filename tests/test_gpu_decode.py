@@ -6,7 +6,7 @@ Bar: INT32 bit-exact; FP16 bit-exact to the oracle's epilogue. Shapes exercise t
 K split over 8 wavefronts (K = 128: one wave works; K = 1152: 9 stages, uneven slices and
 idle waves), ragged N (not a multiple of the 32-row workgroup tile), M from 1 to 16 (the
 sparse register kernel for M <= 8 with K % 256 == 0, the DMA-ring kernel otherwise), and
-configs[3] at full size (M = 16 and 1, N = K = 8192; sampled output columns); narrow N with K
+configs[3] at full size (M = 16, 4 and 1, N = K = 8192; every output column); narrow N with K
 split across workgroups (exact INT32 hand-off), repeated and on two streams at once."""
 import numpy as np
 import pytest
@@ -71,38 +71,59 @@ def test_decode_sparse(dev, orc, M, K, N):
         assert np.array_equal(to_host(Y).view(np.uint16), orc.dequant_epilogue(acc, act, ws, b).view(np.uint16))
 
 
-@pytest.mark.parametrize("M", [16, 1])
-def test_config4_full_size_sampled(dev, orc, M):
-    """M = 16 and 1 tokens, N = K = 8192, dense and 2:4, FP16 tokens quantized per
-    token, dequant + bias; sampled output columns against the oracle."""
+@pytest.mark.parametrize("M", [16, 4, 1])
+def test_config4_full_size(dev, orc, M):
+    """M = 1, 4 and 16 tokens, N = K = 8192, dense and 2:4, FP16 tokens quantized
+    per token, dequant + bias. Every output column against the oracle, through the whole
+    int8_linear / sparse_int8_linear and through the GEMM alone on the quantized tokens
+    (int8_gemm_dequant / sparse_int8_gemm), with poisoned outputs."""
     import torch
     from forge_amd import ops
     rng = np.random.default_rng(4 + M)
     K, N = 8192, 8192
+    T = orc.cpu_threads()
     W = int8_uniform(rng, (N, K))
     x = fp16_normal(rng, (M, K))
     ws = rng.uniform(1e-3, 1e-2, N).astype(np.float16)
     b = fp16_normal(rng, (N,), 0.1)
-    cols = np.array([0, 1, 31, 32, 4095, 4096, 8160, 8191])
     q, s = orc.quantize_rows(x)
-    ref_d = orc.dequant_epilogue(orc.gemm_s32(q, W[cols]), s, ws[cols], b[cols]).view(np.uint16)
+    ref_d = orc.gemm_dequant(q, W, s, ws, b, threads=T).view(np.uint16)
     cr, mr = orc.prune_compress_24(W)
     Wp = orc.decompress_24(cr, mr, N, K)
-    ref_s = orc.dequant_epilogue(orc.gemm_s32(q, Wp[cols]), s, ws[cols], b[cols]).view(np.uint16)
+    ref_s = orc.gemm_dequant(q, Wp, s, ws, b, threads=T).view(np.uint16)
     xd, Wd, wsd, bd = to_dev(x, dev), to_dev(W, dev), to_dev(ws, dev), to_dev(b, dev)
     sq = torch.empty((M, K), dtype=torch.int8, device=dev)
     ss = torch.empty((M,), dtype=torch.float32, device=dev)
-    say(f"config4 dense {M}x8192x8192")
-    yd = to_host(ops.int8_linear(xd, Wd, wsd, bd, sq, ss)).view(np.uint16)
-    assert np.array_equal(yd[:, cols], ref_d)
+    y = torch.empty((M, N), dtype=torch.float16, device=dev)
+
+    def check(what, ref):
+        got = to_host(y).view(np.uint16)
+        bad = int((got != ref).sum())
+        assert bad == 0, f"{what}: {bad} of {got.size} outputs differ"
+
+    say(f"config4 dense int8_linear {M}x8192x8192")
+    poison(y, 0x7B)
+    ops.int8_linear(xd, Wd, wsd, bd, sq, ss, out=y)
+    check("int8_linear", ref_d)
+    assert np.array_equal(to_host(sq), q) and np.array_equal(to_host(ss), s)
+    say(f"config4 dense gemm {M}x8192x8192")
+    poison(y, 0x7B)
+    ops.int8_gemm_dequant(sq, Wd, ss, wsd, bd, out=y)
+    check("int8_gemm_dequant", ref_d)
     comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
     raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
     meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
     ops.prune_compress_24(Wd, comp, raw, N, K)
     ops.pack_metadata(raw, meta, N, K)
-    say(f"config4 sparse {M}x8192x8192")
-    ys = to_host(ops.sparse_int8_linear(xd, comp, meta, wsd, bd, sq, ss)).view(np.uint16)
-    assert np.array_equal(ys[:, cols], ref_s)
+    say(f"config4 sparse sparse_int8_linear {M}x8192x8192")
+    poison(y, 0x7B)
+    ops.sparse_int8_linear(xd, comp, meta, wsd, bd, sq, ss, out=y)
+    check("sparse_int8_linear", ref_s)
+    ops.fused_quantize_activation(xd, M, K, out=sq, scales=ss)
+    say(f"config4 sparse gemm {M}x8192x8192")
+    poison(y, 0x7B)
+    ops.sparse_int8_gemm(comp, sq, meta, ss, wsd, bd, out=y)
+    check("sparse_int8_gemm", ref_s)
 
 
 # 16 < M <= 64: two (M <= 32) or four token blocks, partial last block; K covering every padded

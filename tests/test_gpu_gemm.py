@@ -86,9 +86,9 @@ def test_int8_linear(dev, orc, M, K, N):
     assert np.array_equal(to_host(Y).view(np.uint16), ref.view(np.uint16))
 
 
-def test_config2_full_size_sampled(dev, orc):
-    """W8A8 linear 4096^3, outlier channels; all quantized activations and
-    sampled output rows compared bit-exactly; repeat run bit-identical."""
+def test_config2_full_size(dev, orc):
+    """W8A8 linear 4096^3, outlier channels; every quantized activation, scale and
+    FP16 output compared bit-exactly with the oracle (threaded loop); repeat run bit-identical."""
     import torch
     from forge_amd import ops
     rng = np.random.default_rng(2)
@@ -99,34 +99,32 @@ def test_config2_full_size_sampled(dev, orc):
     W = int8_uniform(rng, (N, K))
     ws = rng.uniform(1e-3, 1e-2, N).astype(np.float32).astype(np.float16)
     b = (rng.standard_normal(N) * 0.1).astype(np.float16)
-    qr, sr = orc.quantize_rows(x)
-    rows = np.array([0, 1, 255, 256, 1000, 2047, 2048, 3071, 4094, 4095])
-    ref = orc.gemm_dequant(qr[rows], W, sr[rows], ws, b)
+    ref, qr, sr = orc.linear(x, W, ws, b, threads=orc.cpu_threads())
     say("config2 4096^3 linear")
     sq = torch.empty((M, K), dtype=torch.int8, device=dev)
     ss = torch.empty((M,), dtype=torch.float32, device=dev)
     xd, Wd, wsd, bd = to_dev(x, dev), to_dev(W, dev), to_dev(ws, dev), to_dev(b, dev)
-    Y1 = to_host(ops.int8_linear(xd, Wd, wsd, bd, sq, ss))
+    out = torch.empty((M, N), dtype=torch.float16, device=dev)
+    poison(out, 0x7B)
+    Y1 = to_host(ops.int8_linear(xd, Wd, wsd, bd, sq, ss, out=out))
     assert np.array_equal(to_host(sq), qr) and np.array_equal(to_host(ss), sr)
-    assert np.array_equal(Y1[rows].view(np.uint16), ref.view(np.uint16))
+    bad = int((Y1.view(np.uint16) != ref.view(np.uint16)).sum())
+    assert bad == 0, f"{bad} of {Y1.size} outputs differ"
     Y2 = to_host(ops.int8_linear(xd, Wd, wsd, bd, sq, ss))
     assert np.array_equal(Y1.view(np.uint16), Y2.view(np.uint16))
-    assert np.isfinite(Y1.astype(np.float32)).all()
 
 
-def test_4096_cube_int32_sampled(dev, orc):
+def test_4096_cube_int32(dev, orc):
+    """4096^3 INT32 (the headline GEMM shape without the epilogue): every output bit-exact."""
     from forge_amd import ops
     rng = np.random.default_rng(4096)
     A = int8_uniform(rng, (4096, 4096))
     B = int8_uniform(rng, (4096, 4096))
-    rows = np.array([0, 31, 32, 255, 256, 2049, 4095])
-    ref = orc.gemm_s32(A[rows], B)
+    ref = orc.gemm_s32(A, B, threads=orc.cpu_threads())
     say("gemm s32 4096^3")
     C = to_host(ops.int8_gemm_s32(to_dev(A, dev), to_dev(B, dev)))
-    assert np.array_equal(C[rows], ref)
-    # column checksum identity: sum_m C[m, :] == (sum_m A[m, :]) . B^T  (exact in int64)
-    colsum = C.astype(np.int64).sum(axis=0)
-    assert np.array_equal(colsum, A.astype(np.int64).sum(axis=0) @ B.astype(np.int64).T)
+    bad = int((C != ref).sum())
+    assert bad == 0, f"{bad} of {C.size} outputs differ"
 
 
 @pytest.mark.parametrize("N", [256, 200])

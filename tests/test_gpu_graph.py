@@ -48,7 +48,7 @@ def _replay_check(dev, calls, outputs, replays=4):
 
 def test_graph_int8_linear(dev):
     """configs[1]-style fused linear (quantize + dequantizing GEMM), plus decode shapes; (16, 4096,
-    1024) and (40, 8192, 512) split K across workgroups (the sum slots of the capture stream)."""
+    1024) and (40, 8192, 512) split K across workgroups (on the capture's own sum slot)."""
     import torch
     from forge_amd import ops
     rng = np.random.default_rng(21)
@@ -65,6 +65,69 @@ def test_graph_int8_linear(dev):
         calls = [lambda: ops.int8_linear(x, w, ws, b, q, s, out=y),
                  lambda: ops.int8_gemm_s32(q, w, out=c32)]
         _replay_check(dev, calls, [q, s, y, c32])
+
+
+def test_graph_ksplit_slot_keys(dev):
+    """Decode K split inside graphs: a capture records split launches on a slot of its own,
+    distinct from the eager slot of the capture stream and from another capture's slot; replays
+    interleaved with eager split work on the capture stream (its own slot) all give the eager
+    bits; forge_ksplit_reset leaves the slots usable."""
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(26)
+    M, K, N = 16, 4096, 1024
+    x = to_dev(fp16_normal(rng, (M, K)), dev)
+    w = to_dev(int8_uniform(rng, (N, K)), dev)
+    x2 = to_dev(fp16_normal(rng, (M, K)), dev)
+    w2 = to_dev(int8_uniform(rng, (N, K)), dev)
+    ws = to_dev(rng.uniform(1e-3, 1e-2, N).astype(np.float16), dev)
+    b = to_dev(fp16_normal(rng, (N,), 0.1), dev)
+    q, q2 = (torch.empty((M, K), dtype=torch.int8, device=dev) for _ in range(2))
+    s, s2 = (torch.empty((M,), dtype=torch.float32, device=dev) for _ in range(2))
+    y, y2, y3 = (torch.empty((M, N), dtype=torch.float16, device=dev) for _ in range(3))
+    say("graph ksplit slots: eager")
+    ops.int8_linear(x, w, ws, b, q, s, out=y)
+    slot_e, kp_e = ops.ksplit_last()
+    assert slot_e >= 0 and kp_e > 1, (slot_e, kp_e)
+    ops.int8_linear(x2, w2, ws, b, q2, s2, out=y2)
+    torch.cuda.synchronize()
+    ref, ref2 = y.clone(), y2.clone()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        ops.int8_linear(x2, w2, ws, b, q2, s2, out=y2)
+        slot_ce, _ = ops.ksplit_last()
+    torch.cuda.current_stream().wait_stream(cap)
+    torch.cuda.synchronize()
+    assert slot_ce >= 0 and slot_ce != slot_e
+    say("graph ksplit slots: capture")
+    g1, g2 = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1, stream=cap):
+        ops.int8_linear(x, w, ws, b, q, s, out=y)
+        slot_g1, kp_g1 = ops.ksplit_last()
+    with torch.cuda.graph(g2, stream=cap):
+        ops.int8_linear(x, w, ws, b, q, s, out=y3)
+        slot_g2, kp_g2 = ops.ksplit_last()
+    assert kp_g1 > 1 and kp_g2 > 1, (kp_g1, kp_g2)
+    assert len({slot_e, slot_ce, slot_g1, slot_g2}) == 4 and min(slot_g1, slot_g2) >= 0
+    for r in range(4):
+        if r == 2:
+            ops.ksplit_reset()
+        y.view(torch.uint8).fill_(0x5A)
+        y2.view(torch.uint8).fill_(0x5A)
+        y3.view(torch.uint8).fill_(0x5A)
+        torch.cuda.synchronize()
+        say(f"graph ksplit slots: replay {r}")
+        g1.replay()
+        cap.wait_stream(torch.cuda.current_stream()) if r == 3 else None
+        with torch.cuda.stream(cap):
+            for _ in range(3):
+                ops.int8_linear(x2, w2, ws, b, q2, s2, out=y2)
+        g2.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.uint8), ref.view(torch.uint8)), f"replay {r}: graph 1 differs"
+        assert torch.equal(y3.view(torch.uint8), ref.view(torch.uint8)), f"replay {r}: graph 2 differs"
+        assert torch.equal(y2.view(torch.uint8), ref2.view(torch.uint8)), f"replay {r}: eager work differs"
 
 
 def test_graph_sparse_splitk(dev):

@@ -108,3 +108,32 @@ def test_w_meta_conversion(dev, orc, N, K):
     assert np.array_equal(to_host(got).view(np.uint32), gfx_words)
     back = w_meta_to_reference(to_dev(gfx_words.view(np.int32), dev))
     assert np.array_equal(to_host(back).view(np.uint32), ref_words)
+
+
+@pytest.mark.parametrize("M,K,N", [(9, 512, 64), (300, 1280, 320)])
+def test_sparse_linear_loads_reference_state_dict(dev, orc, M, K, N):
+    """A state_dict laid out as the reference's SparseLinear saves it (w_meta in its row-major
+    word order, module version 1) loads into a module on the device and computes the oracle's
+    outputs for those weights."""
+    import collections
+    import torch
+    from forge_amd.nn import SparseLinear
+    rng = np.random.default_rng(M + 2 * K + N)
+    q = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    comp, raw = orc.prune_compress_24(q)
+    ws = rng.uniform(1e-3, 1e-2, N).astype(np.float16)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float16)
+    sd = collections.OrderedDict()
+    sd["W_comp"] = torch.from_numpy(comp)
+    sd["w_meta"] = torch.from_numpy(orc.pack_metadata_ref(raw, N, K).view(np.int32).copy())
+    sd["w_scale"] = torch.from_numpy(ws)
+    sd["bias"] = torch.from_numpy(b)
+    sd._metadata = collections.OrderedDict({"": {"version": 1}})
+    x = fp16_normal(rng, (M, K))
+    say(f"SparseLinear reference state_dict M={M} K={K} N={N}")
+    m = SparseLinear(K, N).to(dev)
+    m.load_state_dict(sd)
+    y = to_host(m(to_dev(x, dev)))
+    qx, sx = orc.quantize_rows(x)
+    ref = orc.dequant_epilogue(orc.sparse_gemm_s32(comp, qx, raw, N, K), sx, ws, b)
+    assert np.array_equal(y.view(np.uint16), ref.view(np.uint16))

@@ -508,3 +508,44 @@ def test_sparse_weight_prep_is_the_composition(orc):
     kept = d != 0
     assert np.all(kept.sum(axis=2) <= 2)
     assert np.array_equal(d[kept], qg[kept])
+
+
+@pytest.mark.parametrize("threads", [2, 3, 7])
+def test_threaded_forms_equal_single_thread(orc, threads):
+    """The threaded loops used for whole-output comparisons at full size give the single-threaded
+    functions' bits, also where the rows do not divide evenly among the threads."""
+    rng = np.random.default_rng(threads)
+    M, K, N = 37, 96, 53
+    A = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    B = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    assert np.array_equal(orc.gemm_s32(A, B, threads=threads), orc.gemm_s32(A, B))
+    act = rng.uniform(1e-3, 5e-2, M).astype(np.float32)
+    ws = rng.uniform(1e-3, 5e-2, N).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
+    for bias in (b, None):
+        assert np.array_equal(orc.gemm_dequant(A, B, act, ws, bias, threads=threads).view(np.uint16),
+                              orc.gemm_dequant(A, B, act, ws, bias).view(np.uint16))
+    Wd = rng.integers(-127, 128, (48, 128)).astype(np.int8)
+    comp, raw = orc.prune_compress_24(Wd)
+    x = rng.integers(-127, 128, (29, 128)).astype(np.int8)
+    assert np.array_equal(orc.sparse_gemm_s32(comp, x, raw, 48, 128, threads=threads),
+                          orc.sparse_gemm_s32(comp, x, raw, 48, 128))
+    xc = rng.integers(-127, 128, (3, 9, 7, 16)).astype(np.int8)
+    wc = rng.integers(-127, 128, (5, 3, 2, 16)).astype(np.int8)
+    for pad, stride, dil in (((1, 1), (1, 1), (1, 1)), ((0, 1), (2, 1), (1, 2))):
+        assert np.array_equal(orc.conv2d_nhwc_s32(xc, wc, pad, stride, dil, threads=threads),
+                              orc.conv2d_nhwc_s32(xc, wc, pad, stride, dil))
+
+
+def test_splitk_reduce_matches_numpy(orc):
+    """ws + bias in float32, then float16 RNE (numpy's conversion is IEEE RNE, pinned above);
+    without bias a plain conversion. Values near fp16 ties, overflow to inf and subnormals."""
+    rng = np.random.default_rng(8)
+    ws = (rng.standard_normal((23, 41)) * 50).astype(np.float32)
+    ws[0, :4] = [65520.0, -65520.0, 1e-6, 2049.0]
+    b = (rng.standard_normal(41) * 3).astype(np.float16)
+    got = orc.splitk_reduce(ws, b)
+    ref = (ws + b.astype(np.float32)[None, :]).astype(np.float16)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+    assert np.array_equal(orc.splitk_reduce(ws).view(np.uint16), ws.astype(np.float16).view(np.uint16))
+    assert np.isinf(got[0, 0]) or abs(float(ws[0, 0]) + float(b[0])) < 65520
