@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from conftest import golden
-from helpers import int8_uniform, say, to_dev, to_host
+from helpers import int8_uniform, poison, say, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
 
