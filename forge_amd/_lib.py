@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(HERE, "lib", "libforge_amd.so")
 FORGE_OK = 0
 FORGE_EINVAL = -1
 FORGE_ENODEV = -2
+FORGE_ERANGE = -3
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -34,6 +35,7 @@ SIGNATURES = {
     "forge_int8_gemm": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "forge_int8_linear": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P]),
     "forge_int8_gemm_s32": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "forge_int8_linear_noalloc": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "forge_prune_compress_24": (_I, [_P, _P, _P, _I, _I, _P]),
     "forge_pack_metadata": (_I, [_P, _P, _I, _I, _P]),
     "forge_unpack_metadata": (_I, [_P, _P, _I, _I, _P]),

@@ -42,6 +42,7 @@ SOURCES = [
     "conv.hip",
     "conv_transpose.hip",
     "conv_depthwise.hip",
+    "noalloc.hip",
     "forge_api.cpp",
 ]
 

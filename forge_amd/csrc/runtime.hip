@@ -70,6 +70,8 @@ extern "C" const char* forge_status_string(int status) {
     if (status == FORGE_OK) return "ok";
     if (status == FORGE_EINVAL) return "invalid argument (shape, alignment or null pointer)";
     if (status == FORGE_ENODEV) return "no HIP device";
+    if (status == FORGE_ERANGE)
+        return "size beyond the no-allocation limit (M * K <= 16 MiB of quantized activations, M <= 65536)";
     return hipGetErrorString(static_cast<hipError_t>(status));
 }
 
@@ -79,7 +81,8 @@ extern "C" int forge_init(void) {
     int st = FORGE_OK;
     device_info(&st);
     if (st != FORGE_OK) return st;
-    return ksplit_prepare();
+    if ((st = ksplit_prepare()) != FORGE_OK) return st;
+    return noalloc_prepare();
 }
 
 extern "C" int forge_get_compute_capability(int device, int* out_cc) {

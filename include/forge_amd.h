@@ -34,6 +34,7 @@ extern "C" {
 #define FORGE_OK      0
 #define FORGE_EINVAL  (-1)
 #define FORGE_ENODEV  (-2)
+#define FORGE_ERANGE  (-3)   /* size beyond a fixed limit of forge_int8_linear_noalloc */
 
 /* Sparse tile configurations (weight rows x tokens per workgroup tile).
  * Reference: include/forge/gemm/int8_sparse.cuh:26-31. */
@@ -127,6 +128,20 @@ int forge_int8_gemm(const int8_t* A, const int8_t* B, const float* act_scale,
 int forge_int8_linear(const uint16_t* x, const int8_t* w, const uint16_t* w_scale,
                       const uint16_t* bias, uint16_t* out, int M, int K, int N,
                       int8_t* scratch_q, float* scratch_scale, void* stream);
+
+/* No counterpart in the reference. forge_int8_linear for callers that cannot allocate
+ * device memory (code under graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): the same computation and bits, with the quantized activations and scales in
+ * a fixed per-GPU device array of the library instead of caller scratch. Limits: M * K <=
+ * FORGE_NOALLOC_MAX_QBYTES and M <= FORGE_NOALLOC_MAX_ROWS, else FORGE_ERANGE (nothing is
+ * launched). Allocates nothing. Every call on one GPU shares the array: calls that overlap
+ * in time on one GPU race and must not be made. The array's address is resolved by
+ * forge_init or by the first call on a device; a first call inside a graph capture returns
+ * FORGE_EINVAL (call forge_init before capturing). */
+#define FORGE_NOALLOC_MAX_QBYTES (16u << 20)
+#define FORGE_NOALLOC_MAX_ROWS   65536
+int forge_int8_linear_noalloc(const uint16_t* x, const int8_t* w, const uint16_t* w_scale,
+                              const uint16_t* bias, uint16_t* out, int M, int K, int N, void* stream);
 
 /* Extension (no reference counterpart: the reference GEMMs always dequantize):
  * C (M,N) int32 = A (M,K) x B (N,K)^T, exact INT32 accumulation. */

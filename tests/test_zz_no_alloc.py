@@ -1,0 +1,56 @@
+"""GPU: forge_int8_linear_noalloc (the no-allocation form of forge_int8_linear, whose quantized
+activations live in the library's per-GPU device array) against forge_int8_linear with caller
+scratch, through the C ABI: two calls in a row, the second with a smaller input, bit-identical
+outputs; sizes beyond the array's limits are rejected with FORGE_ERANGE before any launch."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from helpers import fp16_normal, int8_uniform, poison, say, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def _call_noalloc(lib, x, w, ws, b, out, M, K, N, stream):
+    return lib.forge_int8_linear_noalloc(x.data_ptr(), w.data_ptr(), ws.data_ptr(),
+                                         None if b is None else b.data_ptr(), out.data_ptr(), M, K, N, stream)
+
+
+def test_noalloc_matches_int8_linear(dev, orc):
+    import torch
+    from forge_amd import _lib, ops
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    rng = np.random.default_rng(77)
+    # the second call is smaller than the first (fewer rows, shorter K), so it reads only what
+    # it wrote itself; the third runs the decode path with the quantize fused into the GEMM
+    for M, K, N, bias in [(1024, 2048, 768, True), (37, 512, 264, False), (2, 8192, 512, True)]:
+        x = to_dev(fp16_normal(rng, (M, K)), dev)
+        w = to_dev(int8_uniform(rng, (N, K)), dev)
+        ws = to_dev(rng.uniform(1e-3, 1e-2, N).astype(np.float16), dev)
+        b = to_dev(fp16_normal(rng, (N,), 0.1), dev) if bias else None
+        q = torch.empty((M, K), dtype=torch.int8, device=dev)
+        s = torch.empty((M,), dtype=torch.float32, device=dev)
+        want = torch.empty((M, N), dtype=torch.float16, device=dev)
+        ops.int8_linear(x, w, ws, b, q, s, out=want)
+        got = torch.empty((M, N), dtype=torch.float16, device=dev)
+        poison(got, 0x7B)
+        say(f"int8_linear_noalloc M={M} K={K} N={N} bias={bias}")
+        assert _call_noalloc(lib, x, w, ws, b, got, M, K, N, stream) == _lib.FORGE_OK
+        assert np.array_equal(to_host(got).view(np.uint16), to_host(want).view(np.uint16))
+
+
+def test_noalloc_limits(dev):
+    import torch
+    from forge_amd import _lib
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    x = torch.empty((8,), dtype=torch.float16, device=dev)
+    w = torch.empty((8,), dtype=torch.int8, device=dev)
+    ws = torch.empty((8,), dtype=torch.float16, device=dev)
+    out = torch.empty((8,), dtype=torch.float16, device=dev)
+    # shapes only: nothing is launched for a rejected size, so the tiny buffers are never read
+    assert _call_noalloc(lib, x, w, ws, None, out, 4097, 4096, 16, stream) == _lib.FORGE_ERANGE
+    assert _call_noalloc(lib, x, w, ws, None, out, 65537, 16, 16, stream) == _lib.FORGE_ERANGE
+    assert lib.forge_int8_linear_noalloc(None, None, None, None, None, 4, 64, 16, stream) == _lib.FORGE_EINVAL
