@@ -1,7 +1,8 @@
 """Benchmark of the INT8 quantized-inference path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
-    python bench.py --traffic-probe     (kernels for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)
+    python bench.py --traffic-probe     (the dominant kernels, for rocprofv3 --pmc counter runs)
+    python bench.py --counter-summary DIR   (rocprofv3 CSVs -> profiles/kernel_counters.{json,md})
 
 Headline (`value`): configs[1] of BASELINE.json -- the fused W8A8 linear at M=N=K=4096
 (FP16 activations with 8 outlier channels x20, per-token quantize, INT8 MFMA GEMM with
@@ -13,9 +14,11 @@ algorithmic ops 2*M*N*K per launch against MI355X's dense INT8 peak (5.0 POP/s).
 cpu_baseline: the oracle's INT32 loop + dequant epilogue (oracle/) over the whole configs[1]
 workload, split over output rows on up to 16 threads (the box's CPU share per GPU), timed on
 this host; the single-threaded rate is in its sample text.
-roofline.traffic: HBM bytes per launch of the GEMM, read from TRAFFIC_FILE, which records two
-rocprofv3 --pmc runs of `bench.py --traffic-probe` (FETCH_SIZE, then WRITE_SIZE) scaled by
-what the same counters read for a device copy of known size in the same runs.
+roofline.traffic / roofline.mfma_busy: HBM bytes per launch of the GEMM and its matrix-core
+busy fraction, read from COUNTERS_FILE (profiles/kernel_counters.json), which `--counter-summary`
+writes from rocprofv3 --pmc runs of `bench.py --traffic-probe` (FETCH_SIZE and WRITE_SIZE scaled
+by what the same counters read for a device copy of known size in the same runs; MFMA busy
+cycles; see profiles/kernel_counters.md).
 extra: configs[2] (2:4 sparse vs dense at 4096x11008x4096), configs[3] (decode
 M = 1/4/16, N = K = 8192, dense and 2:4, HBM GB/s with 8 dense / 10 sparse rotating weight
 copies so the 256 MB MALL cannot hold them; calls captured into a HIP graph and replayed so host launch
@@ -45,41 +48,58 @@ sys.path.insert(0, ROOT)
 METRIC = "INT8 dense/2:4-sparse GEMM TOPS @4096^3 (% MFMA peak); M=16 HBM GB/s"
 PEAK_INT8_TOPS = 5000.0      # MI355X dense INT8 MFMA, 5.0 POP/s
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "int8_linear_c2_gemm_traffic.json")
 COPY_PROBE_BYTES = 256 << 20  # calibration copy for the traffic counters
+PROBE_REPS = 5
+
+
+COUNTERS_FILE = os.path.join(ROOT, "profiles", "kernel_counters.json")
+
+
+def _c2_counters():
+    try:
+        with open(COUNTERS_FILE) as f:
+            return json.load(f)["kernels"]["c2_gemm"]
+    except (OSError, ValueError, KeyError, TypeError):
+        return {}
 
 
 def measured_traffic():
-    """HBM bytes per GEMM launch from the committed counter runs, or None."""
-    try:
-        with open(TRAFFIC_FILE) as f:
-            return int(json.load(f)["gemm_bytes_per_launch"])
-    except (OSError, ValueError, KeyError):
-        return None
-
-
-COUNTERS_FILE = os.path.join(ROOT, "profiles", "int8_linear_c2_gemm_counters.json")
+    """HBM-side bytes per launch of the configs[1] GEMM from the committed counter runs
+    (FETCH_SIZE and WRITE_SIZE, scaled by the counters' reading for a device copy of known
+    size), or None."""
+    v = _c2_counters().get("traffic_bytes")
+    return int(v) if v else None
 
 
 def measured_mfma_busy():
-    """MFMA-busy fraction of the configs[1] GEMM from the committed counter run
-    (SQ_VALU_MFMA_BUSY_CYCLES over SQ_BUSY_CYCLES x 4 SIMDs ... see the file), or None."""
-    try:
-        with open(COUNTERS_FILE) as f:
-            return float(json.load(f)["gemm"]["mfma_busy"])
-    except (OSError, ValueError, KeyError, TypeError):
-        return None
+    """Matrix-core busy fraction of the configs[1] GEMM from the committed counter run
+    (SQ_VALU_MFMA_BUSY_CYCLES over 4 x SQ_BUSY_CU_CYCLES), or None."""
+    v = _c2_counters().get("mfma_busy")
+    return round(float(v), 4) if v is not None else None
 
 
 def traffic_probe() -> int:
-    """Launches for the two counter runs: the configs[1] dequant GEMM 5 times on the quantized
-    activations, then a COPY_PROBE_BYTES device-to-device copy 5 times (its FETCH_SIZE and
-    WRITE_SIZE give the counters' scale: COPY_PROBE_BYTES each, by construction)."""
+    """Launches for the counter runs (rocprofv3 --pmc, one counter set per run), each kernel
+    PROBE_REPS times on its configs' shape with inputs resident on the device:
+    c2 = the configs[1] dequant GEMM (4096^3, FP16 out); c3 sparse / dense = configs[2]
+    (4096 x 11008 x 4096, INT32 out) on the 2:4 and the dense engine; c5 = configs[4] NHWC
+    conv (INT32 out; a 256-row and a 192-row tail launch); c4 = configs[3] M = 16 decode GEMMs
+    (N = K = 8192, pre-quantized tokens, FP16 out) dense and 2:4; then a COPY_PROBE_BYTES
+    device-to-device copy, the calibration of known size for FETCH_SIZE / WRITE_SIZE."""
     import torch
     import forge_amd
     from forge_amd import ops
     forge_amd.load()
     dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+
+    def reps(tag, fn):
+        for _ in range(PROBE_REPS):
+            fn()
+        torch.cuda.synchronize()
+        print(f"probe {tag} done", flush=True)
+
     x, W, ws, b = make_c2(dev)
     M, K = x.shape
     N = W.shape[0]
@@ -87,16 +107,243 @@ def traffic_probe() -> int:
     ss = torch.empty((M,), dtype=torch.float32, device=dev)
     y = torch.empty((M, N), dtype=torch.float16, device=dev)
     ops.fused_quantize_activation(x, M, K, out=sq, scales=ss)
-    for _ in range(5):
-        ops.int8_gemm_dequant(sq, W, ss, ws, b, out=y)
+    reps("c2_gemm", lambda: ops.int8_gemm_dequant(sq, W, ss, ws, b, out=y))
+    del x, W, y
+
+    M, K, N = 4096, 4096, 11008
+    W = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+    comp, meta = _prep_sparse(ops, W)
+    C = torch.empty((M, N), dtype=torch.int32, device=dev)
+    reps("c3_sparse", lambda: ops.sparse_int8_gemm_s32(comp, sq, meta, out=C))
+    reps("c3_dense", lambda: ops.int8_gemm_s32(sq, W, out=C))
+    del W, comp, meta, C
+
+    xc = torch.randint(-127, 128, (32, 56, 56, 256), generator=g, device=dev, dtype=torch.int8)
+    wc = torch.randint(-127, 128, (256, 3, 3, 256), generator=g, device=dev, dtype=torch.int8)
+    o32 = torch.empty((32, 56, 56, 256), dtype=torch.int32, device=dev)
+    reps("c5_conv", lambda: ops.int8_conv2d_nhwc_s32(xc, wc, pad=(1, 1), out=o32))
+    del xc, wc, o32
+
+    M, N, K = 16, 8192, 8192
+    W = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+    comp, meta = _prep_sparse(ops, W)
+    xh = torch.randn((M, K), generator=g, device=dev).half()
+    q16 = torch.empty((M, K), dtype=torch.int8, device=dev)
+    s16 = torch.empty((M,), dtype=torch.float32, device=dev)
+    ops.fused_quantize_activation(xh, M, K, out=q16, scales=s16)
+    ws8 = (torch.rand((N,), generator=g, device=dev) * 9e-3 + 1e-3).half()
+    b8 = (torch.randn((N,), generator=g, device=dev) * 0.1).half()
+    y16 = torch.empty((M, N), dtype=torch.float16, device=dev)
+    reps("c4_dense_M16", lambda: ops.int8_gemm_dequant(q16, W, s16, ws8, b8, out=y16))
+    reps("c4_sparse_M16", lambda: ops.sparse_int8_gemm(comp, q16, meta, s16, ws8, b8, out=y16))
+    del W, comp, meta
+
     src = torch.empty((COPY_PROBE_BYTES,), dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     src.fill_(1)
-    for _ in range(5):
-        dst.copy_(src)
-    torch.cuda.synchronize()
+    reps("copy", lambda: dst.copy_(src))
     print("traffic probe done", flush=True)
     return 0
+
+
+def _prep_sparse(ops, W):
+    import torch
+    N, K = W.shape
+    comp = torch.empty((N, K // 2), dtype=torch.int8, device=W.device)
+    raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=W.device)
+    meta = torch.empty((N * K // 32,), dtype=torch.int32, device=W.device)
+    ops.prune_compress_24(W, comp, raw, N, K)
+    ops.pack_metadata(raw, meta, N, K)
+    return comp, meta
+
+
+# ---- counter summary (rocprofv3 --pmc runs of --traffic-probe) ---------------------------
+
+PROBE_KERNELS = {
+    # probe: (kernel-name substrings, any of which marks a dispatch of the probe)
+    "c2_gemm": ("gemm_dma_kernel<256, 256, true, forge_amd::DmaRowMajor>",),
+    "c3_sparse": ("sparse_dma32_kernel<false>",),
+    "c3_dense": ("gemm_dma_kernel<256, 256, false, forge_amd::DmaRowMajor>",),
+    "c5_conv": ("gemm_dma_kernel<256, 256, false, forge_amd::DmaConv>",
+                "gemm_dma_kernel<192, 256, false, forge_amd::DmaConv>"),
+    "c4_dense_M16": ("decode_dense_kernel<true",),
+    "c4_sparse_M16": ("decode_sparse_kernel<true",),
+    "copy": ("copyBuffer",),
+}
+_C4_TOK = 16 * 8192
+PROBE_WORK = {
+    # probe: (algorithmic ops per call, algorithmic bytes per call, MFMA peak TOPS)
+    "c2_gemm": (2.0 * 4096 ** 3, 4 * 4096 * 4096 + 4096 * 4 + 4096 * 4, 5000.0),
+    "c3_sparse": (2.0 * 4096 * 11008 * 4096, 4096 * 4096 + 11008 * 4096 // 2 + 11008 * 4096 // 8 + 4096 * 11008 * 4,
+                  10000.0),
+    "c3_dense": (2.0 * 4096 * 11008 * 4096, 4096 * 4096 + 11008 * 4096 + 4096 * 11008 * 4, 5000.0),
+    "c5_conv": (2.0 * 100352 * 256 * 2304, 32 * 56 * 56 * 256 + 256 * 2304 + 100352 * 256 * 4, 5000.0),
+    "c4_dense_M16": (2.0 * 16 * 8192 * 8192, 8192 * 8192 + _C4_TOK + 16 * 8192 * 2 + 8192 * 4 + 16 * 4, 5000.0),
+    "c4_sparse_M16": (2.0 * 16 * 8192 * 8192, 8192 * 8192 // 2 + 8192 * 8192 // 8 + _C4_TOK + 16 * 8192 * 2
+                      + 8192 * 4 + 16 * 4, 10000.0),
+}
+SIMDS = 256 * 4          # MI355X: 256 CUs x 4 SIMDs
+XCDS = 8
+
+
+def counter_summary(outdir: str) -> int:
+    """Reads the rocprofv3 --pmc CSVs of --traffic-probe runs under outdir (one subdirectory per
+    counter set) and writes profiles/kernel_counters.json: per probe, medians over its dispatches
+    (a probe with two kernels per call, the conv, sums them per call)."""
+    import csv
+    import glob
+    import statistics
+    rows = {}   # probe -> counter -> list of per-call values
+    durs = {}
+    gui_floor = []   # smallest GRBM_GUI_ACTIVE per XCD in each run: the dispatch overhead
+    for path in sorted(glob.glob(os.path.join(outdir, "*", "*counter_collection.csv"))):
+        per_dispatch = {}
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] == "GRBM_GUI_ACTIVE" and float(r["Counter_Value"]) > 0:
+                    v = float(r["Counter_Value"]) / XCDS
+                    if len(gui_floor) <= len(durs.get("_runs", [])):
+                        gui_floor.append(v)
+                    gui_floor[-1] = min(gui_floor[-1], v)
+                probe = next((p for p, subs in PROBE_KERNELS.items() if any(x in r["Kernel_Name"] for x in subs)),
+                             None)
+                if probe is None:
+                    continue
+                if probe == "copy" and int(r["Grid_Size"]) < (1 << 16):
+                    continue
+                d = per_dispatch.setdefault(int(r["Dispatch_Id"]), {"probe": probe, "c": {}})
+                d["c"][r["Counter_Name"]] = float(r["Counter_Value"])
+                d["t"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3
+        # consecutive dispatches of a two-kernel probe form one call
+        calls = []
+        for did in sorted(per_dispatch):
+            d = per_dispatch[did]
+            if calls and calls[-1]["probe"] == d["probe"] == "c5_conv" and calls[-1]["n"] == 1:
+                for k, v in d["c"].items():
+                    calls[-1]["c"][k] = calls[-1]["c"].get(k, 0.0) + v
+                calls[-1]["t"] += d["t"]
+                calls[-1]["n"] = 2
+            else:
+                calls.append({"probe": d["probe"], "c": dict(d["c"]), "t": d["t"], "n": 1})
+        for c in calls:
+            for k, v in c["c"].items():
+                rows.setdefault(c["probe"], {}).setdefault(k, []).append(v)
+            durs.setdefault(c["probe"], []).append(c["t"])
+        durs.setdefault("_runs", []).append(path)
+    overhead = statistics.median(gui_floor) if gui_floor else 0.0
+    med = {p: {k: statistics.median(v) for k, v in cs.items()} for p, cs in rows.items()}
+    copy = med.get("copy", {})
+    fetch_scale = COPY_PROBE_BYTES / (copy["FETCH_SIZE"] * 1024) if copy.get("FETCH_SIZE") else None
+    write_scale = COPY_PROBE_BYTES / (copy["WRITE_SIZE"] * 1024) if copy.get("WRITE_SIZE") else None
+    out = {"calibration": {"copy_bytes": COPY_PROBE_BYTES, "copy_fetch_kib": copy.get("FETCH_SIZE"),
+                           "copy_write_kib": copy.get("WRITE_SIZE"), "fetch_scale": fetch_scale,
+                           "write_scale": write_scale, "gui_overhead_cycles_per_xcd": overhead}, "kernels": {}}
+    for p, (ops_, alg_bytes, peak) in PROBE_WORK.items():
+        c = med.get(p)
+        if not c:
+            continue
+        e = {"raw": c, "algorithmic_ops": ops_, "algorithmic_bytes": alg_bytes,
+             "duration_us_in_counter_run": statistics.median(durs[p])}
+        gui = c.get("GRBM_GUI_ACTIVE")
+        if gui:
+            # GRBM_GUI_ACTIVE is summed over the 8 XCDs and also counts a fixed per-dispatch
+            # overhead (its smallest reading in the run, a 256-thread fill kernel's), taken off
+            # once per kernel of the call.
+            n_k = 2 if p == "c5_conv" else 1
+            e["clock_ghz"] = (gui / XCDS - n_k * overhead) / (e["duration_us_in_counter_run"] * 1e3)
+            e["peak_tops_at_clock"] = peak * e["clock_ghz"] / 2.4
+        busy, cu_busy = c.get("SQ_VALU_MFMA_BUSY_CYCLES"), c.get("SQ_BUSY_CU_CYCLES")
+        if busy is not None and cu_busy:
+            # matrix-core busy SIMD-cycles over the SIMD-cycles of CUs with waves resident
+            e["mfma_busy"] = busy / (4 * cu_busy)
+            e["cu_busy_cycles_per_cu"] = cu_busy / (SIMDS // 4)
+        if busy is not None and gui:
+            e["mfma_busy_at_clock"] = busy / (SIMDS * e["clock_ghz"] * e["duration_us_in_counter_run"] * 1e3)
+        mops = c.get("SQ_INSTS_VALU_MFMA_MOPS_I8")
+        if mops is not None:
+            e["mfma_ops_counted"] = mops * 512
+        if c.get("TCP_TCC_READ_REQ_sum"):
+            e["l2_read_latency_cycles"] = c["TCP_TCC_READ_REQ_LATENCY_sum"] / c["TCP_TCC_READ_REQ_sum"]
+            e["l2_read_requests"] = c["TCP_TCC_READ_REQ_sum"]
+        if c.get("TA_TA_BUSY_sum") and gui:
+            e["ta_busy"] = c["TA_TA_BUSY_sum"] / (SIMDS // 4) / (e["clock_ghz"] * e["duration_us_in_counter_run"] * 1e3)
+        if c.get("SQ_LDS_IDX_ACTIVE"):
+            e["lds_bank_conflict_per_active"] = c.get("SQ_LDS_BANK_CONFLICT", 0.0) / c["SQ_LDS_IDX_ACTIVE"]
+        if "FETCH_SIZE" in c and fetch_scale:
+            e["read_bytes"] = c["FETCH_SIZE"] * 1024 * fetch_scale
+        if "WRITE_SIZE" in c and write_scale:
+            e["write_bytes"] = c["WRITE_SIZE"] * 1024 * write_scale
+        if "read_bytes" in e and "write_bytes" in e:
+            e["traffic_bytes"] = e["read_bytes"] + e["write_bytes"]
+            e["traffic_over_algorithmic"] = e["traffic_bytes"] / alg_bytes
+        if c.get("TCC_HIT_sum") is not None and c.get("TCC_MISS_sum") is not None:
+            tot = c["TCC_HIT_sum"] + c["TCC_MISS_sum"]
+            e["l2_hit_rate"] = c["TCC_HIT_sum"] / tot if tot else None
+        out["kernels"][p] = e
+    path = os.path.join(ROOT, "profiles", "kernel_counters.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1, sort_keys=True)
+    with open(os.path.join(ROOT, "profiles", "kernel_counters.md"), "w") as f:
+        f.write(_counter_markdown(out))
+    print(path)
+    return 0
+
+
+COUNTER_SETS = [
+    ("sq", "SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_WAVE_CYCLES SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE "
+           "SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_BUSY_CU_CYCLES GRBM_GUI_ACTIVE"),
+    ("fetch", "FETCH_SIZE GRBM_GUI_ACTIVE"),
+    ("write", "WRITE_SIZE TCC_HIT_sum TCC_MISS_sum GRBM_GUI_ACTIVE"),
+    ("ta", "TA_TA_BUSY_sum TD_TD_BUSY_sum GRBM_TA_BUSY GRBM_GUI_ACTIVE TCP_TCC_READ_REQ_sum "
+           "TCP_TCC_READ_REQ_LATENCY_sum"),
+]
+PROBE_TITLES = {
+    "c2_gemm": "configs[1] GEMM 4096^3, FP16 out (`gemm_dma_kernel<256,256,true>`)",
+    "c3_sparse": "configs[2] 2:4 sparse 4096x11008x4096, INT32 out (`sparse_dma32_kernel<false>`)",
+    "c3_dense": "configs[2] shape dense, INT32 out (`gemm_dma_kernel<256,256,false>`)",
+    "c5_conv": "configs[4] NHWC conv, INT32 out (`gemm_dma_kernel<256 and 192,256,false,DmaConv>`, 2 launches)",
+    "c4_dense_M16": "configs[3] M=16 dense decode GEMM (`decode_dense_kernel`)",
+    "c4_sparse_M16": "configs[3] M=16 2:4 decode GEMM (`decode_sparse_kernel`)",
+}
+
+
+def _counter_markdown(out) -> str:
+    cal = out["calibration"]
+    L = ["# Hardware counters of the dominant kernels (one MI355X)", "",
+         "Made by `bench.py --traffic-probe` under `rocprofv3 --pmc`, one counter set per run, then "
+         "`python bench.py --counter-summary <out>` (this file and `kernel_counters.json`). Commands, from the "
+         "repository root on the GPU box:", "", "```", "cd /tmp && export TMPDIR=/tmp && cd <repo>"]
+    for name, counters in COUNTER_SETS:
+        L.append(f"rocprofv3 --pmc {counters} --output-format csv -d <out>/{name} -o {name} -- "
+                 f"python3 bench.py --traffic-probe")
+    L += ["python3 bench.py --counter-summary <out>", "```", "",
+          f"Each probe runs its kernel {PROBE_REPS} times; values are medians per call. Definitions:", "",
+          "- clock = (GRBM_GUI_ACTIVE / 8 XCDs - the per-dispatch overhead) / kernel duration in the counter "
+          f"run; the overhead is the smallest per-XCD GRBM_GUI_ACTIVE of the run ({cal.get('gui_overhead_cycles_per_xcd', 0):.0f} "
+          "cycles, a 256-thread fill kernel), taken once per launch.",
+          "- MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (4 SIMDs x SQ_BUSY_CU_CYCLES): matrix-core busy cycles over "
+          "the SIMD cycles of CUs holding waves. The counter adds 32 cycles per `v_mfma_i32_32x32x32_i8` and per "
+          "`v_smfmac_i32_32x32x64_i8` (checked: c2 = 2,097,152 MFMAs x 32); `at clock` divides by 1024 SIMDs x "
+          "clock x duration instead.",
+          "- peak at clock = the 2.4 GHz peak (dense INT8 5.0 POP/s, 2:4 10.0) scaled to the measured clock.",
+          f"- HBM bytes = FETCH_SIZE x {cal['fetch_scale']:.3f} + WRITE_SIZE x {cal['write_scale']:.3f} (KiB x 1024), "
+          f"the factors that make a {COPY_PROBE_BYTES >> 20} MiB device copy in the same runs read and write its size "
+          f"(FETCH_SIZE {cal['copy_fetch_kib']:.1f} KiB, WRITE_SIZE {cal['copy_write_kib']:.1f} KiB).",
+          "- L2 read latency = TCP_TCC_READ_REQ_LATENCY_sum / TCP_TCC_READ_REQ_sum (cycles); TA busy = "
+          "TA_TA_BUSY_sum / 256 / (clock x duration).", "",
+          "| probe | us (counter run) | clock GHz | MFMA busy (at clock) | peak at clock | HBM MB (alg.) | L2 hit | "
+          "L2 lat. | TA busy | LDS confl./active |",
+          "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for p, e in out["kernels"].items():
+        unit = "TOPS"
+        L.append(f"| {PROBE_TITLES.get(p, p)} | {e['duration_us_in_counter_run']:.1f} | {e.get('clock_ghz', 0):.2f} | "
+                 f"{100 * e.get('mfma_busy', 0):.1f} % ({100 * e.get('mfma_busy_at_clock', 0):.1f} %) | "
+                 f"{e.get('peak_tops_at_clock', 0):.0f} {unit} | {e.get('traffic_bytes', 0) / 1e6:.1f} "
+                 f"({e['algorithmic_bytes'] / 1e6:.1f}) | {100 * (e.get('l2_hit_rate') or 0):.1f} % | "
+                 f"{e.get('l2_read_latency_cycles', 0):.0f} | {100 * e.get('ta_busy', 0):.0f} % | "
+                 f"{e.get('lds_bank_conflict_per_active', 0):.3f} |")
+    L += ["", "Raw medians per call (counter: value) are in `kernel_counters.json` under each probe's `raw`.", ""]
+    return "\n".join(L)
 
 
 def events_time_ms(fn, reps: int) -> float:
@@ -520,9 +767,12 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true")
+    ap.add_argument("--counter-summary", metavar="DIR", default=None)
     args = ap.parse_args()
     if args.traffic_probe:
         return traffic_probe()
+    if args.counter_summary:
+        return counter_summary(args.counter_summary)
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(the W8A8 kernels shard by token rows or weight columns with no communication).",
