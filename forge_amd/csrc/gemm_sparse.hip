@@ -546,7 +546,158 @@ struct SpDmaTile32 {
     }
 };
 
-template <bool DEQUANT>
+// SpDmaTile32 with 256-deep weight stages (K % 256 == 0): each compressed weight row's 128
+// bytes covering two dense 128-deep stages arrive as one full cache line (one 128-byte
+// request instead of two 64-byte ones), every other stage, into a 2-slot weight ring of its
+// own; tokens and index words keep their per-stage 2-slot rings. A stage's L2 requests go from
+// 256 (tokens) + 256 (weights, 64 B) + 32 (index) to 256 + 128 + 32 on average. Weight rows use
+// the token rows' 128-byte swizzle (lds_off128), the half of stage kt being chunks 4 (kt & 1) ..
+// 4 (kt & 1) + 3. Slot reuse: the weights of stages (kt + 2, kt + 3) are issued at stage kt's
+// barrier (kt even); their slot held stages (kt - 2, kt - 1), last read before stage kt - 1's
+// barrier.
+struct SpDmaTile32W {
+    static constexpr int BNW = 256, BMT = 256;
+    static constexpr int kTN = 4, kTM = 4;
+    static constexpr int kWBytes = BNW * 128;          // one weight slot: two stages
+    static constexpr int kXBytes = BMT * 128;
+    static constexpr int kIBytes = BNW / 16 * 256;
+    static constexpr int kXOff = 2 * kWBytes;
+    static constexpr int kIOff = kXOff + 2 * kXBytes;
+    static constexpr int kLdsBytes = kIOff + 2 * kIBytes;
+    static constexpr int kWIns = BNW * 8 / kWave / 4;   // 1 KB DMA instructions per wave per weight slot
+    static constexpr int kXIns = BMT * 8 / kWave / 4;
+
+    v16i acc[kTN][kTM];   // acc[j][i]: D[n: 32j + row(e, l)][m: 32i + l%32]
+
+    struct Frags { v4i a[kTN]; int idx[kTN]; v8i b[kTM]; };
+
+    __device__ __forceinline__ void run(const int8_t* W, const int8_t* X, const uint32_t* meta, int M, int N,
+                                        int K, int n0, int m0, int8_t* lds) {
+        const int lane = threadIdx.x & (kWave - 1);
+        const int wave = threadIdx.x / kWave;
+        const int wm = (wave >> 1) * (BMT / 2);
+        const int wn = (wave & 1) * (BNW / 2);
+        const int l31 = lane & 31, g = lane >> 5;
+        const int Kc = K >> 1, cpr = K >> 5;
+
+#pragma unroll
+        for (int j = 0; j < kTN; j++)
+#pragma unroll
+            for (int i = 0; i < kTM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[j][i][e] = 0;
+
+        // 32-bit byte offsets into buffer resources (the launcher checks N * K / 2 and M * K
+        // < 2^31): one VGPR per load instead of a 64-bit address, which the 256 accumulators
+        // leave no room for; the stage offset goes in the instruction's scalar offset.
+        uint32_t ow[kWIns], ox[kXIns];
+#pragma unroll
+        for (int q = 0; q < kWIns; q++) {
+            const int s = (wave * kWIns + q) * kWave + lane;
+            const int r = s >> 3, c = (s & 7) ^ lds_swz8(r);
+            const int gr = (n0 + r) < N ? (n0 + r) : N - 1;
+            ow[q] = static_cast<uint32_t>(gr) * static_cast<uint32_t>(Kc) + 16 * c;
+        }
+#pragma unroll
+        for (int q = 0; q < kXIns; q++) {
+            const int s = (wave * kXIns + q) * kWave + lane;
+            const int r = s >> 3, c = (s & 7) ^ lds_swz8(r);
+            const int gr = (m0 + r) < M ? (m0 + r) : M - 1;
+            ox[q] = static_cast<uint32_t>(gr) * static_cast<uint32_t>(K) + 16 * c;
+        }
+        uint32_t oi;
+        {
+            const int s = wave * kWave + lane;
+            int b = (n0 >> 4) + (s >> 4);
+            b = b < (N >> 4) ? b : (N >> 4) - 1;
+            const int k = (s & 15) ^ (((s >> 4) & 1) * 12);
+            oi = static_cast<uint32_t>(b) * static_cast<uint32_t>(cpr) * 64u + 16u * k;
+        }
+        const __amdgpu_buffer_rsrc_t rw = buf_rsrc(W, static_cast<uint32_t>(N) * static_cast<uint32_t>(Kc));
+        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(X, static_cast<uint32_t>(M) * static_cast<uint32_t>(K));
+        const __amdgpu_buffer_rsrc_t ri = buf_rsrc(meta, static_cast<uint32_t>(N) * static_cast<uint32_t>(cpr) * 4u);
+        const int nst = K / 128;   // even
+        // Stage st's tokens and index words; at even st also the weights of st and st + 1.
+        auto issue = [&](int st, bool with_w) {
+            const int sc = st < nst ? st : nst - 1;       // past the end: re-read (dead slot)
+            if (with_w) {
+                const int sw = st < nst ? st : nst - 2;
+                int8_t* wslot = lds + ((st >> 1) & 1) * kWBytes;
+#pragma unroll
+                for (int q = 0; q < kWIns; q++)
+                    dma16_buf(rw, ow[q], static_cast<uint32_t>(sw * 64), wslot + (wave * kWIns + q) * 1024);
+            }
+            int8_t* xslot = lds + kXOff + (st & 1) * kXBytes;
+#pragma unroll
+            for (int q = 0; q < kXIns; q++)
+                dma16_buf(rx, ox[q], static_cast<uint32_t>(sc * 128), xslot + (wave * kXIns + q) * 1024);
+            dma16_buf(ri, oi, static_cast<uint32_t>(sc * 256), lds + kIOff + (st & 1) * kIBytes + wave * 1024);
+        };
+        auto load = [&](int st, int h, Frags& F) {
+            const int8_t* Ws = lds + ((st >> 1) & 1) * kWBytes;
+            const int8_t* Xs = lds + kXOff + (st & 1) * kXBytes;
+            const uint32_t* Is = reinterpret_cast<const uint32_t*>(lds + kIOff + (st & 1) * kIBytes);
+            const int wc = 4 * (st & 1) + 2 * h + g;
+#pragma unroll
+            for (int j = 0; j < kTN; j++) {
+                const int r = wn + 32 * j + l31;
+                F.a[j] = *reinterpret_cast<const v4i*>(Ws + lds_off128(r, wc));
+                const int w = ((2 * h + g) * 16 + (r & 15)) ^ (((r >> 4) & 1) * 48);
+                F.idx[j] = static_cast<int>(Is[(r >> 4) * 64 + w]);
+            }
+#pragma unroll
+            for (int i = 0; i < kTM; i++) {
+                const int r = wm + 32 * i + l31;
+                const v4i lo = *reinterpret_cast<const v4i*>(Xs + lds_off128(r, 4 * h + g));
+                const v4i hi = *reinterpret_cast<const v4i*>(Xs + lds_off128(r, 4 * h + 2 + g));
+                F.b[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+        };
+        auto smfmacs = [&](const Frags& F) {
+#pragma unroll
+            for (int j = 0; j < kTN; j++)
+#pragma unroll
+                for (int i = 0; i < kTM; i++)
+                    acc[j][i] = __builtin_amdgcn_smfmac_i32_32x32x64_i8(F.a[j], F.b[i], acc[j][i], F.idx[j], 0, 0);
+        };
+        constexpr int kMf = kTN * kTM, kRd = 2 * kTN + 2 * kTM;
+        // Stage kt as in SpDmaTile32; EVEN: kt is even, so the weights of kt + 2, kt + 3 are
+        // issued with the tokens of kt + 2.
+        auto stage = [&](int kt, Frags& F0, Frags& F1, auto even) {
+            constexpr bool EVEN = decltype(even)::value;
+            constexpr int kVm = kXIns + 1 + (EVEN ? kWIns : 0);
+            load(kt, 1, F1);
+            smfmacs(F0);
+            sched_interleave<kMf, kRd, 0>();
+            wait_vm_lgkm0();
+            lds_barrier();
+            issue(kt + 2, EVEN);
+            load(kt + 1, 0, F0);
+            smfmacs(F1);
+            sched_interleave<kMf / 2, 0, kVm>();
+            sched_interleave<kMf / 2, kRd, 0>();
+        };
+        issue(0, true);
+        wait_vm_lgkm0();
+        lds_barrier();
+        issue(1, false);
+        Frags F0, F1;
+        load(0, 0, F0);
+        int kt = 0;
+        for (; kt + 2 < nst; kt += 2) {
+            stage(kt, F0, F1, std::true_type{});
+            stage(kt + 1, F0, F1, std::false_type{});
+        }
+        stage(kt, F0, F1, std::true_type{});   // kt = nst - 2
+        load(nst - 1, 1, F1);
+        smfmacs(F0);
+        smfmacs(F1);
+        wait_vm_lgkm0();
+        lds_barrier();
+    }
+};
+
+template <bool DEQUANT, class Tile>
 __global__ __launch_bounds__(256) void sparse_dma32_kernel(const int8_t* __restrict__ W, const int8_t* __restrict__ X,
                                                            const uint32_t* __restrict__ meta, GemmEpilogue ep,
                                                            int tiles_n, int tiles_m, int K)
@@ -555,25 +706,40 @@ __global__ __launch_bounds__(256) void sparse_dma32_kernel(const int8_t* __restr
     int tn, tm;
     tile_coords(blockIdx.x, tiles_n, tiles_m, tn, tm);
     const int n0 = tn * 256, m0 = tm * 256;
-    SpDmaTile32 t;
+    Tile t;
     t.run(W, X, meta, ep.M, ep.N, K, n0, m0, lds);
     store_tile<256, 256, DEQUANT>(t.acc, ep, m0, n0, lds);
 }
 
-template <bool DEQUANT>
-static int launch_sparse_dma32(const int8_t* W, const int8_t* X, const uint32_t* meta, const GemmEpilogue& ep,
-                               int K, hipStream_t s)
+template <bool DEQUANT, class Tile>
+static int launch_sparse_dma32_tile(const int8_t* W, const int8_t* X, const uint32_t* meta, const GemmEpilogue& ep,
+                                    int K, hipStream_t s)
 {
     constexpr int epi = epilogue_lds_bytes<256, 256, DEQUANT>();
-    constexpr int lds = SpDmaTile32::kLdsBytes > epi ? SpDmaTile32::kLdsBytes : epi;
+    constexpr int lds = Tile::kLdsBytes > epi ? Tile::kLdsBytes : epi;
     const int tiles_n = divup(ep.N, 256), tiles_m = divup(ep.M, 256);
     const long long total = static_cast<long long>(tiles_n) * tiles_m;
     if (total > 0x7FFFFFFFLL) return FORGE_EINVAL;
     static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&sparse_dma32_kernel<DEQUANT>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        reinterpret_cast<const void*>(&sparse_dma32_kernel<DEQUANT, Tile>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        lds);
     if (attr != hipSuccess) return static_cast<int>(attr);
-    sparse_dma32_kernel<DEQUANT><<<static_cast<unsigned>(total), 256, lds, s>>>(W, X, meta, ep, tiles_n, tiles_m, K);
+    sparse_dma32_kernel<DEQUANT, Tile><<<static_cast<unsigned>(total), 256, lds, s>>>(W, X, meta, ep, tiles_n, tiles_m,
+                                                                                      K);
     return launch_status();
+}
+
+// 256 x 256 SMFMAC engine: 256-deep weight stages (full 128-byte lines) for INT32 outputs when
+// K % 256 == 0 (configs[2]: 175 -> 160 us, measured in one run); the FP16 epilogue's registers
+// do not fit beside them (the kernel spills), so dequantizing outputs keep 128-deep stages.
+template <bool DEQUANT>
+static int launch_sparse_dma32(const int8_t* W, const int8_t* X, const uint32_t* meta, const GemmEpilogue& ep,
+                               int K, hipStream_t s)
+{
+    if (!DEQUANT && K % 256 == 0 && static_cast<long long>(ep.N) * (K / 2) < (1LL << 31) &&
+        static_cast<long long>(ep.M) * K < (1LL << 31) && static_cast<long long>(ep.N) * (K / 32) * 4 < (1LL << 31))
+        return launch_sparse_dma32_tile<DEQUANT, SpDmaTile32W>(W, X, meta, ep, K, s);
+    return launch_sparse_dma32_tile<DEQUANT, SpDmaTile32>(W, X, meta, ep, K, s);
 }
 
 // Epilogue of a SpDmaTile: lane l of block (i, j) holds outputs (m = 16j + l%16, n = 16i +

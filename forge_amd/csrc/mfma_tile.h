@@ -64,6 +64,18 @@ __device__ __forceinline__ void dma16(const int8_t* src, int8_t* lds_base) {
     __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
 }
 
+// The same DMA through a buffer resource (buffer_load_dwordx4 ... lds): this lane's 16 bytes
+// at byte offset voff + soff of the resource land at lds_base + 16 * lane. The offsets are
+// 32-bit (voff per lane, soff wave-uniform), so no 64-bit address is formed per load, and a
+// read past the resource's size returns zeros instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, int8_t* lds_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base, 16, voff, soff, 0,
+                                             0);
+}
+
 // Instruction-scheduling pattern for one MFMA sub-step: NMFMA MFMAs with NDS LDS reads and
 // NVM vector-memory (DMA) instructions spread evenly between them, in issue order. Without
 // it the scheduler clusters the loads behind the MFMAs.

@@ -215,3 +215,25 @@ def test_sparse_auto_engines(dev, orc, M, K, N):
     ops.sparse_int8_gemm(comp, xd, meta, to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev), split_k=0, out=Y)
     ref = orc.dequant_epilogue(acc, act[rows], ws, b).view(np.uint16)
     assert np.array_equal(to_host(Y)[rows].view(np.uint16), ref)
+
+
+# The 256 x 256 SMFMAC engine with 256-deep weight stages (INT32 out, K % 256 == 0): one and
+# three weight double-stages, ragged token and weight tiles; every output against the oracle.
+# The grid is large enough that the engine choice takes 256 x 256 tiles (checked by route).
+@pytest.mark.parametrize("M,K,N", [(4040, 256, 8112), (4096, 768, 8192), (3000, 512, 8208)])
+def test_sparse_256x256_int32_whole(dev, orc, M, K, N):
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(M + K + N)
+    W = int8_uniform(rng, (N, K))
+    x = int8_uniform(rng, (M, K))
+    cr, mr = orc.prune_compress_24(W)
+    ref = orc.sparse_gemm_s32(cr, x, mr, N, K, threads=orc.cpu_threads())
+    comp, raw, meta = _prep(dev, W)
+    say(f"sparse 256x256 INT32 M={M} K={K} N={N}")
+    C = torch.empty((M, N), dtype=torch.int32, device=dev)
+    poison(C, 0x7B)
+    got = to_host(ops.sparse_int8_gemm_s32(comp, to_dev(x, dev), meta, out=C))
+    assert ops.last_route() == "dma256x256"
+    bad = int((got != ref).sum())
+    assert bad == 0, f"{bad} of {got.size} outputs differ"
