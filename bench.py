@@ -26,7 +26,8 @@ overhead is not timed; the whole int8_linear / sparse_int8_linear, and the GEMM 
 pre-quantized tokens, *_gemm_*), configs[4] (INT8 NHWC 3x3 conv, INT32 and dequant outputs), and
 the rest of the INT8 conv family on NCHW FP16 maps: depthwise 3x3 (1, 64, 540, 960) and
 ConvTranspose2d k2s2 (1, 64, 270, 480) -> (1, 32, 540, 960), as time and HBM GB/s of
-input + output bytes (rotating over more than 256 MB of inputs and outputs, graph-replayed); and SparseLinear's weight preparation at 11008 x 4096 fp32, one pass
+input + output bytes (rotating over more than 256 MB of inputs and outputs, graph-replayed); the
+reference's NCHW FP16 int8_conv2d_forward on a (1, 32, 540, 960) 3x3 layer (one fused launch); and SparseLinear's weight preparation at 11008 x 4096 fp32, one pass
 against the reference's separate quantize / prune+compress / pack steps; and
 extra.reference_sweep: the reference's own sparse benchmark (bench_int8_sparse.cu shapes and
 protocol) with the dense path beside it.
@@ -702,6 +703,27 @@ def bench_extra(dev):
     out["f2_convT_us"] = t_ct * 1e3
     out["f2_convT_GBs"] = (xts[0].numel() * 2 + yts[0].numel() * 2 + wt.numel()) / t_ct / 1e6
     del xds, yds, xts, yts, wsp
+    torch.cuda.empty_cache()
+
+    # The reference's NCHW FP16 conv API (int8_conv2d_forward) on one launch: per-patch-row
+    # quantize, implicit GEMM and NCHW epilogue fused; an upscaler-style 3x3 layer,
+    # (1, 32, 540, 960) -> (1, 32, 540, 960), pad 1; HBM GB/s of input + output bytes, rotating
+    # over 5 input/output pairs (330 MB) so the MALL cannot hold them, graph-replayed.
+    nn_ = 5
+    xcs = [(torch.rand((1, 32, 540, 960), generator=g, device=dev) * 2 - 1).half() for _ in range(nn_)]
+    wcn = torch.randint(-127, 128, (32, 32 * 9), generator=g, device=dev, dtype=torch.int8)
+    wscn = (torch.rand((32,), generator=g, device=dev) * 0.045 + 0.005).half()
+    bcn = (torch.rand((32,), generator=g, device=dev) - 0.5).half()
+    ycs = [torch.empty((1, 32, 540, 960), dtype=torch.float16, device=dev) for _ in range(nn_)]
+    wspn = torch.empty((ops.int8_conv2d_workspace_size(32, 540, 960, 32, 3, 3, 1, 1, 1, 1),), dtype=torch.uint8,
+                       device=dev)
+    cns = [lambda i=i: ops.int8_conv2d_forward(xcs[i], wcn, wscn, bcn, 3, 3, (1, 1), (1, 1), (1, 1), workspace=wspn,
+                                               out=ycs[i]) for i in range(nn_)]
+    t_cn = graph_time_ms(cns * 4)
+    out["f2_conv_nchw_us"] = t_cn * 1e3
+    out["f2_conv_nchw_GBs"] = (xcs[0].numel() * 2 + ycs[0].numel() * 2) / t_cn / 1e6
+    out["f2_conv_nchw_tops"] = 2.0 * 540 * 960 * 32 * 288 / t_cn / 1e9
+    del xcs, ycs, wspn
     torch.cuda.empty_cache()
 
     # Weight preparation for SparseLinear at configs[2]'s weight (11008 x 4096, fp32): the one

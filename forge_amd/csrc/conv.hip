@@ -19,6 +19,7 @@
 #include "forge/nn/int8_conv2d.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace forge_amd {
 
@@ -86,6 +87,530 @@ __global__ __launch_bounds__(256) void transpose_f16_kernel(const uint16_t* __re
     }
 }
 
+// ---- NCHW FP16 conv in one launch (implicit GEMM with per-patch-row quantization) ------
+//
+// The reference's int8_conv2d_forward (src/nn/int8_conv2d.cu:151-223) runs, per image, an FP16
+// im2col into the workspace, the per-row quantize of that patch matrix, the dequantizing GEMM
+// and a transpose to NCHW: 4 launches and ~3 passes over a K-times-inflated buffer per image.
+// conv_nchw_fused_kernel does all of it in one pass for every image of the call: a workgroup
+// owns a tile of up to 64 output pixels (R output rows x Wt columns of one image) and all
+// output channels.
+//   1. It loads the input window of the tile -- C x IH x IW FP16 values, zero outside the
+//      image -- into LDS once (coalesced along W).
+//   2. Per pixel, the absmax over its patch (C x kH x kW taps, the reference's im2col row,
+//      padding included as zeros) is a max over LDS (fmaxf, which skips NaN as the reference
+//      quantizer's reduction does), giving scale = max(absmax, 1e-8) / 127 and 1 / scale.
+//   3. The patch rows are quantized into an INT8 A tile in LDS (64 rows x Kp bytes, K in the
+//      reference's c*kH*kW + kh*kW + kw order, zero from K to Kp; row pitch Kp + 16 bytes so
+//      the 16 rows of a ds_read_b128 phase fall on distinct banks).
+//   4. v_mfma_i32_32x32x32_i8 items (32 output channels x 32 pixels) go round-robin to the 4
+//      waves; weight fragments (the reference's (C_out, K) rows, K % 16 == 0) come from L2.
+//   5. The accumulators are dequantized as the reference's GEMM epilogue does
+//      (fma((float)acc, act_scale * w_scale, bias), one FP16 rounding) and stored straight to
+//      NCHW: 32 adjacent pixels of one channel per store instruction.
+// Every output equals the reference pipeline's on the same input: the INT8 rows and scales are
+// those of quantize_rows on the im2col rows, the INT32 sums are exact, the epilogue identical.
+struct ConvNchwArgs {
+    const uint16_t* x;
+    const int8_t* w;
+    const uint16_t* w_scale;
+    const uint16_t* bias;
+    uint16_t* y;
+    int C, H, W, Co, kH, kW, padH, padW, sH, sW, dH, dW, Ho, Wo;
+    int K, Kp, pitch;          // patch length, padded to 32, A row pitch (bytes)
+    int R, Wt, IH, IW;         // tile rows / columns, input window rows / columns
+    int P, G;                  // window row pitch (values); 8-value groups per row (vector loads)
+    int tiles_h, tiles_w, tiles, N;
+    int xin_bytes;             // LDS bytes of the input window (16-byte multiple)
+    int Cop;                   // Co rounded up to 32 (w_scale / bias strips in LDS)
+    int rpi, ninst, step_c, step_ih;   // vector loads: rows per instruction, instructions, 4 rpi rows as (c, ih)
+    uint32_t mg_khw, mg_kw, mg_ih, mg_wt, mg_g;   // udiv_magic multipliers
+    uint32_t x_bytes, y_bytes; // bytes of one image of x / of y (buffer-resource ranges)
+};
+
+constexpr int kCnPix = 64;     // output pixels per workgroup tile
+
+// n / d for n * d < 2^32, with m = ceil(2^32 / d) (m = 0 stands for d = 1): n m / 2^32 exceeds
+// n / d by n (m d - 2^32) / (d 2^32) < 1 / d, which cannot carry it past the next integer.
+__device__ __forceinline__ int udiv_magic(int n, uint32_t m) {
+    return m ? static_cast<int>(__umulhi(static_cast<uint32_t>(n), m)) : n;
+}
+static uint32_t udiv_multiplier(int d) {
+    return d == 1 ? 0u : static_cast<uint32_t>(((1ULL << 32) + d - 1) / d);
+}
+
+// One value of a quantized row as qrow_bits computes it, with the fp16 widening and the product
+// in one v_fma_mix_f32 (f16 source in the low half, fp32 inv, + 0): fma(a, b, 0) rounds a b once
+// as the multiply does (only a zero's sign can differ, and the + 1.5 2^23 erases it).
+__device__ __forceinline__ uint32_t qrow_bits_mix(uint32_t h, float inv) {
+    float p;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(p) : "v"(h), "v"(inv));
+    return __float_as_uint(p + 12582912.0f);
+}
+
+// A persistent workgroup runs tiles start, start + stride, ... of its XCD's contiguous range
+// (xcd_contiguous's split of the tiles over the 8 XCDs), so the workgroups of one XCD work on
+// neighbouring tiles together and share their window halos in that XCD's L2.
+struct ConvTileWalk {
+    int next, end, stride;
+};
+__device__ __forceinline__ ConvTileWalk conv_tile_walk(int total)
+{
+    constexpr int kXcd = 8;
+    const int b = blockIdx.x, grid = gridDim.x;
+    const int x = b % kXcd, j = b / kXcd;
+    const int q = total / kXcd, r = total % kXcd;
+    const int gq = grid / kXcd, gr = grid % kXcd;
+    const int start = x * q + min(x, r);
+    return {start + j, start + q + (x < r ? 1 : 0), gq + (x < gr ? 1 : 0)};
+}
+
+// VEC (W % 8 == 0, 16-byte-aligned input): window rows start at the 8-aligned column at or
+// before the window's first one (shift s0 = 0..7) and load as 16-byte buffer loads, several rows
+// per instruction, whose out-of-image groups read as zeros (offsets past the buffer's range);
+// with PF the next tile's loads are in flight while the current tile computes (a.ninst <=
+// 4 kPF). Otherwise 2-byte loads, one row per instruction and lane.
+constexpr int kPF = 4;   // prefetched 16-byte loads per lane (4 workgroups per CU keep 128 VGPRs)
+template <bool VEC, bool PF>
+__global__ __launch_bounds__(256, 4) void conv_nchw_fused_kernel(ConvNchwArgs a)
+{
+    extern __shared__ __align__(16) int8_t lds[];
+    uint16_t* xin = reinterpret_cast<uint16_t*>(lds);
+    int8_t* At = lds + a.xin_bytes;
+    float* s_scale = reinterpret_cast<float*>(At + kCnPix * a.pitch);
+    float* s_inv = s_scale + kCnPix;
+    float* s_m1 = s_inv + kCnPix;                         // per window position: channel absmax
+    int* koff = reinterpret_cast<int*>(s_m1 + ((a.IH * a.P + 3) & ~3));   // per k: window offset of tap k
+    float* s_ws = reinterpret_cast<float*>(koff + a.K);   // Cop entries each, zero past Co
+    float* s_b = s_ws + a.Cop;
+
+    const int t = threadIdx.x, lane = t & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int l31 = lane & 31, hi = lane >> 5;
+    const int P = a.P;
+    const int HW = a.H * a.W;
+    const int IHP = a.IH * P;
+    const int ksteps = a.Kp >> 5;
+    const int items = ((a.Co + 31) >> 5) * 2;
+    const int rows = a.C * a.IH;
+    const int npix = a.R * a.Wt;
+    const uint32_t plane2 = 2u * static_cast<uint32_t>(a.Ho * a.Wo);
+    const bool has_bias = a.bias != nullptr;
+
+    // weight fragments: kG in flight per wave
+    constexpr int kG = 4;
+    v4i fw[kG];
+    auto load_w = [&](int it, int ks0) {
+        const int co_l = min((it >> 1) * 32 + l31, a.Co - 1);
+        const int8_t* wr = a.w + static_cast<size_t>(co_l) * a.K;
+#pragma unroll
+        for (int g = 0; g < kG; g++) {
+            const int kk = 32 * (ks0 + g) + 16 * hi;
+            fw[g] = *reinterpret_cast<const v4i*>(wr + (ks0 + g < ksteps && kk < a.K ? kk : 0));
+        }
+    };
+
+    // 0. tap offsets into the window (k = c kH kW + kh kW + kw, the reference's im2col order)
+    //    and the w_scale / bias strips as floats, once per workgroup
+    for (int k = t; k < a.K; k += 256) {
+        const int c = udiv_magic(k, a.mg_khw), r = k - c * (a.kH * a.kW);
+        const int kh = udiv_magic(r, a.mg_kw), kw = r - kh * a.kW;
+        koff[k] = c * IHP + kh * a.dH * P + kw * a.dW;
+    }
+    for (int c = t; c < a.Cop; c += 256) {
+        s_ws[c] = c < a.Co ? h2f(a.w_scale[c]) : 0.0f;
+        s_b[c] = c < a.Co && a.bias ? h2f(a.bias[c]) : 0.0f;
+    }
+
+    // Tile geometry
+    struct Geo {
+        int n, ho0, wo0, hb, a0, s0;
+    };
+    auto geo_of = [&](int tile) {
+        Geo g;
+        g.n = tile / a.tiles;
+        const int rem = tile - g.n * a.tiles;
+        const int th = rem / a.tiles_w, tw = rem - th * a.tiles_w;
+        g.ho0 = th * a.R;
+        g.wo0 = tw * a.Wt;
+        g.hb = g.ho0 * a.sH - a.padH;
+        const int wb = g.wo0 * a.sW - a.padW;
+        g.a0 = VEC ? (wb & ~7) : wb;                     // global column of window value 0
+        g.s0 = wb - g.a0;                                // window column iw sits at iw + s0
+        return g;
+    };
+
+    // 1. input window (C x IH rows, zero outside the image), VEC form: lane l of an instruction
+    //    takes 8-value group l % G of window row slot l / G; the wave's instructions i = wave,
+    //    wave + 4, ... cover rows [i rpi, i rpi + rpi), stepping (c, ih) by 4 rpi rows. W % 8 == 0,
+    //    so a group lies wholly inside the image or wholly outside it. The window holds
+    //    ninst * rpi rows (rows past C IH are zeros and never read).
+    const int slot = VEC ? udiv_magic(lane, a.mg_g) : 0, grp = lane - slot * a.G;
+    const bool lok = VEC && slot < a.rpi;
+    const int r_first = wave * a.rpi + slot;
+    const int c_first = VEC ? udiv_magic(r_first, a.mg_ih) : 0, ih_first = r_first - c_first * a.IH;
+    const int dgoff = a.step_c * HW + a.step_ih * a.W, wrap = HW - a.IH * a.W;
+    // issues the loads of instructions i0, i0 + 4, ... (kIB of them) of tile g into v
+    auto issue_vec = [&](const Geo& g, int& r, int& ih, int& goff, v4i* v, int kIB) {
+        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x + static_cast<size_t>(g.n) * a.C * HW, a.x_bytes);
+        const int col = g.a0 + 8 * grp;
+        const bool cok = col >= 0 && col < a.W;
+        for (int q = 0; q < kIB; q++) {
+            const bool ok = cok && r < rows && static_cast<unsigned>(g.hb + ih) < static_cast<unsigned>(a.H);
+            v[q] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? 2u * static_cast<uint32_t>(goff + col) : 0x80000000u,
+                                                         0, 0);
+            r += 4 * a.rpi;
+            ih += a.step_ih;
+            goff += dgoff;
+            if (ih >= a.IH) {
+                ih -= a.IH;
+                goff += wrap;
+            }
+        }
+    };
+    auto goff_first = [&](const Geo& g) { return c_first * HW + (g.hb + ih_first) * a.W; };
+
+    v4i pf[PF ? kPF : 1];
+    auto prefetch = [&](const Geo& g) {
+        int r = r_first, ih = ih_first, goff = goff_first(g);
+#pragma unroll
+        for (int q = 0; q < (PF ? kPF : 1); q++) {
+            if (PF && wave + 4 * q < a.ninst) issue_vec(g, r, ih, goff, &pf[q], 1);
+        }
+    };
+    auto store_prefetched = [&]() {
+        if (lok) {
+#pragma unroll
+            for (int q = 0; q < (PF ? kPF : 1); q++)
+                if (PF && wave + 4 * q < a.ninst)
+                    *reinterpret_cast<v4i*>(xin + (r_first + 4 * q * a.rpi) * P + 8 * grp) = pf[q];
+        }
+    };
+    auto load_window_sync = [&](const Geo& g) {
+        if constexpr (VEC) {
+            int r = r_first, ih = ih_first, goff = goff_first(g);
+            constexpr int kIB = 4;
+            for (int i0 = wave; i0 < a.ninst; i0 += 4 * kIB) {
+                v4i v[kIB];
+                const int rb = r;
+#pragma unroll
+                for (int q = 0; q < kIB; q++) issue_vec(g, r, ih, goff, &v[q], 1);
+                if (lok) {
+#pragma unroll
+                    for (int q = 0; q < kIB; q++)
+                        if (i0 + 4 * q < a.ninst) *reinterpret_cast<v4i*>(xin + (rb + 4 * q * a.rpi) * P + 8 * grp) = v[q];
+                }
+            }
+        } else {
+            // Row (c, ih) of wave c % 4; up to kRB rows per batch, loads issued together.
+            const uint16_t* xn = a.x + static_cast<size_t>(g.n) * a.C * HW;
+            const int nu = a.IW > kWave ? 2 : 1;   // the plan keeps IW <= 128 here
+            bool cok[2];
+            int wi[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int iw = lane + kWave * u;
+                wi[u] = g.a0 + iw;
+                cok[u] = u < nu && iw < a.IW && wi[u] >= 0 && wi[u] < a.W;
+            }
+            const int nrw = ((a.C - wave + 3) / 4) * a.IH;   // rows of this wave
+            constexpr int kRB = 16;
+            int cc0 = 0, ih0 = 0;
+            for (int i0 = 0; i0 < nrw; i0 += kRB) {
+                uint16_t v[kRB][2];
+                int cc = cc0, ih = ih0;
+#pragma unroll
+                for (int q = 0; q < kRB; q++) {
+                    const int c = wave + 4 * cc;
+                    const int h_ = g.hb + ih;
+                    const bool rok = i0 + q < nrw && h_ >= 0 && h_ < a.H;
+                    const uint16_t* xr = xn + static_cast<size_t>(c) * HW + static_cast<size_t>(h_) * a.W;
+#pragma unroll
+                    for (int u = 0; u < 2; u++) v[q][u] = (rok && cok[u]) ? xr[wi[u]] : static_cast<uint16_t>(0);
+                    if (++ih == a.IH) {
+                        ih = 0;
+                        cc++;
+                    }
+                }
+                cc = cc0;
+                ih = ih0;
+#pragma unroll
+                for (int q = 0; q < kRB; q++) {
+                    uint16_t* dst = xin + ((wave + 4 * cc) * a.IH + ih) * P;
+#pragma unroll
+                    for (int u = 0; u < 2; u++)
+                        if (i0 + q < nrw && u < nu && lane + kWave * u < a.IW) dst[lane + kWave * u] = v[q][u];
+                    if (++ih == a.IH) {
+                        ih = 0;
+                        cc++;
+                    }
+                }
+                cc0 = cc;
+                ih0 = ih;
+            }
+        }
+    };
+
+    ConvTileWalk walk = conv_tile_walk(a.tiles * a.N);
+    if (walk.next >= walk.end) return;
+    Geo cur = geo_of(walk.next);
+    if constexpr (PF) prefetch(cur);
+
+    while (true) {
+        // the window of the current tile into LDS (the previous tile's readers of xin and At
+        // are past the barrier at the end of the loop)
+        if constexpr (PF) store_prefetched();
+        else load_window_sync(cur);
+        if (wave < items) load_w(wave, 0);   // the first item's first weight fragments
+        const int nxt = walk.next + walk.stride;
+        const bool has_next = nxt < walk.end;
+        Geo ng = cur;
+        if (has_next) ng = geo_of(nxt);
+        __syncthreads();
+        if constexpr (PF) {
+            if (has_next) prefetch(ng);   // in flight while this tile computes
+        }
+
+        // 2. per window position the absmax over the channels on fp16 magnitude bit patterns
+        //    (they order as the magnitudes; a pattern above 0x7C00 is a NaN, and such a position
+        //    takes the fp32 maximum, which skips NaN as the reference quantizer's reduction does),
+        //    then per pixel the max over its kH x kW positions: the absmax of its im2col row
+        //    (padding taps are zeros). s_m1 has the window's layout (IH rows of pitch P).
+        if constexpr (VEC) {
+            // two adjacent positions per thread, as packed u16 maxima of 4-byte reads
+            const int npairs = a.IH * (P >> 1);
+            const uint32_t* x32 = reinterpret_cast<const uint32_t*>(xin);
+            for (int j = t; j < npairs; j += 256) {
+                const uint32_t* xp = x32 + j;
+                uint32_t mb = 0u;
+                int c = 0;
+                for (; c + 8 <= a.C; c += 8) {
+                    uint32_t h[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) h[u] = xp[(c + u) * npairs];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) mb = pk_max_u16(mb, h[u] & 0x7FFF7FFFu);
+                }
+                for (; c < a.C; c++) mb = pk_max_u16(mb, xp[c * npairs] & 0x7FFF7FFFu);
+                float m[2];
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const uint32_t b = (mb >> (16 * u)) & 0xFFFFu;
+                    m[u] = h2f(static_cast<uint16_t>(b));
+                    if (b > kHalfInfBits) {
+                        m[u] = 0.0f;
+                        for (int c2 = 0; c2 < a.C; c2++) m[u] = fmaxf(m[u], fabsf(h2f(xin[2 * j + u + c2 * IHP])));
+                    }
+                }
+                *reinterpret_cast<float2*>(s_m1 + 2 * j) = make_float2(m[0], m[1]);
+            }
+        } else {
+            const int IHW = a.IH * a.IW;
+            for (int pos = t; pos < IHW; pos += 256) {
+                const int ih = pos / a.IW, iw = pos - ih * a.IW;
+                const uint16_t* xp = xin + ih * P + iw;
+                uint32_t mb = 0u;
+                int c = 0;
+                for (; c + 8 <= a.C; c += 8) {
+                    uint32_t h[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) h[u] = xp[(c + u) * IHP];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) mb = max(mb, h[u] & 0x7FFFu);
+                }
+                for (; c < a.C; c++) mb = max(mb, static_cast<uint32_t>(xp[c * IHP]) & 0x7FFFu);
+                float m = h2f(static_cast<uint16_t>(mb));
+                if (mb > kHalfInfBits) {
+                    m = 0.0f;
+                    for (int c2 = 0; c2 < a.C; c2++) m = fmaxf(m, fabsf(h2f(xp[c2 * IHP])));
+                }
+                s_m1[ih * P + iw] = m;
+            }
+        }
+        __syncthreads();
+        if (t < kCnPix) {
+            const int p = t < npix ? t : npix - 1;
+            const int pr = udiv_magic(p, a.mg_wt), pc = p - pr * a.Wt;
+            float m = 0.0f;
+            for (int kh = 0; kh < a.kH; kh++)
+                for (int kw = 0; kw < a.kW; kw++)
+                    m = fmaxf(m, s_m1[(pr * a.sH + kh * a.dH) * P + pc * a.sW + kw * a.dW + cur.s0]);
+            const float scale = row_scale(m);
+            s_scale[t] = scale;
+            s_inv[t] = 1.0f / scale;
+        }
+        __syncthreads();
+
+        // 3. quantized A tile: lane = pixel, a wave takes 16-byte chunks ch = wave, wave + 4, ...;
+        //    a chunk's 16 tap offsets are uniform LDS reads, its 16 window reads issue together
+        //    (adjacent pixels read adjacent window values). K % 16 == 0, so a chunk is all taps or
+        //    all padding (zeros).
+        {
+            const int p = lane < npix ? lane : npix - 1;
+            const int pr = udiv_magic(p, a.mg_wt), pc = p - pr * a.Wt;
+            const int base = pr * a.sH * P + pc * a.sW + cur.s0;
+            const float inv = s_inv[lane];
+            const int nch = a.Kp >> 4, nkc = a.K >> 4;
+            for (int ch = wave; ch < nch; ch += 4) {
+                uint4 qv = make_uint4(0u, 0u, 0u, 0u);
+                if (ch < nkc) {
+                    const int k0 = ch * 16;
+                    int o[16];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int4 v = *reinterpret_cast<const int4*>(koff + k0 + 4 * q);
+                        o[4 * q] = v.x;
+                        o[4 * q + 1] = v.y;
+                        o[4 * q + 2] = v.z;
+                        o[4 * q + 3] = v.w;
+                    }
+                    uint32_t h[16];
+#pragma unroll
+                    for (int j = 0; j < 16; j++) h[j] = xin[base + o[j]];
+                    uint32_t b[16];
+#pragma unroll
+                    for (int j = 0; j < 16; j++) b[j] = qrow_bits_mix(h[j], inv);
+                    qv.x = pack_low_bytes(b[0], b[1], b[2], b[3]);
+                    qv.y = pack_low_bytes(b[4], b[5], b[6], b[7]);
+                    qv.z = pack_low_bytes(b[8], b[9], b[10], b[11]);
+                    qv.w = pack_low_bytes(b[12], b[13], b[14], b[15]);
+                }
+                *reinterpret_cast<uint4*>(At + lane * a.pitch + 16 * ch) = qv;
+            }
+        }
+        __syncthreads();
+
+        // 4./5. MFMA items (32 channels x 32 pixels) and the NCHW epilogue: 2-byte buffer stores at
+        //    32-bit offsets within image n's output, whose channels past Co and pixels outside the
+        //    tile carry offsets past the range (dropped)
+        const __amdgpu_buffer_rsrc_t ry =
+            buf_rsrc(a.y + static_cast<size_t>(cur.n) * a.Co * (plane2 >> 1), a.y_bytes);
+        for (int it = wave; it < items; it += 4) {
+            const int cb = it >> 1, pb = it & 1;
+            const int8_t* ar = At + (pb * 32 + l31) * a.pitch;
+            v16i acc;
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[e] = 0;
+            for (int ks0 = 0; ks0 < ksteps; ks0 += kG) {
+                if (ks0 > 0) load_w(it, ks0);
+#pragma unroll
+                for (int g = 0; g < kG; g++) {
+                    if (ks0 + g < ksteps) {
+                        const v4i fa = *reinterpret_cast<const v4i*>(ar + 16 * (2 * (ks0 + g) + hi));
+                        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[g], fa, acc, 0, 0, 0);
+                    }
+                }
+            }
+            if (it + 4 < items) load_w(it + 4, 0);   // the next item's first fragments
+            const int p = pb * 32 + l31;
+            const int pr = udiv_magic(p, a.mg_wt), pc = p - pr * a.Wt;
+            const int ho = cur.ho0 + pr, wo = cur.wo0 + pc;
+            const bool pok = p < npix && ho < a.Ho && wo < a.Wo;
+            const int co0 = cb * 32 + 4 * hi;
+            const uint32_t vo = pok ? 2u * static_cast<uint32_t>(ho * a.Wo + wo) + static_cast<uint32_t>(co0) * plane2
+                                    : 0x80000000u;
+            const float as = s_scale[p < npix ? p : 0];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 ws4 = *reinterpret_cast<const float4*>(s_ws + co0 + 8 * g);
+                const float4 b4 = *reinterpret_cast<const float4*>(s_b + co0 + 8 * g);
+                const float wsv[4] = {ws4.x, ws4.y, ws4.z, ws4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint16_t yv = dequant_gemm(acc[4 * g + e], as, wsv[e], bv[e], has_bias);
+                    __builtin_amdgcn_raw_buffer_store_b16(yv, ry, vo + static_cast<uint32_t>(8 * g + e) * plane2, 0, 0);
+                }
+            }
+        }
+        if (!has_next) break;
+        walk.next = nxt;
+        cur = ng;
+        __syncthreads();   // xin, s_m1, s_scale and At are free for the next tile
+    }
+}
+
+// Workgroups of fn with lds bytes resident per CU (the persistent grid is CUs times this), or
+// minus a HIP error. Sets the 160 KB dynamic-LDS limit on first use of each kernel.
+static int conv_nchw_fused_residency(const void* fn, size_t lds)
+{
+    static std::once_flag once[3];
+    static hipError_t attr[3];
+    static const void* fns[3] = {reinterpret_cast<const void*>(&conv_nchw_fused_kernel<true, true>),
+                                 reinterpret_cast<const void*>(&conv_nchw_fused_kernel<true, false>),
+                                 reinterpret_cast<const void*>(&conv_nchw_fused_kernel<false, false>)};
+    int i = 0;
+    while (i < 3 && fns[i] != fn) i++;
+    if (i == 3) return -static_cast<int>(hipErrorInvalidDeviceFunction);
+    std::call_once(once[i], [&] {
+        attr[i] = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    });
+    if (attr[i] != hipSuccess) return -static_cast<int>(attr[i]);
+    int blocks = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 256, lds);
+    if (e != hipSuccess) return -static_cast<int>(e);
+    return blocks > 0 ? blocks : 1;
+}
+
+// Geometry of the one-launch path, or false when it does not apply (the per-image pipeline
+// runs instead): K % 16 == 0 with 16-byte-aligned weights (weight fragments are 16-byte
+// loads), the input window and A tile within LDS, the weights small enough to re-read per tile.
+static bool conv_nchw_fused_plan(ConvNchwArgs& a, int N, size_t* lds_bytes, bool* vec)
+{
+    if (a.K % 16 != 0 || !aligned(a.w, 16)) return false;
+    a.Kp = (a.K + 31) & ~31;
+    if (a.Kp > 2048 || static_cast<long long>(a.Co) * a.Kp > (128 << 10) || a.Co > 4096) return false;
+    // buffer-resource offsets of one image stay 32-bit: valid ones below 2^30, and an invalid
+    // 0x80000000 plus a channel offset (channels up to Co rounded to 32) below 2^32
+    a.Cop = (a.Co + 31) & ~31;
+    const long long xb = 2LL * a.C * a.H * a.W, yb = 2LL * a.Co * a.Ho * a.Wo;
+    if (xb >= (1LL << 30) || 2LL * a.Cop * a.Ho * a.Wo >= (1LL << 31)) return false;
+    a.x_bytes = static_cast<uint32_t>(xb);
+    a.y_bytes = static_cast<uint32_t>(yb);
+    *vec = a.W % 8 == 0 && aligned(a.x, 16);
+    a.pitch = a.Kp + 16;
+    a.Wt = a.Wo < kCnPix ? a.Wo : kCnPix;
+    a.R = kCnPix / a.Wt;
+    if (a.R > a.Ho) a.R = a.Ho;
+    a.IH = (a.R - 1) * a.sH + (a.kH - 1) * a.dH + 1;
+    a.IW = (a.Wt - 1) * a.sW + (a.kW - 1) * a.dW + 1;
+    long long xrows = static_cast<long long>(a.C) * a.IH;
+    if (*vec) {
+        // a window row spans the 8-aligned groups from the one holding its first value
+        a.G = (a.IW + 7 + 7) / 8;
+        if (a.G > kWave) return false;
+        a.P = 8 * a.G;
+        a.rpi = kWave / a.G;
+        a.ninst = static_cast<int>((xrows + a.rpi - 1) / a.rpi);
+        xrows = static_cast<long long>(a.ninst) * a.rpi;
+        a.step_c = 4 * a.rpi / a.IH;
+        a.step_ih = 4 * a.rpi - a.step_c * a.IH;
+        a.mg_g = udiv_multiplier(a.G);
+        a.mg_ih = udiv_multiplier(a.IH);
+        if (xrows * a.IH >= (1LL << 32)) return false;   // udiv_magic range (row / IH)
+    } else {
+        if (a.IW > 2 * kWave) return false;
+        a.G = a.rpi = a.ninst = a.step_c = a.step_ih = 0;
+        a.mg_g = a.mg_ih = 0;
+        a.P = a.IW;
+    }
+    a.mg_khw = udiv_multiplier(a.kH * a.kW);
+    a.mg_kw = udiv_multiplier(a.kW);
+    a.mg_wt = udiv_multiplier(a.Wt);
+    const long long xin = (2LL * xrows * a.P + 15) & ~15LL;
+    const long long bytes = xin + static_cast<long long>(kCnPix) * a.pitch + 2 * kCnPix * 4 +
+                            4LL * ((a.IH * a.P + 3) & ~3) + 4LL * a.K + 8LL * a.Cop;
+    if (bytes > 160 * 1024) return false;
+    a.xin_bytes = static_cast<int>(xin);
+    a.tiles_h = divup(a.Ho, a.R);
+    a.tiles_w = divup(a.Wo, a.Wt);
+    const long long tiles = static_cast<long long>(a.tiles_h) * a.tiles_w;
+    if (tiles * N > 0x7FFFFFFFLL) return false;
+    a.tiles = static_cast<int>(tiles);
+    a.N = N;
+    *lds_bytes = static_cast<size_t>(bytes);
+    return true;
+}
+
 }  // namespace forge_amd
 
 using namespace forge_amd;
@@ -113,13 +638,39 @@ extern "C" int forge_int8_conv2d_forward(const uint16_t* input, const int8_t* we
     const int Ho = conv_out(H, padH, dilH, kH, strideH), Wo = conv_out(W, padW, dilW, kW, strideW);
     if (Ho <= 0 || Wo <= 0) return FORGE_OK;
     const int M = Ho * Wo, K = C_in * kH * kW;
+    hipStream_t s = as_stream(stream);
+    {
+        ConvNchwArgs a{input, weight, w_scale, bias, output, C_in, H, W, C_out, kH, kW, padH, padW, strideH, strideW,
+                       dilH, dilW, Ho, Wo, K};
+        size_t lds = 0;
+        bool vec = false;
+        if (conv_nchw_fused_plan(a, N, &lds, &vec)) {
+            const bool pf = vec && a.ninst <= 4 * kPF;
+            const void* fn = vec ? (pf ? reinterpret_cast<const void*>(&conv_nchw_fused_kernel<true, true>)
+                                       : reinterpret_cast<const void*>(&conv_nchw_fused_kernel<true, false>))
+                                 : reinterpret_cast<const void*>(&conv_nchw_fused_kernel<false, false>);
+            int st = FORGE_OK;
+            const DeviceInfo& dinfo = device_info(&st);
+            if (st != FORGE_OK) return st;
+            const int per_cu = conv_nchw_fused_residency(fn, lds);
+            if (per_cu < 0) return -per_cu;
+            const long long total = static_cast<long long>(a.tiles) * N;
+            const long long cap = static_cast<long long>(dinfo.cu_count) * per_cu;
+            const unsigned grid = static_cast<unsigned>(total < cap ? total : cap);
+            note_route(pf ? "conv-nchw-fused prefetch" : "conv-nchw-fused");
+            if (pf) conv_nchw_fused_kernel<true, true><<<grid, 256, lds, s>>>(a);
+            else if (vec) conv_nchw_fused_kernel<true, false><<<grid, 256, lds, s>>>(a);
+            else conv_nchw_fused_kernel<false, false><<<grid, 256, lds, s>>>(a);
+            return launch_status();
+        }
+    }
+    note_route("conv-nchw-per-image");
     auto up = [](size_t b) { return (b + 255) & ~static_cast<size_t>(255); };
     char* ws = static_cast<char*>(workspace);
     uint16_t* col16 = reinterpret_cast<uint16_t*>(ws);
     int8_t* col8 = reinterpret_cast<int8_t*>(ws + up(static_cast<size_t>(M) * K * 2));
     float* as = reinterpret_cast<float*>(reinterpret_cast<char*>(col8) + up(static_cast<size_t>(M) * K));
     uint16_t* gout = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(as) + up(static_cast<size_t>(M) * 4));
-    hipStream_t s = as_stream(stream);
     const long long total = static_cast<long long>(M) * K;
     const int blocks = static_cast<int>(std::min<long long>(divupll(total, 256), 16384));
     const dim3 tgrid(divup(M, 32), divup(C_out, 32));

@@ -323,7 +323,8 @@ def int8_conv2d_workspace_size(C_in, H, W, C_out, kH, kW, padH, padW, strideH, s
 
 def int8_conv2d_forward(input: torch.Tensor, weight: torch.Tensor, w_scale: torch.Tensor,
                         bias: Optional[torch.Tensor], kH: int, kW: int, pad=(0, 0), stride=(1, 1), dil=(1, 1),
-                        workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                        workspace: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """int8_conv2d.cuh:33-53; `out` may be passed to reuse an (N, C_out, H_out, W_out) FP16 buffer."""
     N, C, H, W = input.shape
     Co = weight.shape[0]
     _need(input, torch.float16, "input")
@@ -338,7 +339,9 @@ def int8_conv2d_forward(input: torch.Tensor, weight: torch.Tensor, w_scale: torc
         workspace = torch.empty((nbytes,), dtype=torch.uint8, device=input.device)
     if workspace.numel() * workspace.element_size() < nbytes:
         raise ValueError(f"workspace needs {nbytes} bytes")
-    out = torch.empty((N, Co, Ho, Wo), dtype=torch.float16, device=input.device)
+    if out is None:
+        out = torch.empty((N, Co, Ho, Wo), dtype=torch.float16, device=input.device)
+    _need(out, torch.float16, "out", N * Co * Ho * Wo)
     _call("forge_int8_conv2d_forward", _p(input), _p(weight), _p(w_scale), _p(bias), _p(out), N, C, H, W, Co, kH, kW,
           pad[0], pad[1], stride[0], stride[1], dil[0], dil[1], _p(workspace), _stream())
     return out

@@ -141,3 +141,96 @@ def test_conv_nchw_api(dev, orc, C, H, W, Co, k, pad, stride, dil, bias):
             fref += b.astype(np.float64)
         err = np.abs(y[n].reshape(Co, -1).T.astype(np.float64) - fref)
         assert err.max() < 0.5 and err.mean() < 0.1
+
+
+# The one-launch NCHW path (K % 16 == 0): 64-pixel tiles of one output row (partial column
+# tiles at Wo = 70), several output rows per tile when Wo < 64 (stride 2: Wo = 10, 6 rows),
+# two and more 32-channel blocks (Co = 48: partial), a 5x5 dilated kernel (K = 800), K % 32 ==
+# 16 (C = 48, 3x3: the last 32-deep step half past K), pointwise 1x1, three images. Every output
+# against the reference pipeline's composition on the oracle.
+FUSED_CASES = [(32, 64, 64, 32, 3, 1, 1, 1, True), (32, 45, 70, 48, 3, 1, 1, 1, True),
+               (16, 20, 20, 24, 3, 1, 2, 1, False), (32, 24, 40, 16, 5, 4, 1, 2, True),
+               (48, 17, 33, 16, 3, 1, 1, 1, True), (64, 33, 33, 128, 1, 0, 1, 1, True)]
+
+
+@pytest.mark.parametrize("C,H,W,Co,k,pad,stride,dil,bias", FUSED_CASES)
+def test_conv_nchw_fused(dev, orc, C, H, W, Co, k, pad, stride, dil, bias):
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(C * W + Co + k)
+    N = 3
+    x = rng.uniform(-1, 1, (N, C, H, W)).astype(np.float16)
+    w = int8_uniform(rng, (Co, C * k * k))
+    ws = rng.uniform(0.005, 0.05, Co).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, Co).astype(np.float16) if bias else None
+    say(f"conv nchw fused C={C} H={H} W={W} Co={Co} k={k} s={stride} d={dil}")
+    Ho = (H + 2 * pad - dil * (k - 1) - 1) // stride + 1
+    Wo = (W + 2 * pad - dil * (k - 1) - 1) // stride + 1
+    out = torch.empty((N, Co, Ho, Wo), dtype=torch.float16, device=dev)
+    poison(out, 0x7B)
+    y = to_host(ops.int8_conv2d_forward(to_dev(x, dev), to_dev(w, dev), to_dev(ws, dev),
+                                        None if b is None else to_dev(b, dev), k, k, (pad, pad), (stride, stride),
+                                        (dil, dil), out=out))
+    assert ops.last_route().startswith("conv-nchw-fused")
+    for n in range(N):
+        cols, Ho2, Wo2 = _im2col_nchw(x[n], k, k, (pad, pad), (stride, stride), (dil, dil))
+        assert (Ho2, Wo2) == (Ho, Wo)
+        q, s = orc.quantize_rows(cols)
+        ref = orc.gemm_dequant(q, w, s, ws, b)
+        got = y[n].reshape(Co, -1).T.copy().view(np.uint16)
+        bad = int((got != ref.view(np.uint16)).sum())
+        assert bad == 0, f"image {n}: {bad} of {got.size} outputs differ"
+
+
+# Shapes with more tiles than the persistent grid holds (each workgroup walks several tiles):
+# 16-byte window loads with the next tile's loads in flight, 16-byte loads without (a window of
+# more than 16 load rounds), and 2-byte loads (W % 8 != 0).
+PERSISTENT_CASES = [(4, 16, 256, 512, 16, "conv-nchw-fused prefetch"), (2, 128, 64, 256, 32, "conv-nchw-fused"),
+                    (3, 16, 200, 250, 24, "conv-nchw-fused")]
+
+
+@pytest.mark.parametrize("N,C,H,W,Co,route", PERSISTENT_CASES)
+def test_conv_nchw_fused_persistent(dev, orc, N, C, H, W, Co, route):
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(N * C + W)
+    x = rng.uniform(-1, 1, (N, C, H, W)).astype(np.float16)
+    w = int8_uniform(rng, (Co, C * 9))
+    ws = rng.uniform(0.005, 0.05, Co).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, Co).astype(np.float16)
+    say(f"conv nchw fused persistent N={N} C={C} H={H} W={W} Co={Co}")
+    out = torch.empty((N, Co, H, W), dtype=torch.float16, device=dev)
+    poison(out, 0x7B)
+    y = to_host(ops.int8_conv2d_forward(to_dev(x, dev), to_dev(w, dev), to_dev(ws, dev), to_dev(b, dev), 3, 3,
+                                        (1, 1), (1, 1), (1, 1), out=out))
+    assert ops.last_route() == route
+    for n in range(N):
+        cols, Ho, Wo = _im2col_nchw(x[n], 3, 3, (1, 1), (1, 1), (1, 1))
+        q, s = orc.quantize_rows(cols)
+        ref = orc.gemm_dequant(q, w, s, ws, b)
+        got = y[n].reshape(Co, -1).T.copy().view(np.uint16)
+        bad = int((got != ref.view(np.uint16)).sum())
+        assert bad == 0, f"image {n}: {bad} of {got.size} outputs differ"
+
+
+def test_conv_nchw_fused_special_values(dev, orc):
+    """Patches holding NaN, +-inf, subnormals and all-zero windows through the one-launch path:
+    the same bits as quantize_rows on the reference's im2col rows, then its GEMM epilogue."""
+    from forge_amd import ops
+    from helpers import special_fp16_rows
+    rng = np.random.default_rng(77)
+    N, C, H, W, Co = 2, 16, 12, 80, 32
+    x = special_fp16_rows(rng, N * C * H, W).reshape(N, C, H, W)
+    x[1, :, 4:7, 10:20] = 0
+    w = int8_uniform(rng, (Co, C * 9))
+    ws = rng.uniform(0.005, 0.05, Co).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, Co).astype(np.float16)
+    say("conv nchw fused special values")
+    y = to_host(ops.int8_conv2d_forward(to_dev(x, dev), to_dev(w, dev), to_dev(ws, dev), to_dev(b, dev), 3, 3,
+                                        (1, 1), (1, 1), (1, 1)))
+    assert ops.last_route().startswith("conv-nchw-fused")
+    for n in range(N):
+        cols, Ho, Wo = _im2col_nchw(x[n], 3, 3, (1, 1), (1, 1), (1, 1))
+        q, s = orc.quantize_rows(cols)
+        ref = orc.gemm_dequant(q, w, s, ws, b)
+        assert np.array_equal(y[n].reshape(Co, -1).T.copy().view(np.uint16), ref.view(np.uint16))
