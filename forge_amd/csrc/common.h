@@ -34,7 +34,7 @@ int default_cu_count();
 // tile/split appended when >= 0 / > 0), read back by forge_last_route.
 void note_route(const char* engine, int tile = -1, int split = 0);
 
-inline int divup(int a, int b) { return (a + b - 1) / b; }
+inline int divup(int a, int b) { return static_cast<int>((static_cast<long long>(a) + b - 1) / b); }
 inline long long divupll(long long a, long long b) { return (a + b - 1) / b; }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

@@ -19,12 +19,21 @@
 #include "forge/nn/int8_conv2d.h"
 
 #include <algorithm>
+#include <climits>
 #include <mutex>
 
 namespace forge_amd {
 
+// Output size (int8_conv2d.cu:29-31): (in + 2 pad - dil (k - 1) - 1) / stride + 1 with C's
+// truncating division, evaluated in 64 bits; 0 for a geometry no convolution has (kernel, stride
+// or dilation <= 0, negative padding), INT_MAX where the size passes the int range.
 static int conv_out(int in, int pad, int dil, int k, int stride) {
-    return (in + 2 * pad - dil * (k - 1) - 1) / stride + 1;
+    if (k <= 0 || stride <= 0 || dil <= 0 || pad < 0) return 0;
+    const long long o = (static_cast<long long>(in) + 2LL * pad - static_cast<long long>(dil) * (k - 1) - 1) / stride + 1;
+    return o > INT_MAX ? INT_MAX : static_cast<int>(o);
+}
+static bool conv_geom_ok(int kH, int kW, int padH, int padW, int strideH, int strideW, int dilH, int dilW) {
+    return kH > 0 && kW > 0 && strideH > 0 && strideW > 0 && dilH > 0 && dilW > 0 && padH >= 0 && padW >= 0;
 }
 
 static int conv_nhwc(const int8_t* x, const int8_t* w, const float* act_scale, const uint16_t* w_scale,
@@ -33,8 +42,7 @@ static int conv_nhwc(const int8_t* x, const int8_t* w, const float* act_scale, c
                      int dilW, hipStream_t s)
 {
     if (N <= 0 || C <= 0 || Co <= 0 || H <= 0 || W <= 0) return FORGE_OK;
-    if (!x || !w || (!out16 && !out32) || kH <= 0 || kW <= 0 || strideH <= 0 || strideW <= 0 ||
-        dilH <= 0 || dilW <= 0 || padH < 0 || padW < 0)
+    if (!x || !w || (!out16 && !out32) || !conv_geom_ok(kH, kW, padH, padW, strideH, strideW, dilH, dilW))
         return FORGE_EINVAL;
     if (out16 && (!act_scale || !w_scale)) return FORGE_EINVAL;
     const int Ho = conv_out(H, padH, dilH, kH, strideH), Wo = conv_out(W, padW, dilW, kW, strideW);
@@ -619,6 +627,7 @@ extern "C" size_t forge_int8_conv2d_workspace_size(int C_in, int H, int W, int C
                                                    int padH, int padW, int strideH, int strideW,
                                                    int dilH, int dilW)
 {
+    if (C_in <= 0 || C_out <= 0 || !conv_geom_ok(kH, kW, padH, padW, strideH, strideW, dilH, dilW)) return 0;
     const int Ho = conv_out(H, padH, dilH, kH, strideH), Wo = conv_out(W, padW, dilW, kW, strideW);
     if (Ho <= 0 || Wo <= 0) return 0;
     const size_t M = static_cast<size_t>(Ho) * Wo, K = static_cast<size_t>(C_in) * kH * kW;
@@ -635,8 +644,12 @@ extern "C" int forge_int8_conv2d_forward(const uint16_t* input, const int8_t* we
 {
     if (N <= 0 || C_in <= 0 || C_out <= 0) return FORGE_OK;
     if (!input || !weight || !w_scale || !output || !workspace) return FORGE_EINVAL;
+    if (!conv_geom_ok(kH, kW, padH, padW, strideH, strideW, dilH, dilW)) return FORGE_EINVAL;
     const int Ho = conv_out(H, padH, dilH, kH, strideH), Wo = conv_out(W, padW, dilW, kW, strideW);
     if (Ho <= 0 || Wo <= 0) return FORGE_OK;
+    if (static_cast<long long>(Ho) * Wo > INT_MAX || static_cast<long long>(C_in) * kH * kW > INT_MAX ||
+        static_cast<long long>(H) * W > INT_MAX)
+        return FORGE_EINVAL;
     const int M = Ho * Wo, K = C_in * kH * kW;
     hipStream_t s = as_stream(stream);
     {

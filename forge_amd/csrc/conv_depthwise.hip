@@ -25,6 +25,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <climits>
 
 namespace forge_amd {
 
@@ -32,8 +33,11 @@ constexpr int kDwTileH = 32, kDwTileW = 64, kDwPer = 8;
 constexpr int kDwMaxKH = 16, kDwMaxKW = 9;
 constexpr int kDwPitch = 72;   // halves per staged row (>= kDwTileW + kDwMaxKW - 1, 16-byte multiple)
 
+// Output size (int8_depthwise_conv2d.cu's formula, C's truncating division) in 64 bits, INT_MAX
+// where it passes the int range; the caller has checked k, stride, dil > 0 and pad >= 0.
 static int dw_out(int in, int pad, int dil, int k, int stride) {
-    return (in + 2 * pad - dil * (k - 1) - 1) / stride + 1;
+    const long long o = (static_cast<long long>(in) + 2LL * pad - static_cast<long long>(dil) * (k - 1) - 1) / stride + 1;
+    return o > INT_MAX ? INT_MAX : static_cast<int>(o);
 }
 
 template <bool MASK>
@@ -398,6 +402,7 @@ extern "C" int forge_int8_depthwise_conv2d_forward(const uint16_t* input, const 
     if (H <= 0 || W <= 0) return FORGE_OK;
     const int Ho = dw_out(H, padH, dilH, kH, strideH), Wo = dw_out(W, padW, dilW, kW, strideW);
     if (Ho <= 0 || Wo <= 0) return FORGE_OK;
+    if (static_cast<long long>(H) * W > INT_MAX || static_cast<long long>(Ho) * Wo > INT_MAX) return FORGE_EINVAL;
     const long long planes = static_cast<long long>(N) * C;
     hipStream_t s = as_stream(stream);
     const bool unit = strideH == 1 && strideW == 1 && dilH == 1 && dilW == 1;

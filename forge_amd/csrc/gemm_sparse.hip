@@ -32,6 +32,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <cmath>
 #include <type_traits>
 
 namespace forge_amd {
@@ -1103,9 +1104,10 @@ double sparse_plan_cost(int M, int K, int N, int split_k, bool have_ws, int tile
         for (int c = 0; c < ncand; c++) {
             const int sp = auto_split ? kAutoSplits[c] : split_k;
             if (auto_split && sp > 1 && sp > steps / 2) continue;
-            const long long waves = divupll(tiles * sp, cu);
+            // in double: a forced split times the tile count can pass 2^63 (exact below 2^53)
+            const double waves = std::ceil(static_cast<double>(tiles) * sp / cu);
             const int ks = divup(steps, sp);
-            double cost = static_cast<double>(waves) * (kA[t] * ks + kB[t]);
+            double cost = waves * (kA[t] * ks + kB[t]);
             if (sp > 1) cost += kC0 + (kC1 + kC2 * sp) * (static_cast<double>(M) * N * 1e-6);
             if (cost < best) { best = cost; best_t = t; best_s = sp; }
         }
