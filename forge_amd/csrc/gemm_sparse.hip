@@ -864,17 +864,21 @@ static int launch_sparse_dma(const int8_t* W, const int8_t* X, const uint32_t* m
 // own DMAs of it) and marks stage kt - 1's slot read by every wave, which then receives stage
 // kt + D - 1. Waves in a 2 x 2 grid own 64 weight rows x 32 tokens: 4 x 2 blocks of
 // v_smfmac_i32_16x16x128_i8 per stage.
-template <int D>
+// BNW = 64 (64 weight rows x 64 tokens, 13 KB stages): twice the tiles, and with a shallower
+// ring two or three workgroups per CU, for the shapes whose 128-row tiles leave CUs idle.
+template <int D, int BNW_ = 128>
 struct SpRingTile {
-    static constexpr int BNW = 128, BMT = 64;
-    static constexpr int kTN = 4, kTM = 2;
+    static constexpr int BNW = BNW_, BMT = 64;
+    static constexpr int kTN = BNW / 32, kTM = 2;
     static constexpr int kWBytes = BNW * 64, kXBytes = BMT * 128, kIBytes = BNW / 16 * 256;
     static constexpr int kSlotBytes = kWBytes + kXBytes + kIBytes;
     static constexpr int kLdsBytes = D * kSlotBytes;
     static constexpr int kWIns = kWBytes / 1024 / 4;    // 1 KB DMA instructions per wave per stage
     static constexpr int kXIns = kXBytes / 1024 / 4;
-    static constexpr int kVm = kWIns + kXIns + 1;       // + one half-wave index DMA
-    static_assert(kIBytes == 4 * 512, "each wave copies 512 bytes of index words per stage");
+    static constexpr int kVm = kWIns + kXIns + 1;       // + one partial-wave index DMA
+    static constexpr int kILanes = kIBytes / 4 / 16;    // lanes of a wave copying 16 index bytes each
+    static_assert(BNW == 64 || BNW == 128, "ring tile rows");
+    static_assert(kWIns >= 1 && kILanes >= 1 && kILanes <= 32, "ring stage split over 4 waves");
     static_assert(D >= 2 && (D - 2) * kVm < 64, "ring depth");
 
     v4i acc[kTN][kTM];
@@ -910,7 +914,7 @@ struct SpRingTile {
         }
         const int8_t* pi;
         {
-            const int s = wave * 32 + (lane & 31);        // 16-byte chunk of the stage's index area
+            const int s = wave * kILanes + (lane & (kILanes - 1));   // 16-byte chunk of the stage's index area
             int b = (n0 >> 4) + (s >> 4);
             b = b < (N >> 4) ? b : (N >> 4) - 1;
             pi = reinterpret_cast<const int8_t*>(meta + static_cast<size_t>(b) * cpr * 16) + 16 * (s & 15);
@@ -923,7 +927,7 @@ struct SpRingTile {
             for (int q = 0; q < kWIns; q++) dma16(pw[q] + st * 64, slot + (wave * kWIns + q) * 1024);
 #pragma unroll
             for (int q = 0; q < kXIns; q++) dma16(px[q] + st * 128, slot + kWBytes + (wave * kXIns + q) * 1024);
-            if (lane < 32) dma16(pi + st * 256, slot + kWBytes + kXBytes + wave * 512);
+            if (lane < kILanes) dma16(pi + st * 256, slot + kWBytes + kXBytes + wave * (16 * kILanes));
         };
         // Waits for this wave's DMAs of stage kt when `later` stages were issued after it.
         auto wait_stage = [&](int later) {
@@ -975,12 +979,12 @@ constexpr int kSpRingSlots = 8;
 
 // Lane l of block (i, j) holds outputs (m = 16 j + l % 16, n = 16 i + 4 (l / 16) + e): one
 // 8-byte FP16 or 16-byte INT32 store each (N % 16 == 0, so the 4 columns are in or out together).
-template <bool DEQUANT>
+template <bool DEQUANT, int BNW = 128, int D = kSpRingSlots>
 __global__ __launch_bounds__(256) void sparse_ring_kernel(const int8_t* __restrict__ W, const int8_t* __restrict__ X,
                                                           const uint32_t* __restrict__ meta, GemmEpilogue ep,
                                                           int tiles_n, int tiles_m, int K)
 {
-    using T = SpRingTile<kSpRingSlots>;
+    using T = SpRingTile<D, BNW>;
     extern __shared__ __align__(16) int8_t lds[];
     int tn, tm;
     tile_coords(blockIdx.x, tiles_n, tiles_m, tn, tm);
@@ -1017,19 +1021,20 @@ __global__ __launch_bounds__(256) void sparse_ring_kernel(const int8_t* __restri
     }
 }
 
-template <bool DEQUANT>
+template <bool DEQUANT, int BNW = 128, int D = kSpRingSlots>
 static int launch_sparse_ring(const int8_t* W, const int8_t* X, const uint32_t* meta, const GemmEpilogue& ep, int K,
                               hipStream_t s)
 {
-    using T = SpRingTile<kSpRingSlots>;
+    using T = SpRingTile<D, BNW>;
     constexpr int lds = T::kLdsBytes;
     const int tiles_n = divup(ep.N, T::BNW), tiles_m = divup(ep.M, T::BMT);
     const long long total = static_cast<long long>(tiles_n) * tiles_m;
     if (total > 0x7FFFFFFFLL) return FORGE_EINVAL;
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&sparse_ring_kernel<DEQUANT>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&sparse_ring_kernel<DEQUANT, BNW, D>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (attr != hipSuccess) return static_cast<int>(attr);
-    sparse_ring_kernel<DEQUANT><<<static_cast<unsigned>(total), 256, lds, s>>>(W, X, meta, ep, tiles_n, tiles_m, K);
+    sparse_ring_kernel<DEQUANT, BNW, D>
+        <<<static_cast<unsigned>(total), 256, lds, s>>>(W, X, meta, ep, tiles_n, tiles_m, K);
     return launch_status();
 }
 
@@ -1124,21 +1129,26 @@ static int cu_count_or_default() {
 }
 
 // Unsplit DMA engine choice (automatic plans, M > 64, K % 128 == 0): 256 weight rows x 256
-// tokens (sparse_dma32, M > 128), x 128 tokens (sparse_dma<128>), or the 128 x 64 ring engine
-// (sparse_ring). A tile wave costs stages x stage time + a fixed part (ring fill, epilogue),
-// with stage times measured on MI355X: the two 256-row engines stream about the same bytes per
-// CU per microsecond, so their stages cost in proportion to their bytes (52 KB: ~1.16 us; 36 KB:
-// ~0.80 us); a ring stage (18 KB) costs ~0.62 us. Measured: 1536x6144 at M = 1024 256x128
-// 15.6 us (256x256 20.0); 6144x1536 at M = 4096 256x128 43.0 us (256x256 55.7, ring 86.2);
-// 6144x1536 at M = 1024 ring 30.3 us (256x128 39.8); configs[2] on 256x256.
+// tokens (sparse_dma32, M > 128), x 128 tokens (sparse_dma<128>), or the 64 x 64 ring engine
+// (sparse_ring, 4 slots: three workgroups per CU). A tile wave costs stages x stage time + a
+// fixed part (ring fill, epilogue), with stage times measured on MI355X: the two 256-row
+// engines stream about the same bytes per CU per microsecond, so their stages cost in
+// proportion to their bytes (52 KB: ~1.16 us; 36 KB: ~0.80 us). The ring's tiles share CUs
+// (up to 3 at once), a stage costing ~0.30 us per round of up to 3 tiles plus ~0.10 us per tile
+// on the busiest CU. Measured: 1536x6144 at M = 1024 256x128 15.6 us (256x256 20.0);
+// 6144x1536 at M = 4096 256x128 43.0 us (256x256 55.7); at M = 1024 the 64-row ring 24.4 us
+// (128-row ring with 8 slots, one workgroup per CU: 30.4; 256x128 39.8); 5120x1280 at M = 1024
+// 21.6 us (26.7); 4096x1024 at M = 1024 15.3 us (22.3); configs[2] on 256x256.
 enum class SpEngine { k256x256, k256x128, kRing };
+constexpr int kSpRingRows = 64, kSpRingDepth = 4, kSpRingPerCu = 3;
 
 static SpEngine sparse_pick_engine(int M, int N, int K, int cu)
 {
     const double steps = static_cast<double>(divup(K, kSpStep));
-    const long long tn256 = divup(N, 256), tn128 = divup(N, 128);
+    const long long tn256 = divup(N, 256), tnr = divup(N, kSpRingRows);
     const double w128 = static_cast<double>(divupll(tn256 * divup(M, 128), cu));
-    const double wring = static_cast<double>(divupll(tn128 * divup(M, 64), cu));
+    const long long wr = divupll(tnr * divup(M, 64), cu);   // ring tiles on the busiest CU
+    const double ring = steps * (0.30 * static_cast<double>(divupll(wr, kSpRingPerCu)) + 0.10 * static_cast<double>(wr)) + 1.5;
     double best = w128 * (0.80 * steps + 3.0);
     SpEngine e = SpEngine::k256x128;
     if (M > 128) {
@@ -1146,7 +1156,7 @@ static SpEngine sparse_pick_engine(int M, int N, int K, int cu)
         const double t = w256 * (1.16 * steps + 4.0);
         if (t <= best) { best = t; e = SpEngine::k256x256; }
     }
-    if (wring * (0.62 * steps + 1.5) < best) e = SpEngine::kRing;
+    if (ring < best) e = SpEngine::kRing;
     return e;
 }
 
@@ -1210,13 +1220,13 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
         GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N, aligned(o, 16) ? 1 : 0};
         const SpEngine e = tile == FORGE_SPARSE_TILE_AUTO ? sparse_pick_engine(M, N, K, cu_count_or_default())
                                                           : SpEngine::k256x128;
-        note_route(e == SpEngine::k256x256 ? "dma256x256" : e == SpEngine::kRing ? "ring128x64" : "dma256x128");
+        note_route(e == SpEngine::k256x256 ? "dma256x256" : e == SpEngine::kRing ? "ring64x64" : "dma256x128");
         if (e == SpEngine::k256x256)
             return out16 ? launch_sparse_dma32<true>(W_comp, x, meta, ep, K, s)
                          : launch_sparse_dma32<false>(W_comp, x, meta, ep, K, s);
         if (e == SpEngine::kRing)
-            return out16 ? launch_sparse_ring<true>(W_comp, x, meta, ep, K, s)
-                         : launch_sparse_ring<false>(W_comp, x, meta, ep, K, s);
+            return out16 ? launch_sparse_ring<true, kSpRingRows, kSpRingDepth>(W_comp, x, meta, ep, K, s)
+                         : launch_sparse_ring<false, kSpRingRows, kSpRingDepth>(W_comp, x, meta, ep, K, s);
         return out16 ? launch_sparse_dma<128, true>(W_comp, x, meta, ep, K, s)
                      : launch_sparse_dma<128, false>(W_comp, x, meta, ep, K, s);
     }

@@ -173,21 +173,22 @@ def test_config3_full_size(dev, orc):
     assert bad == 0, f"{bad} of {C.size} outputs differ"
 
 
-# Automatic plans on each unsplit DMA engine, chosen by tile waves: the 128 x 64 ring engine
-# (narrow N or few token tiles with deep K: fewer stages than ring slots, more, partial last
-# token tile, partial last 16-row weight block), the 256 x 128 engine and the 256 x 256 one.
+# Plans on each unsplit DMA engine, chosen by tile waves (tile -1) or forced to the reference's
+# 256 x 128 tile (0): the 64 x 64 ring engine (narrow N or few token tiles with deep K: fewer
+# stages than the 3 the ring keeps in flight, more, partial last token tile, partial last 64-row
+# weight tile), the 256 x 128 engine and the 256 x 256 one. The INT32 call always plans itself.
 ENGINE_SHAPES = [
-    (200, 2048, 256),    # ring: 4 token tiles (last 8 rows), 2 weight tiles
-    (100, 384, 144),     # ring: 3 stages (< 7 in flight), weight tile of 144 rows (+16)
-    (1024, 6144, 1536),  # ring: the reference benchmark's narrow deep-K layer
-    (512, 128, 2048),    # 256 x 128 engine: one stage
-    (1024, 1536, 6144),  # 256 x 128 engine
-    (600, 4096, 4096),   # 256 x 256 engine (ragged token tile)
+    (200, 2048, 256, -1, "ring64x64"),     # 4 token tiles (last 8 rows), 4 weight tiles
+    (100, 256, 144, -1, "ring64x64"),      # 2 stages (< 3 in flight), last weight tile 16 of 64 rows
+    (1024, 6144, 1536, -1, "ring64x64"),   # the reference benchmark's narrow deep-K layer
+    (512, 128, 2048, 0, "dma256x128"),     # one stage
+    (1024, 1536, 6144, -1, "dma256x128"),
+    (4000, 4096, 4096, -1, "dma256x256"),  # ragged token tile
 ]
 
 
-@pytest.mark.parametrize("M,K,N", ENGINE_SHAPES)
-def test_sparse_auto_engines(dev, orc, M, K, N):
+@pytest.mark.parametrize("M,K,N,tile,engine", ENGINE_SHAPES)
+def test_sparse_auto_engines(dev, orc, M, K, N, tile, engine):
     import torch
     from forge_amd import ops
     rng = np.random.default_rng(M + 3 * K + 7 * N)
@@ -212,7 +213,9 @@ def test_sparse_auto_engines(dev, orc, M, K, N):
     assert np.array_equal(to_host(ops.sparse_int8_gemm_s32(comp, xd, meta, out=C))[rows], acc)
     Y = torch.empty((M, N), dtype=torch.float16, device=dev)
     poison(Y, 0x7B)
-    ops.sparse_int8_gemm(comp, xd, meta, to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev), split_k=0, out=Y)
+    ops.sparse_int8_gemm(comp, xd, meta, to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev), split_k=0, tile=tile,
+                         out=Y)
+    assert ops.last_route() == engine
     ref = orc.dequant_epilogue(acc, act[rows], ws, b).view(np.uint16)
     assert np.array_equal(to_host(Y)[rows].view(np.uint16), ref)
 
