@@ -14,12 +14,12 @@
 // 64 MB weight matrix from HBM faster than staging it through LDS: coalesced register loads at
 // this shape reach ~6 TB/s in isolation, LDS DMA rings of any shape stay under 4.8 TB/s.
 //
-// Sparse, up to 8 tokens (decode_sparse_reg_kernel): the dense kernel's structure on 256-deep
+// Sparse with K % 256 == 0 (decode_sparse_reg_kernel): the dense kernel's structure on 256-deep
 // segments of compressed rows, with a K permutation that keeps the SMFMAC operands consistent
 // (described at the kernel). The same kernel serves 16 < M <= 64 tokens of the sparse GEMM with
 // TB = 2 or 4 token blocks per weight fragment (launch_skinny_tb).
 //
-// Sparse, 9-16 tokens (decode_sparse_kernel): a 512-thread workgroup owns 32 weight rows and all of K; its 8
+// Sparse with K % 256 == 128 (decode_sparse_kernel): a 512-thread workgroup owns 32 weight rows and all of K; its 8
 // wavefronts split K into 128-deep stages, each wave streaming its slice of the compressed
 // rows, index words and token rows through a PRIVATE LDS ring with global_load_lds_dwordx4,
 // so only the wave's own vmcnt orders the ring -- no barrier in the K loop (4 slots of
@@ -50,7 +50,7 @@ constexpr int kDecDenseWaves = 4;
 constexpr int kDecDenseWavesTwoBlock = 8;   // 8 tokens and more: measured 17.96 -> 17.47 us at M = 16
                                             // (graph-replayed int8_linear); 4 waves stay faster at M <= 4
 constexpr int kDecDenseAhead = 6;
-constexpr int kDecSparseRegMaxM = 8;   // register sparse kernel up to this many tokens
+constexpr int kDecSparseRegMaxM = 16;   // register sparse kernel up to this many tokens
 
 struct SparseDecodeCfg {
     // Per-wave ring slot: 32 rows x 64 compressed bytes, 2 x 64 index words, then the stage's
@@ -1074,20 +1074,18 @@ static int launch_decode_sparse_reg_kp(const int8_t* W, const uint32_t* meta, co
     return launch_status();
 }
 
-// K parts for the sparse register kernel (up to 8 tokens): as decode_dense_kparts, in whole
-// 256-deep segments, from K = 8192 on and with parts at least 2048 deep (a launch streams half
-// the dense bytes per K). Measured (M = 8 / 1, K = 8192): N = 4096 9.7 / 8.4 -> 8.2 / 7.7 us,
+// K parts for the sparse register kernel: as decode_dense_kparts, in whole 256-deep segments;
+// up to 8 tokens from K = 8192 on with parts at least 2048 deep (a launch streams half the dense
+// bytes per K), 9-16 tokens (twice the token bytes per weight byte) from K = 6144 on with parts
+// at least 1536 deep. Measured (M = 8 / 1, K = 8192): N = 4096 9.7 / 8.4 -> 8.2 / 7.7 us,
 // N = 1024 9.5 / 8.1 -> 6.3 / 5.8 us; at K = 4096 splits moved times by -0.45 to +0.4 us.
-constexpr int kKSplitMinKSparse = 8192;
-constexpr int kKSplitMinPartKSparse = 2048;
-
-static int decode_sparse_kparts(int N, int K, int rb, int cu)
+static int decode_sparse_kparts(int N, int K, int rb, int cu, int M)
 {
+    const int min_k = M > 8 ? 6144 : 8192, min_part = M > 8 ? 1536 : 2048;
     const int g = divup(N, 16 * rb);
-    if (K < kKSplitMinKSparse || g * rb > kKSplitMaxBlocks) return 1;
+    if (K < min_k || g * rb > kKSplitMaxBlocks) return 1;
     int kp = 1;
-    while (kp < kKSplitMaxParts && 2 * g * kp * 4 <= 5 * cu && K % (512 * kp) == 0 &&
-           K / (2 * kp) >= kKSplitMinPartKSparse)
+    while (kp < kKSplitMaxParts && 2 * g * kp * 4 <= 5 * cu && K % (512 * kp) == 0 && K / (2 * kp) >= min_part)
         kp *= 2;
     return kp;
 }
@@ -1101,7 +1099,7 @@ static int launch_decode_sparse_reg(const int8_t* W, const uint32_t* meta, const
         int st = FORGE_OK;
         const DeviceInfo& di = device_info(&st);
         if (st != FORGE_OK) return st;
-        kp = decode_sparse_kparts(ep.N, K, RB, di.cu_count);
+        kp = decode_sparse_kparts(ep.N, K, RB, di.cu_count, ep.M);
     }
     const KSplit ks = ksplit_take(s, kp);
     switch (kp) {
@@ -1258,7 +1256,7 @@ static int launch_decode_sparse_kp(const int8_t* W, const uint32_t* meta, const 
     return launch_status();
 }
 
-// K parts for the LDS-ring kernel (9-16 tokens, 32-row workgroups, 128-deep stages): as
+// K parts for the LDS-ring kernel (K % 256 == 128, 32-row workgroups, 128-deep stages): as
 // decode_dense_kparts from K = 6144 on, up to 4 parts of at least 1536. Measured (M = 16):
 // K = 8192 N = 4096 11.0 -> 9.6 us, N = 2048 10.1 -> 7.7 us, N = 1024 8.2 -> 6.2 us; K = 6144
 // N = 2048 8.7 -> 7.1 us.
@@ -1271,7 +1269,7 @@ static int decode_ring_kparts(int N, int K, int cu)
     return kp;
 }
 
-// 9-16 tokens: the LDS-ring kernel (kp = 0 chooses the K parts, otherwise 1, 2 or 4).
+// K % 256 == 128: the LDS-ring kernel (kp = 0 chooses the K parts, otherwise 1, 2 or 4).
 template <bool DEQUANT>
 static int launch_decode_sparse(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep,
                                 int K, hipStream_t s, int kp = 0)
@@ -1464,7 +1462,7 @@ static int launch_decode_fq_vpr(const int8_t* W, const uint32_t* meta, const Gem
     int st = FORGE_OK;
     const DeviceInfo& di = device_info(&st);
     if (st != FORGE_OK) return st;
-    int kp = sparse ? decode_sparse_kparts(ep.N, K, 2, di.cu_count) : decode_dense_kparts(ep.N, K, 1, di.cu_count);
+    int kp = sparse ? decode_sparse_kparts(ep.N, K, 2, di.cu_count, ep.M) : decode_dense_kparts(ep.N, K, 1, di.cu_count);
     kp = kp < 4 ? kp : 4;
     const KSplit ks = ksplit_take(s, kp);
     switch (kp) {
@@ -1492,8 +1490,9 @@ int launch_decode(const int8_t* W, const uint32_t* meta, const int8_t* X, const 
                   bool sparse, hipStream_t s)
 {
     if (!decode_supported(ep.M, K)) return FORGE_EINVAL;
-    // Sparse: up to 8 tokens the register kernel is faster (its token loads are light); at
-    // 9-16 tokens the token stream equals the weight stream and the DMA ring is ahead.
+    // Sparse: the register kernel wherever K % 256 == 0 (measured with the weights rotated
+    // past the MALL, N = K = 8192: M = 16 13.6 -> 12.0 us, M = 9 12.6 -> 10.6 us against the
+    // DMA ring, whose LDS-DMA stream tops out lower); the ring takes K % 256 == 128.
     if (sparse && K % 256 == 0 && ep.M <= kDecSparseRegMaxM)
         return ep.c16 ? launch_decode_sparse_reg<true, 2, 4, 4>(W, meta, X, ep, K, s)
                       : launch_decode_sparse_reg<false, 2, 4, 4>(W, meta, X, ep, K, s);

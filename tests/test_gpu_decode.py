@@ -5,7 +5,7 @@ dense and 2:4 sparse, against the oracle; and 16 < M <= 64 on the same kernels w
 Bar: INT32 bit-exact; FP16 bit-exact to the oracle's epilogue. Shapes exercise the kernel's
 K split over 8 wavefronts (K = 128: one wave works; K = 1152: 9 stages, uneven slices and
 idle waves), ragged N (not a multiple of the 32-row workgroup tile), M from 1 to 16 (the
-sparse register kernel for M <= 8 with K % 256 == 0, the DMA-ring kernel otherwise), and
+sparse register kernel with K % 256 == 0, the DMA-ring kernel otherwise), and
 configs[3] at full size (M = 16, 4 and 1, N = K = 8192; every output column); narrow N with K
 split across workgroups (exact INT32 hand-off), repeated and on two streams at once."""
 import numpy as np
@@ -16,9 +16,10 @@ from helpers import fp16_normal, int8_uniform, poison, say, to_dev, to_host
 pytestmark = pytest.mark.gpu
 
 DENSE = [(1, 128, 32), (3, 1152, 96), (16, 2048, 50), (7, 4096, 200), (16, 1024, 8)]
-# K % 256 == 0 with M <= 8 runs the register kernel; the rest run the DMA-ring kernel.
+# K % 256 == 0 runs the register kernel; K % 256 == 128 the DMA-ring kernel.
 SPARSE = [(1, 128, 32), (5, 1152, 48), (16, 2048, 208), (9, 4096, 1024), (16, 1024, 16),
-          (1, 256, 32), (5, 1280, 48), (8, 2048, 208), (3, 768, 16), (4, 8192, 1024)]
+          (1, 256, 32), (5, 1280, 48), (8, 2048, 208), (3, 768, 16), (4, 8192, 1024),
+          (12, 1152, 48), (16, 640, 64), (13, 256, 80)]
 
 
 @pytest.mark.parametrize("M,K,N", DENSE)
