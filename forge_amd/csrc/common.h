@@ -175,6 +175,15 @@ __device__ __forceinline__ uint16_t dequant_gemm(int acc, float as, float ws, fl
     return f2h(has_bias ? __builtin_fmaf(a, s, b) : a * s);
 }
 
+// n / d for 0 <= n with n * d < 2^32, with m = ceil(2^32 / d) (m = 0 stands for d = 1): n m / 2^32
+// exceeds n / d by n (m d - 2^32) / (d 2^32) < 1 / d, which cannot carry it past the next integer.
+__device__ __forceinline__ int udiv_magic(int n, uint32_t m) {
+    return m ? static_cast<int>(__umulhi(static_cast<uint32_t>(n), m)) : n;
+}
+inline uint32_t udiv_multiplier(int d) {
+    return d == 1 ? 0u : static_cast<uint32_t>(((1ULL << 32) + d - 1) / d);
+}
+
 // Workgroup id -> logical tile id such that each of the 8 XCDs (which receive workgroups
 // round-robin by id) runs one contiguous range of tiles: neighbouring tiles, which share
 // halo lines, then meet in the same L2. A bijection on [0, total) for any total.

@@ -138,15 +138,6 @@ struct ConvNchwArgs {
 
 constexpr int kCnPix = 64;     // output pixels per workgroup tile
 
-// n / d for n * d < 2^32, with m = ceil(2^32 / d) (m = 0 stands for d = 1): n m / 2^32 exceeds
-// n / d by n (m d - 2^32) / (d 2^32) < 1 / d, which cannot carry it past the next integer.
-__device__ __forceinline__ int udiv_magic(int n, uint32_t m) {
-    return m ? static_cast<int>(__umulhi(static_cast<uint32_t>(n), m)) : n;
-}
-static uint32_t udiv_multiplier(int d) {
-    return d == 1 ? 0u : static_cast<uint32_t>(((1ULL << 32) + d - 1) / d);
-}
-
 // One value of a quantized row as qrow_bits computes it, with the fp16 widening and the product
 // in one v_fma_mix_f32 (f16 source in the low half, fp32 inv, + 0): fma(a, b, 0) rounds a b once
 // as the multiply does (only a zero's sign can differ, and the + 1.5 2^23 erases it).

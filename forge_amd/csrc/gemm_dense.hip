@@ -56,6 +56,30 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_dma_kernel(
     store_tile<BM, BN, DEQUANT>(t.acc, ep, m0, n0, lds);
 }
 
+// The tail split in one launch: workgroups [0, n1) run the 256-row tiles of the first rows
+// (opa, ep), the rest the 192-row tiles of the remaining rows (opa2, ep2). Workgroups start in
+// index order, so each CU takes a 192-row tile as soon as its 256-row tile ends, while other CUs
+// still run their epilogues -- no launch boundary between the two tile sizes.
+template <bool DEQUANT, class OpA>
+__global__ __launch_bounds__(kGemmThreads) void gemm_dma_tail_kernel(
+    OpA opa, OpA opa2, DmaRowMajor opb, GemmEpilogue ep, GemmEpilogue ep2, int n1, int tiles_m1, int tiles_m2,
+    int tiles_n, int K)
+{
+    extern __shared__ __align__(16) int8_t lds[];
+    int tm, tn;
+    if (static_cast<int>(blockIdx.x) < n1) {
+        tile_coords(blockIdx.x, tiles_m1, tiles_n, tm, tn);
+        DmaTile<256, 256> t;
+        t.run(opa, opb, K, tm * 256, tn * 256, lds);
+        store_tile<256, 256, DEQUANT>(t.acc, ep, tm * 256, tn * 256, lds);
+    } else {
+        tile_coords(blockIdx.x - n1, tiles_m2, tiles_n, tm, tn);
+        DmaTile<192, 256> t;
+        t.run(opa2, opb, K, tm * 192, tn * 256, lds);
+        store_tile<192, 256, DEQUANT>(t.acc, ep2, tm * 192, tn * 256, lds);
+    }
+}
+
 // Raises a kernel's dynamic-LDS limit once (host-side attribute; safe under graph capture).
 template <class Kern>
 static int allow_lds(Kern kern, int bytes) {
@@ -143,15 +167,26 @@ static int launch_dma_tail_split(const OpA& opa, const DmaRowMajor& opb, const G
     const long long m1 = (waves - 1) * cu * 256;
     if (4 * last >= 3LL * cu || m1 >= M || divup(M - static_cast<int>(m1), 192) > cu) return -1;
     const int M1 = static_cast<int>(m1), M2 = M - M1;
-    int st = launch_dma<256, 256, DEQUANT>(opa, opb, ep, M1, N, K, s);
-    if (st != FORGE_OK) return st;
-    GemmEpilogue ep2 = ep;
+    GemmEpilogue ep1 = ep, ep2 = ep;
+    ep1.M = M1;
     ep2.M = M2;
     if (ep.c16) ep2.c16 = ep.c16 + static_cast<size_t>(M1) * N;
     if (ep.c32) ep2.c32 = ep.c32 + static_cast<size_t>(M1) * N;
     if (ep.act_scale) ep2.act_scale = ep.act_scale + M1;
     // 16-byte row stores stay aligned: M1 * N * elem is a multiple of 256 * 16.
-    return launch_dma<192, 256, DEQUANT>(rows_from(opa, M1), opb, ep2, M2, N, K, s);
+    constexpr int l1 = tile_lds_bytes<DmaTile<256, 256>, 256, 256, DEQUANT>();
+    constexpr int l2 = tile_lds_bytes<DmaTile<192, 256>, 192, 256, DEQUANT>();
+    constexpr int lds = l1 > l2 ? l1 : l2;
+    const int tiles_n = divup(N, 256), tiles_m1 = M1 / 256, tiles_m2 = divup(M2, 192);
+    const long long n1 = static_cast<long long>(tiles_m1) * tiles_n;
+    const long long total = n1 + static_cast<long long>(tiles_m2) * tiles_n;
+    if (total > 0x7FFFFFFFLL) return FORGE_EINVAL;
+    auto kern = gemm_dma_tail_kernel<DEQUANT, OpA>;
+    static const int attr = allow_lds(kern, lds);
+    if (attr != FORGE_OK) return attr;
+    gemm_dma_tail_kernel<DEQUANT, OpA><<<static_cast<unsigned>(total), kGemmThreads, lds, s>>>(
+        opa, rows_from(opa, M1), opb, ep1, ep2, static_cast<int>(n1), tiles_m1, tiles_m2, tiles_n, K);
+    return launch_status();
 }
 
 template <class OpA>
@@ -210,10 +245,17 @@ int launch_conv_gemm(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep,
                      hipStream_t s)
 {
     const int M = g.rows, K = g.K;
-    // DMA engine when every 128-deep stage of a patch row is one pixel's contiguous channels.
-    if (vec && g.C % kBK == 0 && aligned(w, 16)) {
+    // DMA engine when every 128-deep stage of a patch row is one pixel's contiguous channels
+    // (and the image fits one buffer resource, the taps one 32-bit mask).
+    const long long img_bytes = static_cast<long long>(g.rows / (g.Ho * g.Wo)) * g.H * g.W * g.C;
+    const int taps = g.K / g.C;
+    if (vec && g.C % kBK == 0 && aligned(w, 16) && img_bytes < (1LL << 31) && taps <= 32) {
         DmaConv a;
         static_cast<ConvGeom&>(a) = g;
+        a.x_bytes = static_cast<uint32_t>(img_bytes);
+        a.cps = g.C / kBK;
+        a.mg_cps = udiv_multiplier(a.cps);
+        a.mg_kw = udiv_multiplier(g.kW);
         const int r = dispatch_dma(a, DmaRowMajor{w, Co, K}, ep, M, Co, K, s);
         if (r != -1) return r;
     }

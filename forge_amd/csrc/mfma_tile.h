@@ -343,19 +343,25 @@ struct DmaRowMajor {
         return p + static_cast<size_t>(r < rows ? r : rows - 1) * K + 16 * c;
     }
     __device__ __forceinline__ const int8_t* src(const Lane& l, int st) const { return l + st * kBK; }
+    using Stage = int;
+    __device__ __forceinline__ Stage stage(int st) const { return st; }
+    __device__ __forceinline__ void dma(const Lane& l, Stage st, int8_t* dst) const { dma16(src(l, st), dst); }
 };
 
-// 128 zero bytes: the DMA source for im2col taps that fall in the padding.
-__device__ __align__(128) const int8_t g_dma_zero_line[128] = {};
-
 // Implicit im2col of an NHWC image, K order (kh, kw, c): with C % 128 == 0 a 128-deep stage of a
-// patch row is one contiguous run of one input pixel's channels, or padding (read from the zero
-// line). Needs a 16-byte aligned image.
+// patch row is one contiguous run of one input pixel's channels, or padding. The image is one
+// buffer resource (x_bytes < 2^31, set by the host with the magic multipliers), and a stage's
+// DMA is a buffer load at a 32-bit offset: the row's pixel offset (fixed per lane) plus the
+// stage's tap offset (uniform: (kh dilH W + kw dilW) C + c0). A row keeps a bit per tap saying
+// whether that tap lies inside the image; a padding tap gets an offset past the range, which
+// the hardware reads as zeros. Needs a 16-byte aligned image and kH kW <= 32.
 struct DmaConv : ConvGeom {
+    uint32_t x_bytes;            // bytes of the whole NHWC input
+    int cps;                     // 128-deep stages per tap (C / 128)
+    uint32_t mg_cps, mg_kw;      // udiv_magic multipliers for / cps and / kW
     struct Lane {
-        const int8_t* img;   // this patch row's image
-        int hb, wb;          // top-left input coordinate of the patch
-        int c16;             // 16 * chunk
+        int off;                 // byte offset of pixel (n, hb, wb) + 16 * chunk (may be negative)
+        uint32_t taps;           // bit kh kW + kw: tap inside the image
     };
     __device__ __forceinline__ Lane lane(int r, int c) const {
         r += r0;
@@ -364,15 +370,28 @@ struct DmaConv : ConvGeom {
         const int t = r / Wo;
         const int ho = t % Ho;
         const int n = t / Ho;
-        return Lane{x + static_cast<size_t>(n) * H * W * C, ho * strideH - padH, wo * strideW - padW, 16 * c};
+        const int hb = ho * strideH - padH, wb = wo * strideW - padW;
+        const int kH = K / (C * kW);
+        uint32_t taps = 0u;
+        for (int kh = 0; kh < kH; kh++)
+            for (int kw = 0; kw < kW; kw++) {
+                const int hi = hb + kh * dilH, wi = wb + kw * dilW;
+                if (hi >= 0 && hi < H && wi >= 0 && wi < W) taps |= 1u << (kh * kW + kw);
+            }
+        return Lane{((n * H + hb) * W + wb) * C + 16 * c, taps};
     }
-    __device__ __forceinline__ const int8_t* src(const Lane& l, int st) const {
-        const int cps = C / kBK;                    // stages per tap (wave-uniform)
-        const int tap = st / cps, c0 = (st - tap * cps) * kBK;
-        const int kh = tap / kW, kw = tap - kh * kW;
-        const int hi = l.hb + kh * dilH, wi = l.wb + kw * dilW;
-        const bool ok = hi >= 0 && hi < H && wi >= 0 && wi < W;
-        return ok ? l.img + (static_cast<size_t>(hi) * W + wi) * C + c0 + l.c16 : g_dma_zero_line + l.c16;
+    struct Stage {
+        int soff;                // (kh dilH W + kw dilW) C + c0
+        int tap;                 // kh kW + kw
+    };
+    __device__ __forceinline__ Stage stage(int st) const {
+        const int tap = udiv_magic(st, mg_cps), c0 = (st - tap * cps) * kBK;
+        const int kh = udiv_magic(tap, mg_kw), kw = tap - kh * kW;
+        return Stage{(kh * dilH * W + kw * dilW) * C + c0, tap};
+    }
+    __device__ __forceinline__ void dma(const Lane& l, const Stage& S, int8_t* dst) const {
+        const uint32_t voff = (l.taps >> S.tap) & 1u ? static_cast<uint32_t>(l.off + S.soff) : 0x80000000u;
+        dma16_buf(buf_rsrc(x, x_bytes), voff, 0, dst);
     }
 };
 
@@ -433,10 +452,12 @@ struct DmaTile {
         auto issue = [&](int st) {
             int8_t* slot = lds + (st & 1) * kSlotBytes;
             const int sc = st < nst ? st : nst - 1;
+            const typename OpA::Stage sa = opa.stage(sc);
+            const typename OpB::Stage sb = opb.stage(sc);
 #pragma unroll
-            for (int q = 0; q < kAIns; q++) dma16(opa.src(la[q], sc), slot + (wave * kAIns + q) * 1024);
+            for (int q = 0; q < kAIns; q++) opa.dma(la[q], sa, slot + (wave * kAIns + q) * 1024);
 #pragma unroll
-            for (int q = 0; q < kBIns; q++) dma16(opb.src(lb[q], sc), slot + BM * kBK + (wave * kBIns + q) * 1024);
+            for (int q = 0; q < kBIns; q++) opb.dma(lb[q], sb, slot + BM * kBK + (wave * kBIns + q) * 1024);
         };
         auto load_frags = [&](int st, int ks, Frags& F) {
             const int8_t* As = lds + (st & 1) * kSlotBytes;
