@@ -196,6 +196,8 @@ static int dispatch_dma(const OpA& opa, const DmaRowMajor& opb, const GemmEpilog
     int st = FORGE_OK;
     const int cu = cu_count(&st);
     if (st != FORGE_OK) return st;
+    // both operands as buffer resources with 32-bit offsets
+    if (static_cast<long long>(opb.rows) * K >= (1LL << 31) || static_cast<long long>(M) * K >= (1LL << 31)) return -1;
     const TileCfg t = pick_tile(M, N, cu);
     const bool out16 = ep.c16 != nullptr;
     if (t == TileCfg::k256) {

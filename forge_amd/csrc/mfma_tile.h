@@ -18,8 +18,9 @@
 // Two K-loop engines share that layout and the epilogue:
 //
 // DmaTile (K % 128 == 0, 16-byte aligned row-major operands; the hot path): 128-byte K
-// stages in two LDS slots, filled by gfx950's global_load_lds_dwordx4 (each lane's 16
-// bytes land at M0 + 16*lane, no VGPR staging). Every row of a stage is one full 128-byte
+// stages in two LDS slots, filled by gfx950's LDS-DMA loads (buffer_load_dwordx4 ... lds
+// through a buffer resource per operand: each lane's 16 bytes land at M0 + 16*lane, no VGPR
+// staging, 32-bit offsets, the stage's K offset in the scalar offset). Every row of a stage is one full 128-byte
 // cache line read by 8 consecutive lanes; on gfx950 this sustains ~30 B/clk per CU into
 // LDS, against ~26 B/clk for 64-byte half-line rows, whatever the number of stages in
 // flight. Stage kt+1 streams in while stage kt is multiplied; MFMA fragments are read two
@@ -335,17 +336,21 @@ __device__ __forceinline__ void wait_vm_lgkm0() { __builtin_amdgcn_s_waitcnt(0x7
 // stage st. lane() runs once per DMA instruction; src() once per stage.
 
 // Row-major (rows, K) matrix, K % 128 == 0; rows past the end are clamped (never stored).
+// A row-major INT8 matrix as one buffer resource (rows * K < 2^31, checked by the host): a lane's
+// chunk offset is fixed, the stage's K offset is the uniform scalar offset of the buffer load,
+// so a stage's DMAs need no per-lane address arithmetic.
 struct DmaRowMajor {
     const int8_t* p;
     int rows, K;
-    using Lane = const int8_t*;
+    using Lane = uint32_t;
     __device__ __forceinline__ Lane lane(int r, int c) const {
-        return p + static_cast<size_t>(r < rows ? r : rows - 1) * K + 16 * c;
+        return static_cast<uint32_t>(r < rows ? r : rows - 1) * static_cast<uint32_t>(K) + 16u * c;
     }
-    __device__ __forceinline__ const int8_t* src(const Lane& l, int st) const { return l + st * kBK; }
-    using Stage = int;
-    __device__ __forceinline__ Stage stage(int st) const { return st; }
-    __device__ __forceinline__ void dma(const Lane& l, Stage st, int8_t* dst) const { dma16(src(l, st), dst); }
+    using Stage = uint32_t;
+    __device__ __forceinline__ Stage stage(int st) const { return static_cast<uint32_t>(st) * kBK; }
+    __device__ __forceinline__ void dma(const Lane& l, Stage soff, int8_t* dst) const {
+        dma16_buf(buf_rsrc(p, static_cast<uint32_t>(rows) * static_cast<uint32_t>(K)), l, soff, dst);
+    }
 };
 
 // Implicit im2col of an NHWC image, K order (kh, kw, c): with C % 128 == 0 a 128-deep stage of a
