@@ -84,7 +84,7 @@ def traffic_probe() -> int:
     PROBE_REPS times on its configs' shape with inputs resident on the device:
     c2 = the configs[1] dequant GEMM (4096^3, FP16 out); c3 sparse / dense = configs[2]
     (4096 x 11008 x 4096, INT32 out) on the 2:4 and the dense engine; c5 = configs[4] NHWC
-    conv (INT32 out; a 256-row and a 192-row tail launch); c4 = configs[3] M = 16 decode GEMMs
+    conv (INT32 out; 256-row and 192-row tiles in one launch); c4 = configs[3] M = 16 decode GEMMs
     (N = K = 8192, pre-quantized tokens, FP16 out) dense and 2:4; then a COPY_PROBE_BYTES
     device-to-device copy, the calibration of known size for FETCH_SIZE / WRITE_SIZE."""
     import torch
@@ -163,12 +163,11 @@ def _prep_sparse(ops, W):
 PROBE_KERNELS = {
     # probe: (kernel-name substrings, any of which marks a dispatch of the probe)
     "c2_gemm": ("gemm_dma_kernel<256, 256, true, forge_amd::DmaRowMajor>",),
-    "c3_sparse": ("sparse_dma32_kernel<false>",),
+    "c3_sparse": ("sparse_dma32_kernel<false,",),
     "c3_dense": ("gemm_dma_kernel<256, 256, false, forge_amd::DmaRowMajor>",),
-    "c5_conv": ("gemm_dma_kernel<256, 256, false, forge_amd::DmaConv>",
-                "gemm_dma_kernel<192, 256, false, forge_amd::DmaConv>"),
+    "c5_conv": ("gemm_dma_tail_kernel<false, forge_amd::DmaConv>",),
     "c4_dense_M16": ("decode_dense_kernel<true",),
-    "c4_sparse_M16": ("decode_sparse_kernel<true",),
+    "c4_sparse_M16": ("decode_sparse_reg_kernel<true",),
     "copy": ("copyBuffer",),
 }
 _C4_TOK = 16 * 8192
@@ -190,7 +189,7 @@ XCDS = 8
 def counter_summary(outdir: str) -> int:
     """Reads the rocprofv3 --pmc CSVs of --traffic-probe runs under outdir (one subdirectory per
     counter set) and writes profiles/kernel_counters.json: per probe, medians over its dispatches
-    (a probe with two kernels per call, the conv, sums them per call)."""
+    (one kernel per call)."""
     import csv
     import glob
     import statistics
@@ -215,17 +214,9 @@ def counter_summary(outdir: str) -> int:
                 d = per_dispatch.setdefault(int(r["Dispatch_Id"]), {"probe": probe, "c": {}})
                 d["c"][r["Counter_Name"]] = float(r["Counter_Value"])
                 d["t"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3
-        # consecutive dispatches of a two-kernel probe form one call
-        calls = []
-        for did in sorted(per_dispatch):
-            d = per_dispatch[did]
-            if calls and calls[-1]["probe"] == d["probe"] == "c5_conv" and calls[-1]["n"] == 1:
-                for k, v in d["c"].items():
-                    calls[-1]["c"][k] = calls[-1]["c"].get(k, 0.0) + v
-                calls[-1]["t"] += d["t"]
-                calls[-1]["n"] = 2
-            else:
-                calls.append({"probe": d["probe"], "c": dict(d["c"]), "t": d["t"], "n": 1})
+        # one dispatch per call for every probe
+        calls = [{"probe": d["probe"], "c": dict(d["c"]), "t": d["t"], "n": 1}
+                 for _, d in sorted(per_dispatch.items())]
         for c in calls:
             for k, v in c["c"].items():
                 rows.setdefault(c["probe"], {}).setdefault(k, []).append(v)
@@ -250,8 +241,7 @@ def counter_summary(outdir: str) -> int:
             # GRBM_GUI_ACTIVE is summed over the 8 XCDs and also counts a fixed per-dispatch
             # overhead (its smallest reading in the run, a 256-thread fill kernel's), taken off
             # once per kernel of the call.
-            n_k = 2 if p == "c5_conv" else 1
-            e["clock_ghz"] = (gui / XCDS - n_k * overhead) / (e["duration_us_in_counter_run"] * 1e3)
+            e["clock_ghz"] = (gui / XCDS - overhead) / (e["duration_us_in_counter_run"] * 1e3)
             e["peak_tops_at_clock"] = peak * e["clock_ghz"] / 2.4
         busy, cu_busy = c.get("SQ_VALU_MFMA_BUSY_CYCLES"), c.get("SQ_BUSY_CU_CYCLES")
         if busy is not None and cu_busy:
@@ -300,11 +290,11 @@ COUNTER_SETS = [
 ]
 PROBE_TITLES = {
     "c2_gemm": "configs[1] GEMM 4096^3, FP16 out (`gemm_dma_kernel<256,256,true>`)",
-    "c3_sparse": "configs[2] 2:4 sparse 4096x11008x4096, INT32 out (`sparse_dma32_kernel<false>`)",
+    "c3_sparse": "configs[2] 2:4 sparse 4096x11008x4096, INT32 out (`sparse_dma32_kernel<false,SpDmaTile32W>`)",
     "c3_dense": "configs[2] shape dense, INT32 out (`gemm_dma_kernel<256,256,false>`)",
-    "c5_conv": "configs[4] NHWC conv, INT32 out (`gemm_dma_kernel<256 and 192,256,false,DmaConv>`, 2 launches)",
+    "c5_conv": "configs[4] NHWC conv, INT32 out (`gemm_dma_tail_kernel<false,DmaConv>`: 256- and 192-row tiles, one launch)",
     "c4_dense_M16": "configs[3] M=16 dense decode GEMM (`decode_dense_kernel`)",
-    "c4_sparse_M16": "configs[3] M=16 2:4 decode GEMM (`decode_sparse_kernel`)",
+    "c4_sparse_M16": "configs[3] M=16 2:4 decode GEMM (`decode_sparse_reg_kernel`)",
 }
 
 

@@ -1305,15 +1305,15 @@ static int pad_stages(int per)
     return -1;
 }
 
-template <bool DEQUANT, int RB, int TB, int KP>
+template <bool DEQUANT, int RB, int TB, int KP, int WV = kDecDenseWaves>
 static int launch_tb_sparse(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep, int K,
                             const KSplit& ks, hipStream_t s)
 {
-    constexpr int WV = kDecDenseWaves, AH = kSkinnyTbAheadSparse;
+    constexpr int AH = kSkinnyTbAheadSparse;
     const dim3 grid(static_cast<unsigned>(divup(ep.N, 16 * RB)), KP);
     const int S = pad_stages(divup(K / KP / 256, WV));
-    // Largest padded per-wave segment count K <= kDecodeMaxK can need at this KP.
-    constexpr int SM = kDecodeMaxK / 256 / KP / WV;
+    // Largest per-wave segment count K <= kDecodeMaxK can need at this KP.
+    constexpr int SM = (kDecodeMaxK / 256 / KP + WV - 1) / WV;
 #define FORGE_TB_SPARSE(SS) \
     decode_sparse_reg_kernel<DEQUANT, (SS <= SM ? SS : SM), RB, WV, AH, TB, 0, KP><<<grid, WV * kWave, 0, s>>>(W, meta, X, ep, K, FqArgs{}, ks)
     switch (S) {
@@ -1368,14 +1368,25 @@ int launch_skinny_tb(const int8_t* W, const uint32_t* meta, const int8_t* X, con
 {
     if (!skinny_tb_supported(ep.M, K)) return FORGE_EINVAL;
     const bool tall = 2 * divup(ep.N, 32) >= cu;
+    // 8 waves (each fewer 256-deep segments) where K is short and N moderate; measured (us, 4 ->
+    // 8 waves): M = 64 1536x6144 7.0 -> 6.4, 1280x5120 7.0 -> 5.9, 4096x4096 13.0 -> 12.3;
+    // M = 32 1280x5120 4.75 -> 4.5; but 4096x11008 at M = 64 22.7 -> 23.2 and 8192x8192 at
+    // M = 32 14.8 -> 16.0.
+    const bool w8 = K <= 4096 && ep.N < 8192;
     const bool dq = ep.c16 != nullptr;
     if (ep.M <= 32) {
+        if (tall && w8)
+            return dq ? launch_tb_sparse<true, 2, 2, 1, 8>(W, meta, X, ep, K, KSplit{}, s)
+                      : launch_tb_sparse<false, 2, 2, 1, 8>(W, meta, X, ep, K, KSplit{}, s);
         if (tall)
             return dq ? launch_tb_sparse<true, 2, 2, 1>(W, meta, X, ep, K, KSplit{}, s)
                       : launch_tb_sparse<false, 2, 2, 1>(W, meta, X, ep, K, KSplit{}, s);
         return dq ? launch_tb_sparse_narrow<true, 2>(W, meta, X, ep, K, cu, s, kp)
                   : launch_tb_sparse_narrow<false, 2>(W, meta, X, ep, K, cu, s, kp);
     }
+    if (tall && w8)
+        return dq ? launch_tb_sparse<true, 2, 4, 1, 8>(W, meta, X, ep, K, KSplit{}, s)
+                  : launch_tb_sparse<false, 2, 4, 1, 8>(W, meta, X, ep, K, KSplit{}, s);
     if (tall)
         return dq ? launch_tb_sparse<true, 2, 4, 1>(W, meta, X, ep, K, KSplit{}, s)
                   : launch_tb_sparse<false, 2, 4, 1>(W, meta, X, ep, K, KSplit{}, s);

@@ -1156,7 +1156,10 @@ static SpEngine sparse_pick_engine(int M, int N, int K, int cu)
         const double t = w256 * (1.16 * steps + 4.0);
         if (t <= best) { best = t; e = SpEngine::k256x256; }
     }
-    if (ring < best) e = SpEngine::kRing;
+    // The ring's model is fitted where its tiles take at most one round of 3 per CU; beyond
+    // that the 256-row engines' reuse wins (measured: 640 x 320 at M = 147,456 on the ring
+    // 128 us against 80 us on 256 x 256).
+    if (wr <= kSpRingPerCu && ring < best) e = SpEngine::kRing;
     return e;
 }
 

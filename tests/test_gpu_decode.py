@@ -139,10 +139,12 @@ TB_DENSE = [(17, 128, 48), (32, 384, 200), (33, 640, 201), (48, 1152, 96), (64, 
             (20, 4096, 2047), (64, 8192, 4000), (48, 4352, 300)]
 # From K = 4096 on, narrow N (16-row workgroups fewer than the CUs) splits K over 2 or 4
 # workgroups per row block: (40, 5120, 64), (64, 8192, 32), (64, 6144, 1536), (64, 8192, 1024),
-# (30, 4096, 1008).
+# (30, 4096, 1008). 32-row workgroups (N >= 4096) run 8 waves for K <= 4096 and N < 8192
+# ((64, 1536, 4160), (25, 3072, 4112), (64, 256, 4096): 7 idle waves, (20, 4096, 4112)), else 4
+# ((64, 5120, 4096), (40, 1024, 8208)).
 TB_SPARSE = [(17, 256, 48), (32, 768, 208), (33, 1280, 16), (48, 2048, 96), (64, 1536, 4160),
              (40, 5120, 64), (64, 8192, 32), (25, 3072, 4112), (64, 6144, 1536), (64, 8192, 1024),
-             (30, 4096, 1008)]
+             (30, 4096, 1008), (64, 256, 4096), (20, 4096, 4112), (64, 5120, 4096), (40, 1024, 8208)]
 
 
 def _check_cols(N):
