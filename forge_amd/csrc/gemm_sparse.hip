@@ -272,6 +272,17 @@ __global__ __launch_bounds__(256) void splitk_reduce_f32_kernel(
 // the next stage's weights, indices and first-half tokens while the second half runs, on the
 // far side of the barrier that publishes the next stage.
 
+// The sparse GEMM operands as buffer resources: compressed weights (N x K/2 bytes), tokens
+// (M x K) and index words (N x K/8 bytes). The host keeps every size under 2^31.
+struct SpBufs {
+    __amdgpu_buffer_rsrc_t w, x, i;
+};
+__device__ __forceinline__ SpBufs sp_bufs(const int8_t* W, const int8_t* X, const uint32_t* meta, int M, int N, int K)
+{
+    const uint32_t n = static_cast<uint32_t>(N), m = static_cast<uint32_t>(M), k = static_cast<uint32_t>(K);
+    return SpBufs{buf_rsrc(W, n * (k / 2)), buf_rsrc(X, m * k), buf_rsrc(meta, n * (k / 8))};
+}
+
 template <int BMT>
 struct SpDmaTile {
     static constexpr int BNW = 256;
@@ -307,38 +318,40 @@ struct SpDmaTile {
 #pragma unroll
             for (int j = 0; j < kTM; j++) acc[i][j] = v4i{0, 0, 0, 0};
 
-        const int8_t* pw[kWIns];
-        const int8_t* px[kXIns];
+        // The three operands as buffer resources (sizes < 2^31, checked by the host): a lane's
+        // offsets are fixed, a stage's K offset is the scalar offset of its DMAs.
+        const SpBufs bf = sp_bufs(W, X, meta, M, N, K);
+        uint32_t ow[kWIns], ox[kXIns];
 #pragma unroll
         for (int q = 0; q < kWIns; q++) {
             const int s = (wave * kWIns + q) * kWave + lane;
             const int r = s >> 2, c = (s & 3) ^ lds_swz4(r);
             const int gr = (n0 + r) < N ? (n0 + r) : N - 1;
-            pw[q] = W + static_cast<size_t>(gr) * Kc + 16 * c;
+            ow[q] = static_cast<uint32_t>(gr) * Kc + 16 * c;
         }
 #pragma unroll
         for (int q = 0; q < kXIns; q++) {
             const int s = (wave * kXIns + q) * kWave + lane;
             const int r = s >> 3, c = (s & 7) ^ lds_swz8(r);
             const int gr = (m0 + r) < M ? (m0 + r) : M - 1;
-            px[q] = X + static_cast<size_t>(gr) * K + 16 * c;
+            ox[q] = static_cast<uint32_t>(gr) * K + 16 * c;
         }
-        const int8_t* pi;
+        uint32_t oi;
         {
             const int s = wave * kWave + lane;            // 16-byte chunk of the stage's index area
             int b = (n0 >> 4) + (s >> 4);
             b = b < (N >> 4) ? b : (N >> 4) - 1;
-            pi = reinterpret_cast<const int8_t*>(meta + static_cast<size_t>(b) * cpr * 16) + 16 * (s & 15);
+            oi = static_cast<uint32_t>(b) * cpr * 64 + 16 * (s & 15);
         }
         const int nst = K / 128;
         auto issue = [&](int st) {
             int8_t* slot = lds + (st & 1) * kSlotBytes;
-            const int sc = st < nst ? st : nst - 1;       // past the end: re-read (dead slot)
+            const uint32_t sc = st < nst ? st : nst - 1;  // past the end: re-read (dead slot)
 #pragma unroll
-            for (int q = 0; q < kWIns; q++) dma16(pw[q] + sc * 64, slot + (wave * kWIns + q) * 1024);
+            for (int q = 0; q < kWIns; q++) dma16_buf(bf.w, ow[q], sc * 64, slot + (wave * kWIns + q) * 1024);
 #pragma unroll
-            for (int q = 0; q < kXIns; q++) dma16(px[q] + sc * 128, slot + kWBytes + (wave * kXIns + q) * 1024);
-            dma16(pi + sc * 256, slot + kWBytes + kXBytes + wave * 1024);
+            for (int q = 0; q < kXIns; q++) dma16_buf(bf.x, ox[q], sc * 128, slot + kWBytes + (wave * kXIns + q) * 1024);
+            dma16_buf(bf.i, oi, sc * 256, slot + kWBytes + kXBytes + wave * 1024);
         };
         auto load_w = [&](int st, WFrag& F) {
             const int8_t* Ws = lds + (st & 1) * kSlotBytes;
@@ -452,43 +465,43 @@ struct SpDmaTile32 {
 #pragma unroll
                 for (int e = 0; e < 16; e++) acc[j][i][e] = 0;
 
-        const int8_t* pw[kWIns];
-        const int8_t* px[kXIns];
+        const SpBufs bf = sp_bufs(W, X, meta, M, N, K);
+        uint32_t ow[kWIns], ox[kXIns];
 #pragma unroll
         for (int q = 0; q < kWIns; q++) {
             const int s = (wave * kWIns + q) * kWave + lane;
             const int r = s >> 2, c = (s & 3) ^ lds_swz4(r);
             const int gr = (n0 + r) < N ? (n0 + r) : N - 1;
-            pw[q] = W + static_cast<size_t>(gr) * Kc + 16 * c;
+            ow[q] = static_cast<uint32_t>(gr) * Kc + 16 * c;
         }
 #pragma unroll
         for (int q = 0; q < kXIns; q++) {
             const int s = (wave * kXIns + q) * kWave + lane;
             const int r = s >> 3, c = (s & 7) ^ lds_swz8(r);
             const int gr = (m0 + r) < M ? (m0 + r) : M - 1;
-            px[q] = X + static_cast<size_t>(gr) * K + 16 * c;
+            ox[q] = static_cast<uint32_t>(gr) * K + 16 * c;
         }
         // Index words: LDS chunk position s (16 blocks x 16 chunks of 4 words) takes chunk
         // (s % 16) ^ 12 of its block in odd blocks (read below as word w ^ 48). The 16-lane
         // groups of an index read (block parity x g) then start at banks {0, 48, 16, 32}
         // (+32 for the odd step): distinct over all 64 lanes and within each 32-lane half.
-        const int8_t* pi;
+        uint32_t oi;
         {
             const int s = wave * kWave + lane;
             int b = (n0 >> 4) + (s >> 4);
             b = b < (N >> 4) ? b : (N >> 4) - 1;
             const int k = (s & 15) ^ (((s >> 4) & 1) * 12);
-            pi = reinterpret_cast<const int8_t*>(meta + static_cast<size_t>(b) * cpr * 16) + 16 * k;
+            oi = static_cast<uint32_t>(b) * cpr * 64 + 16 * k;
         }
         const int nst = K / 128;
         auto issue = [&](int st) {
             int8_t* slot = lds + (st & 1) * kSlotBytes;
-            const int sc = st < nst ? st : nst - 1;
+            const uint32_t sc = st < nst ? st : nst - 1;
 #pragma unroll
-            for (int q = 0; q < kWIns; q++) dma16(pw[q] + sc * 64, slot + (wave * kWIns + q) * 1024);
+            for (int q = 0; q < kWIns; q++) dma16_buf(bf.w, ow[q], sc * 64, slot + (wave * kWIns + q) * 1024);
 #pragma unroll
-            for (int q = 0; q < kXIns; q++) dma16(px[q] + sc * 128, slot + kWBytes + (wave * kXIns + q) * 1024);
-            dma16(pi + sc * 256, slot + kWBytes + kXBytes + wave * 1024);
+            for (int q = 0; q < kXIns; q++) dma16_buf(bf.x, ox[q], sc * 128, slot + kWBytes + (wave * kXIns + q) * 1024);
+            dma16_buf(bf.i, oi, sc * 256, slot + kWBytes + kXBytes + wave * 1024);
         };
         // Sub-step h (dense K [64h, 64h+64) of the stage).
         auto load = [&](int st, int h, Frags& F) {
@@ -896,38 +909,39 @@ struct SpRingTile {
 #pragma unroll
             for (int j = 0; j < kTM; j++) acc[i][j] = v4i{0, 0, 0, 0};
 
-        const int8_t* pw[kWIns];
-        const int8_t* px[kXIns];
+        const SpBufs bf = sp_bufs(W, X, meta, M, N, K);
+        uint32_t ow[kWIns], ox[kXIns];
 #pragma unroll
         for (int q = 0; q < kWIns; q++) {
             const int s = (wave * kWIns + q) * kWave + lane;
             const int r = s >> 2, c = (s & 3) ^ lds_swz4(r);
             const int gr = (n0 + r) < N ? (n0 + r) : N - 1;
-            pw[q] = W + static_cast<size_t>(gr) * Kc + 16 * c;
+            ow[q] = static_cast<uint32_t>(gr) * Kc + 16 * c;
         }
 #pragma unroll
         for (int q = 0; q < kXIns; q++) {
             const int s = (wave * kXIns + q) * kWave + lane;
             const int r = s >> 3, c = (s & 7) ^ lds_swz8(r);
             const int gr = (m0 + r) < M ? (m0 + r) : M - 1;
-            px[q] = X + static_cast<size_t>(gr) * K + 16 * c;
+            ox[q] = static_cast<uint32_t>(gr) * K + 16 * c;
         }
-        const int8_t* pi;
+        uint32_t oi;
         {
             const int s = wave * kILanes + (lane & (kILanes - 1));   // 16-byte chunk of the stage's index area
             int b = (n0 >> 4) + (s >> 4);
             b = b < (N >> 4) ? b : (N >> 4) - 1;
-            pi = reinterpret_cast<const int8_t*>(meta + static_cast<size_t>(b) * cpr * 16) + 16 * (s & 15);
+            oi = static_cast<uint32_t>(b) * cpr * 64 + 16 * (s & 15);
         }
         const int nst = K / 128;
         auto slot_of = [&](int st) { return lds + (st % D) * kSlotBytes; };
         auto issue = [&](int st) {
             int8_t* slot = slot_of(st);
+            const uint32_t su = static_cast<uint32_t>(st);
 #pragma unroll
-            for (int q = 0; q < kWIns; q++) dma16(pw[q] + st * 64, slot + (wave * kWIns + q) * 1024);
+            for (int q = 0; q < kWIns; q++) dma16_buf(bf.w, ow[q], su * 64, slot + (wave * kWIns + q) * 1024);
 #pragma unroll
-            for (int q = 0; q < kXIns; q++) dma16(px[q] + st * 128, slot + kWBytes + (wave * kXIns + q) * 1024);
-            if (lane < kILanes) dma16(pi + st * 256, slot + kWBytes + kXBytes + wave * (16 * kILanes));
+            for (int q = 0; q < kXIns; q++) dma16_buf(bf.x, ox[q], su * 128, slot + kWBytes + (wave * kXIns + q) * 1024);
+            if (lane < kILanes) dma16_buf(bf.i, oi, su * 256, slot + kWBytes + kXBytes + wave * (16 * kILanes));
         };
         // Waits for this wave's DMAs of stage kt when `later` stages were issued after it.
         auto wait_stage = [&](int later) {
@@ -1217,7 +1231,8 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
     }
     // Unsplit plans on 128-deep K stages run on the DMA-fed engines: chosen by tile waves when
     // the planner chose freely, 256 weight rows x 128 tokens for the reference's 256x128 tile.
-    if (K % 128 == 0 && M > 64 && (tile == FORGE_SPARSE_TILE_AUTO || pt == FORGE_SPARSE_TILE_256x128) &&
+    const bool dma_fits = static_cast<long long>(M) * K < (1LL << 31) && static_cast<long long>(N) * K < (1LL << 32);
+    if (dma_fits && K % 128 == 0 && M > 64 && (tile == FORGE_SPARSE_TILE_AUTO || pt == FORGE_SPARSE_TILE_256x128) &&
         (tile == FORGE_SPARSE_TILE_AUTO || tile == FORGE_SPARSE_TILE_256x128)) {
         void* o = out16 ? static_cast<void*>(out16) : static_cast<void*>(out32);
         GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N, aligned(o, 16) ? 1 : 0};
