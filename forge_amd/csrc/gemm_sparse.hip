@@ -283,9 +283,9 @@ __device__ __forceinline__ SpBufs sp_bufs(const int8_t* W, const int8_t* X, cons
     return SpBufs{buf_rsrc(W, n * (k / 2)), buf_rsrc(X, m * k), buf_rsrc(meta, n * (k / 8))};
 }
 
-template <int BMT>
+template <int BMT, int BNW_ = 256>
 struct SpDmaTile {
-    static constexpr int BNW = 256;
+    static constexpr int BNW = BNW_;                   // 256, or 128 for twice the tiles
     static constexpr int kTN = BNW / 2 / 16;           // weight blocks per wave
     static constexpr int kTM = BMT / 2 / 16;           // token blocks per wave
     static constexpr int kTH = kTM / 2;                // token blocks per half
@@ -296,7 +296,9 @@ struct SpDmaTile {
     static constexpr int kLdsBytes = 2 * kSlotBytes;
     static constexpr int kWIns = BNW * 4 / kWave / 4;   // 1 KB DMA instructions per wave per stage
     static constexpr int kXIns = BMT * 8 / kWave / 4;
-    static_assert(BNW / 16 * 16 == kWave * 4, "one index DMA instruction per wave");
+    static constexpr int kILanes = kIBytes / 16 / 4;    // lanes of a wave copying 16 index bytes each
+    static_assert(BNW == 128 || BNW == 256, "weight rows per tile");
+    static_assert(kILanes == 32 || kILanes == 64, "one index DMA instruction per wave");
     static_assert(kTH >= 1, "tile too small");
 
     v4i acc[kTN][kTM];   // acc[i][j]: C[n: 16i + 4*(l/16) + e][m: 16j + l%16]
@@ -338,7 +340,7 @@ struct SpDmaTile {
         }
         uint32_t oi;
         {
-            const int s = wave * kWave + lane;            // 16-byte chunk of the stage's index area
+            const int s = wave * kILanes + (lane & (kILanes - 1));   // 16-byte chunk of the stage's index area
             int b = (n0 >> 4) + (s >> 4);
             b = b < (N >> 4) ? b : (N >> 4) - 1;
             oi = static_cast<uint32_t>(b) * cpr * 64 + 16 * (s & 15);
@@ -351,7 +353,8 @@ struct SpDmaTile {
             for (int q = 0; q < kWIns; q++) dma16_buf(bf.w, ow[q], sc * 64, slot + (wave * kWIns + q) * 1024);
 #pragma unroll
             for (int q = 0; q < kXIns; q++) dma16_buf(bf.x, ox[q], sc * 128, slot + kWBytes + (wave * kXIns + q) * 1024);
-            dma16_buf(bf.i, oi, sc * 256, slot + kWBytes + kXBytes + wave * 1024);
+            if (kILanes == kWave || lane < kILanes)
+                dma16_buf(bf.i, oi, sc * 256, slot + kWBytes + kXBytes + wave * (16 * kILanes));
         };
         auto load_w = [&](int st, WFrag& F) {
             const int8_t* Ws = lds + (st & 1) * kSlotBytes;
@@ -759,18 +762,19 @@ static int launch_sparse_dma32(const int8_t* W, const int8_t* X, const uint32_t*
 // Epilogue of a SpDmaTile: lane l of block (i, j) holds outputs (m = 16j + l%16, n = 16i +
 // 4*(l/16) + e), 4 consecutive columns. FP16: the wave's whole (BMT/2) x 128 tile is staged in
 // LDS; INT32: one 16-row strip per token block. Rows are flushed with 16-byte stores.
-template <int BMT, bool DEQUANT>
-__device__ __forceinline__ void sp_store_tile(const v4i (&acc)[8][BMT / 32], const GemmEpilogue& ep, int n0,
+template <int BMT, bool DEQUANT, int BNW = 256>
+__device__ __forceinline__ void sp_store_tile(const v4i (&acc)[BNW / 32][BMT / 32], const GemmEpilogue& ep, int n0,
                                               int m0, int8_t* lds) {
-    constexpr int kTN = 8, kTM = BMT / 32;
+    constexpr int kTN = BNW / 32, kTM = BMT / 32;
+    constexpr int kWN = BNW / 2;                             // output columns per wave
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    const int wn = n0 + (wave >> 1) * 128;
+    const int wn = n0 + (wave >> 1) * kWN;
     const int wm = m0 + (wave & 1) * (BMT / 2);
     const int r16 = lane & 15, q = lane >> 4;
     const int M = ep.M, N = ep.N;
     if constexpr (DEQUANT) {
-        constexpr int kU = 16, kRowBytes = 256;              // 128 FP16 columns per staged row
+        constexpr int kU = kWN / 8, kRowBytes = 2 * kWN;     // kWN FP16 columns per staged row
         int8_t* stage = lds + wave * ((BMT / 2) * kRowBytes);
         const bool has_bias = ep.bias != nullptr;
         float as[kTM];
@@ -779,19 +783,26 @@ __device__ __forceinline__ void sp_store_tile(const v4i (&acc)[8][BMT / 32], con
             const int m = wm + 16 * j + r16;
             as[j] = ep.act_scale[m < M ? m : M - 1];
         }
-        // The wave's 128 w_scale / bias halves go through a wave-private LDS strip (two loads
-        // per lane, in flight together) instead of one memory latency per column group; the
-        // bias strip holds w_scale when there is no bias (ignored by dequant_gemm).
+        // The wave's kWN w_scale / bias halves go through a wave-private LDS strip (one load
+        // per lane and 64 columns, in flight together) instead of one memory latency per
+        // column group; the bias strip holds w_scale when there is no bias (ignored by
+        // dequant_gemm).
         uint16_t* wsl = reinterpret_cast<uint16_t*>(lds + 4 * (BMT / 2) * kRowBytes) + wave * 256;
         uint16_t* bl = wsl + 128;
         {
             const uint16_t* bsrc = has_bias ? ep.bias : ep.w_scale;
-            const int n0c = min(wn + lane, N - 1), n1c = min(wn + 64 + lane, N - 1);
-            const uint16_t w0 = ep.w_scale[n0c], w1 = ep.w_scale[n1c], b0 = bsrc[n0c], b1 = bsrc[n1c];
-            wsl[lane] = w0;
-            wsl[64 + lane] = w1;
-            bl[lane] = b0;
-            bl[64 + lane] = b1;
+            uint16_t w[kWN / 64], bb[kWN / 64];
+#pragma unroll
+            for (int h = 0; h < kWN / 64; h++) {
+                const int nc = min(wn + 64 * h + lane, N - 1);
+                w[h] = ep.w_scale[nc];
+                bb[h] = bsrc[nc];
+            }
+#pragma unroll
+            for (int h = 0; h < kWN / 64; h++) {
+                wsl[64 * h + lane] = w[h];
+                bl[64 * h + lane] = bb[h];
+            }
         }
 #pragma unroll
         for (int i = 0; i < kTN; i++) {
@@ -818,7 +829,7 @@ __device__ __forceinline__ void sp_store_tile(const v4i (&acc)[8][BMT / 32], con
         }
         flush_rows<kU, 2, true, false, BMT / 2>(stage, ep, wm, wn);
     } else {
-        constexpr int kU = 32, kRowBytes = 512;              // 128 INT32 columns per staged row
+        constexpr int kU = kWN / 4, kRowBytes = 4 * kWN;     // kWN INT32 columns per staged row
         int8_t* strip = lds + wave * (16 * kRowBytes);
 #pragma unroll
         for (int j = 0; j < kTM; j++) {
@@ -833,13 +844,13 @@ __device__ __forceinline__ void sp_store_tile(const v4i (&acc)[8][BMT / 32], con
     }
 }
 
-template <int BMT, bool DEQUANT>
+template <int BMT, bool DEQUANT, int BNW = 256>
 constexpr int sp_dma_lds_bytes() {
-    constexpr int epi = DEQUANT ? 4 * (BMT / 2) * 256 + 4 * 512 : 4 * 16 * 512;
-    return SpDmaTile<BMT>::kLdsBytes > epi ? SpDmaTile<BMT>::kLdsBytes : epi;
+    constexpr int epi = DEQUANT ? 4 * (BMT / 2) * BNW + 4 * 512 : 4 * 16 * (2 * BNW);
+    return SpDmaTile<BMT, BNW>::kLdsBytes > epi ? SpDmaTile<BMT, BNW>::kLdsBytes : epi;
 }
 
-template <int BMT, bool DEQUANT>
+template <int BMT, bool DEQUANT, int BNW = 256>
 __global__ __launch_bounds__(256) void sparse_dma_kernel(const int8_t* __restrict__ W, const int8_t* __restrict__ X,
                                                          const uint32_t* __restrict__ meta, GemmEpilogue ep,
                                                          int tiles_n, int tiles_m, int K)
@@ -847,24 +858,25 @@ __global__ __launch_bounds__(256) void sparse_dma_kernel(const int8_t* __restric
     extern __shared__ __align__(16) int8_t lds[];
     int tn, tm;
     tile_coords(blockIdx.x, tiles_n, tiles_m, tn, tm);
-    const int n0 = tn * 256, m0 = tm * BMT;
-    SpDmaTile<BMT> t;
+    const int n0 = tn * BNW, m0 = tm * BMT;
+    SpDmaTile<BMT, BNW> t;
     t.run(W, X, meta, ep.M, ep.N, K, n0, m0, lds);
-    sp_store_tile<BMT, DEQUANT>(t.acc, ep, n0, m0, lds);
+    sp_store_tile<BMT, DEQUANT, BNW>(t.acc, ep, n0, m0, lds);
 }
 
-template <int BMT, bool DEQUANT>
+template <int BMT, bool DEQUANT, int BNW = 256>
 static int launch_sparse_dma(const int8_t* W, const int8_t* X, const uint32_t* meta, const GemmEpilogue& ep,
                              int K, hipStream_t s)
 {
-    constexpr int lds = sp_dma_lds_bytes<BMT, DEQUANT>();
-    const int tiles_n = divup(ep.N, 256), tiles_m = divup(ep.M, BMT);
+    constexpr int lds = sp_dma_lds_bytes<BMT, DEQUANT, BNW>();
+    const int tiles_n = divup(ep.N, BNW), tiles_m = divup(ep.M, BMT);
     const long long total = static_cast<long long>(tiles_n) * tiles_m;
     if (total > 0x7FFFFFFFLL) return FORGE_EINVAL;
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&sparse_dma_kernel<BMT, DEQUANT>), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&sparse_dma_kernel<BMT, DEQUANT, BNW>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (attr != hipSuccess) return static_cast<int>(attr);
-    sparse_dma_kernel<BMT, DEQUANT><<<static_cast<unsigned>(total), 256, lds, s>>>(W, X, meta, ep, tiles_n, tiles_m, K);
+    sparse_dma_kernel<BMT, DEQUANT, BNW>
+        <<<static_cast<unsigned>(total), 256, lds, s>>>(W, X, meta, ep, tiles_n, tiles_m, K);
     return launch_status();
 }
 
@@ -1143,37 +1155,39 @@ static int cu_count_or_default() {
 }
 
 // Unsplit DMA engine choice (automatic plans, M > 64, K % 128 == 0): 256 weight rows x 256
-// tokens (sparse_dma32, M > 128), x 128 tokens (sparse_dma<128>), or the 64 x 64 ring engine
-// (sparse_ring, 4 slots: three workgroups per CU). A tile wave costs stages x stage time + a
-// fixed part (ring fill, epilogue), with stage times measured on MI355X: the two 256-row
-// engines stream about the same bytes per CU per microsecond, so their stages cost in
-// proportion to their bytes (52 KB: ~1.16 us; 36 KB: ~0.80 us). The ring's tiles share CUs
-// (up to 3 at once), a stage costing ~0.30 us per round of up to 3 tiles plus ~0.10 us per tile
-// on the busiest CU. Measured: 1536x6144 at M = 1024 256x128 15.6 us (256x256 20.0);
-// 6144x1536 at M = 4096 256x128 43.0 us (256x256 55.7); at M = 1024 the 64-row ring 24.4 us
-// (128-row ring with 8 slots, one workgroup per CU: 30.4; 256x128 39.8); 5120x1280 at M = 1024
-// 21.6 us (26.7); 4096x1024 at M = 1024 15.3 us (22.3); configs[2] on 256x256.
-enum class SpEngine { k256x256, k256x128, kRing };
+// tokens (sparse_dma32, M > 128), 128 x 128 (sparse_dma<128, 128>: 52 KB of LDS, two
+// workgroups per CU by registers), or the 64 x 64 ring engine (sparse_ring, 4 slots, three
+// workgroups per CU). Each engine's time is modelled from the tiles on the busiest CU (w) and
+// the 128-deep stages (steps), with coefficients fitted on MI355X timings of every engine on 30
+// shapes (the reference sweep at M = 1024 / 4096 / 8192, its narrow layers at M up to 147,456,
+// the engine tests' shapes, configs[2] with FP16 out, deep-K layers at M = 256-2048), in us:
+//   256 x 256: w (0.88 steps + 10.0)
+//   128 x 128: 0.48 steps + 3.7 for one tile per CU, else ceil(w / 2) (0.71 steps + 5.2)
+//   ring:      steps (0.175 ceil(w / 3) + 0.123 w) + 4.6, only up to one round (w <= 3)
+// The pick is the fastest engine on 28 of the 30 shapes and within 8 % on the other two (the
+// 256 x 128 engine, kept for the reference's forced 256x128 tile, was never the fastest there).
+// Examples (us): 1536x6144 at M = 1024 128x128 13.5 (256x256 19.3, 256x128 15.1); 6144x1536 at
+// M = 1024 ring 24.0 (128x128 32.3); 640x320 at M = 147,456 128x128 53.5 (256x256 71.6);
+// configs[2] on 256x256.
+enum class SpEngine { k256x256, k256x128, k128x128, kRing };
 constexpr int kSpRingRows = 64, kSpRingDepth = 4, kSpRingPerCu = 3;
 
 static SpEngine sparse_pick_engine(int M, int N, int K, int cu)
 {
     const double steps = static_cast<double>(divup(K, kSpStep));
-    const long long tn256 = divup(N, 256), tnr = divup(N, kSpRingRows);
-    const double w128 = static_cast<double>(divupll(tn256 * divup(M, 128), cu));
-    const long long wr = divupll(tnr * divup(M, 64), cu);   // ring tiles on the busiest CU
-    const double ring = steps * (0.30 * static_cast<double>(divupll(wr, kSpRingPerCu)) + 0.10 * static_cast<double>(wr)) + 1.5;
-    double best = w128 * (0.80 * steps + 3.0);
-    SpEngine e = SpEngine::k256x128;
+    const long long w128 = divupll(static_cast<long long>(divup(N, 128)) * divup(M, 128), cu);
+    const long long wr = divupll(static_cast<long long>(divup(N, kSpRingRows)) * divup(M, 64), cu);
+    double best = w128 == 1 ? 0.48 * steps + 3.7 : static_cast<double>(divupll(w128, 2)) * (0.71 * steps + 5.2);
+    SpEngine e = SpEngine::k128x128;
     if (M > 128) {
-        const double w256 = static_cast<double>(divupll(tn256 * divup(M, 256), cu));
-        const double t = w256 * (1.16 * steps + 4.0);
-        if (t <= best) { best = t; e = SpEngine::k256x256; }
+        const double w256 = static_cast<double>(divupll(static_cast<long long>(divup(N, 256)) * divup(M, 256), cu));
+        const double t = w256 * (0.88 * steps + 10.0);
+        if (t < best) { best = t; e = SpEngine::k256x256; }
     }
-    // The ring's model is fitted where its tiles take at most one round of 3 per CU; beyond
-    // that the 256-row engines' reuse wins (measured: 640 x 320 at M = 147,456 on the ring
-    // 128 us against 80 us on 256 x 256).
-    if (wr <= kSpRingPerCu && ring < best) e = SpEngine::kRing;
+    if (wr <= kSpRingPerCu) {
+        const double t = steps * (0.175 * static_cast<double>(divupll(wr, kSpRingPerCu)) + 0.123 * static_cast<double>(wr)) + 4.6;
+        if (t < best) e = SpEngine::kRing;
+    }
     return e;
 }
 
@@ -1238,13 +1252,19 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
         GemmEpilogue ep{out32, out16, act_scale, w_scale, bias, M, N, aligned(o, 16) ? 1 : 0};
         const SpEngine e = tile == FORGE_SPARSE_TILE_AUTO ? sparse_pick_engine(M, N, K, cu_count_or_default())
                                                           : SpEngine::k256x128;
-        note_route(e == SpEngine::k256x256 ? "dma256x256" : e == SpEngine::kRing ? "ring64x64" : "dma256x128");
+        note_route(e == SpEngine::k256x256 ? "dma256x256"
+                   : e == SpEngine::kRing  ? "ring64x64"
+                   : e == SpEngine::k128x128 ? "dma128x128"
+                                             : "dma256x128");
         if (e == SpEngine::k256x256)
             return out16 ? launch_sparse_dma32<true>(W_comp, x, meta, ep, K, s)
                          : launch_sparse_dma32<false>(W_comp, x, meta, ep, K, s);
         if (e == SpEngine::kRing)
             return out16 ? launch_sparse_ring<true, kSpRingRows, kSpRingDepth>(W_comp, x, meta, ep, K, s)
                          : launch_sparse_ring<false, kSpRingRows, kSpRingDepth>(W_comp, x, meta, ep, K, s);
+        if (e == SpEngine::k128x128)
+            return out16 ? launch_sparse_dma<128, true, 128>(W_comp, x, meta, ep, K, s)
+                         : launch_sparse_dma<128, false, 128>(W_comp, x, meta, ep, K, s);
         return out16 ? launch_sparse_dma<128, true>(W_comp, x, meta, ep, K, s)
                      : launch_sparse_dma<128, false>(W_comp, x, meta, ep, K, s);
     }

@@ -173,16 +173,18 @@ def test_config3_full_size(dev, orc):
     assert bad == 0, f"{bad} of {C.size} outputs differ"
 
 
-# Plans on each unsplit DMA engine, chosen by tile waves (tile -1) or forced to the reference's
-# 256 x 128 tile (0): the 64 x 64 ring engine (narrow N or few token tiles with deep K: fewer
-# stages than the 3 the ring keeps in flight, more, partial last token tile, partial last 64-row
-# weight tile), the 256 x 128 engine and the 256 x 256 one. The INT32 call always plans itself.
+# Plans on each unsplit DMA engine, chosen by the engine model (tile -1) or forced to the
+# reference's 256 x 128 tile (0): the 64 x 64 ring engine (narrow N or few token tiles with deep
+# K; partial last token tile), the 128 x 128 engine (one and several rounds of tiles per CU,
+# partial last weight and token tiles), the 256 x 128 engine and the 256 x 256 one. The INT32
+# call always plans itself.
 ENGINE_SHAPES = [
     (200, 2048, 256, -1, "ring64x64"),     # 4 token tiles (last 8 rows), 4 weight tiles
-    (100, 256, 144, -1, "ring64x64"),      # 2 stages (< 3 in flight), last weight tile 16 of 64 rows
     (1024, 6144, 1536, -1, "ring64x64"),   # the reference benchmark's narrow deep-K layer
+    (100, 256, 144, -1, "dma128x128"),     # 2 stages, last weight tile 16 of 128 rows, M < 128
+    (1024, 1536, 6144, -1, "dma128x128"),
+    (40000, 640, 320, -1, "dma128x128"),   # 4 tiles on the busiest CU, ragged token and weight tiles
     (512, 128, 2048, 0, "dma256x128"),     # one stage
-    (1024, 1536, 6144, -1, "dma256x128"),
     (4000, 4096, 4096, -1, "dma256x256"),  # ragged token tile
 ]
 
