@@ -34,6 +34,7 @@
 #include "common.h"
 #include "gemm_dense.h"
 #include "mfma_tile.h"
+#include "stream_slots.h"
 
 #include <mutex>
 
@@ -877,13 +878,8 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
 // K split for narrow N (row blocks fewer than CUs): the KP workgroups of a row block each take
 // K / KP and hand their sums over (ksplit_handoff). The sums and counters live in static device
 // slots, zero when the code object loads and left zero by every launch, so nothing is
-// allocated. Two launches must never use one slot at the same time, so a slot belongs to one
-// key: (stream, 0) for launches made outside graph capture, whose launches on that stream run
-// in order, and (stream, capture id) for launches recorded into a graph, which run in order
-// within each replay of that graph. No key is shared between eager work and a capture, or
-// between two captures; a graph must not be replayed while another replay of the same graph
-// is still running (as for any graph whose nodes share memory). A slot stays with its key
-// until the process ends; with every slot taken, a launch runs unsplit (same bits, no split).
+// allocated; a slot belongs to one launch key (stream_slots.h), and with every slot taken a
+// launch runs unsplit (same bits, no split).
 // Measured at M = 16, K = 8192 (128 and 32 row blocks of 32 rows): N = 4096
 // 13.6 -> 9.9 us, N = 1000 13.2 -> 8.8 us. Where the row blocks already fill the chip the split
 // only adds the hand-off (N = 8192: 14.4 -> 15.2 us), so it is not used there.
@@ -895,16 +891,10 @@ static __device__ int g_ksplit_acc[kKSplitSlots * kKSplitAccPerSlot];
 static __device__ unsigned g_ksplit_cnt[kKSplitSlots * kKSplitMaxBlocks];
 
 namespace {
-constexpr int kKSplitMaxDev = 64;
-struct SlotKey {
-    hipStream_t stream;
-    unsigned long long capture;   // 0: eager launches; otherwise the capture's id
-};
 std::mutex g_ks_mu;
-int* g_ks_acc_dev[kKSplitMaxDev];
-unsigned* g_ks_cnt_dev[kKSplitMaxDev];
-SlotKey g_ks_owner[kKSplitMaxDev][kKSplitSlots];
-int g_ks_used[kKSplitMaxDev];
+int* g_ks_acc_dev[kSlotMaxDev];
+unsigned* g_ks_cnt_dev[kSlotMaxDev];
+SlotOwners<kKSplitSlots> g_ks_slots;
 thread_local int t_ks_last_slot = -1;   // the calling thread's last decode launch: slot (-1: none)
 thread_local int t_ks_last_kp = 0;      // and its K parts (1: unsplit; 0: no decode launch yet)
 
@@ -924,20 +914,12 @@ bool ksplit_resolve(int dev)
     return true;
 }
 
-bool current_device(int* dev)
-{
-    if (hipGetDevice(dev) != hipSuccess || *dev < 0 || *dev >= kKSplitMaxDev) {
-        (void)hipGetLastError();
-        return false;
-    }
-    return true;
-}
 }  // namespace
 
 int ksplit_prepare()
 {
     int dev = 0;
-    if (!current_device(&dev)) return FORGE_ENODEV;
+    if (!slot_device(&dev)) return FORGE_ENODEV;
     std::lock_guard<std::mutex> lock(g_ks_mu);
     return ksplit_resolve(dev) ? FORGE_OK : FORGE_ENODEV;
 }
@@ -949,27 +931,13 @@ int ksplit_prepare()
 static KSplit ksplit_slot(hipStream_t s, int* slot_out)
 {
     *slot_out = -1;
-    if (s == hipStreamPerThread) return {};
     int dev = 0;
-    if (!current_device(&dev)) return {};
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    unsigned long long cid = 0;
-    if (hipStreamGetCaptureInfo(s, &cs, &cid) != hipSuccess) {
-        (void)hipGetLastError();
-        return {};
-    }
-    if (cs == hipStreamCaptureStatusInvalidated) return {};
-    const SlotKey key{s, cs == hipStreamCaptureStatusActive ? (cid ? cid : ~0ull) : 0ull};
+    SlotKey key{};
+    if (!slot_device(&dev) || !slot_key(s, &key)) return {};
     std::lock_guard<std::mutex> lock(g_ks_mu);
     if (!g_ks_acc_dev[dev] && (key.capture != 0 || !ksplit_resolve(dev))) return {};
-    int slot = -1;
-    for (int i = 0; i < g_ks_used[dev]; i++)
-        if (g_ks_owner[dev][i].stream == key.stream && g_ks_owner[dev][i].capture == key.capture) slot = i;
-    if (slot < 0) {
-        if (g_ks_used[dev] == kKSplitSlots) return {};
-        slot = g_ks_used[dev]++;
-        g_ks_owner[dev][slot] = key;
-    }
+    const int slot = g_ks_slots.take(dev, key);
+    if (slot < 0) return {};
     *slot_out = slot;
     return {g_ks_acc_dev[dev] + static_cast<size_t>(slot) * kKSplitAccPerSlot,
             g_ks_cnt_dev[dev] + static_cast<size_t>(slot) * kKSplitMaxBlocks};
@@ -1532,7 +1500,7 @@ extern "C" int forge_ksplit_last(int* slot, int* parts)
 extern "C" int forge_ksplit_reset(void* stream)
 {
     int dev = 0;
-    if (!current_device(&dev)) return FORGE_ENODEV;
+    if (!slot_device(&dev)) return FORGE_ENODEV;
     int* acc = nullptr;
     unsigned* cnt = nullptr;
     {

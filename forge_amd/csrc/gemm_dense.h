@@ -56,6 +56,8 @@ int launch_decode(const int8_t* W, const uint32_t* meta, const int8_t* X, const 
 // Resolves the decode K-split slot arrays on the current device (forge_init calls it, so that a
 // first split launch inside a graph capture needs no symbol lookup).
 int ksplit_prepare();
+// Resolves the fused sparse linear's packed-weight slots on the current device (forge_init).
+int fq_pack_prepare();
 // Resolves the device address of forge_int8_linear_noalloc's array on the current device.
 int noalloc_prepare();
 

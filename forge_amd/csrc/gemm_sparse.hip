@@ -28,6 +28,7 @@
 #include "common.h"
 #include "gemm_dense.h"
 #include "mfma_tile.h"
+#include "stream_slots.h"
 #include "forge/gemm/int8_sparse.h"
 
 #include <algorithm>
@@ -1309,7 +1310,12 @@ constexpr int kFqRowsInFlight = 4;   // token rows per producer wave whose loads
 constexpr int kFqAhead = 3;          // K steps of weight fragments in flight per consumer wave
 constexpr int kFqLds = 160 * 1024;
 
-template <int NBW, int BT>
+// PACKED: W_comp is in fragment order (fq_pack_weights_kernel): a consumer's weight fragment
+// of one block and K step is one contiguous 1 KB load instead of 16 half cache lines, 64 bytes
+// in each of 16 rows -- adjacent lanes then read adjacent 16-byte units, which the texture
+// unit serves several times faster (measured at 147,456 x 1280 -> 320: consumer waves alone
+// 104 -> 64 us).
+template <int NBW, int BT, bool PACKED>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void sparse_fq_kernel(
     const uint16_t* __restrict__ x, const int8_t* __restrict__ W_comp, const uint32_t* __restrict__ meta,
     const uint16_t* __restrict__ w_scale, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
@@ -1439,8 +1445,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
                 for (int i = 0; i < NBW; i++) {
                     const int b = min(wb0 + i, NB - 1);
-                    a[i] = *reinterpret_cast<const v4i*>(W_comp + static_cast<size_t>(16 * b + r16) * Kc +
-                                                         kSpARow * sr + 16 * g);
+                    if constexpr (PACKED)
+                        a[i] = *reinterpret_cast<const v4i*>(W_comp + (static_cast<size_t>(b) * KS + sr) * 1024 +
+                                                             16 * ln);
+                    else
+                        a[i] = *reinterpret_cast<const v4i*>(W_comp + static_cast<size_t>(16 * b + r16) * Kc +
+                                                             kSpARow * sr + 16 * g);
                     ix[i] = static_cast<int>(meta[static_cast<size_t>(b) * cpr * 16 + (4 * sr + g) * 16 + r16]);
                 }
             };
@@ -1557,6 +1567,71 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
+// The fused kernel's weights in fragment order: for 16-row block b and 128-deep step s, the
+// 1 KB at (b * KS + s) * 1024 holds the SMFMAC A operand in lane order, lane 16 g + r at byte
+// 16 (16 g + r): row 16 b + r, compressed bytes 64 s + 16 g .. + 15 of W_comp (N, K/2). One
+// thread per 16-byte unit, read in W_comp's order.
+__global__ __launch_bounds__(256) void fq_pack_weights_kernel(const int8_t* __restrict__ W_comp, int8_t* __restrict__ dst,
+                                                              int N, int K)
+{
+    const int upr = K / 32;                      // 16-byte units per row
+    const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= static_cast<long long>(N) * upr) return;
+    const int row = static_cast<int>(i / upr), u = static_cast<int>(i % upr);
+    const int s = u >> 2, g = u & 3;
+    const size_t o = (static_cast<size_t>(row >> 4) * (K / kSpStep) + s) * 64 + 16 * g + (row & 15);
+    reinterpret_cast<uint4*>(dst)[o] = reinterpret_cast<const uint4*>(W_comp)[i];
+}
+
+// Packed weights live in static device slots owned per launch key (stream_slots.h), so the
+// fused path allocates nothing and leaves the caller's scratch buffers untouched (the
+// reference's contract for it). A launch without a slot, or with weights beyond a slot, reads
+// W_comp in place (same bits).
+constexpr int kFqPackSlots = 8;
+constexpr size_t kFqPackBytes = size_t(1) << 20;   // N * K / 2: 1280 x 1638, 2048 x 1024
+static __device__ __align__(16) int8_t g_fq_pack[kFqPackSlots * kFqPackBytes];
+
+namespace {
+std::mutex g_fq_mu;
+int8_t* g_fq_pack_dev[kSlotMaxDev];
+SlotOwners<kFqPackSlots> g_fq_slots;
+
+// Resolves the pack array of device dev (g_fq_mu held); false if it cannot be resolved.
+bool fq_pack_resolve(int dev)
+{
+    if (g_fq_pack_dev[dev]) return true;
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_fq_pack)) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    g_fq_pack_dev[dev] = static_cast<int8_t*>(p);
+    return true;
+}
+
+// The pack slot of the launch key of s on the current device, or nullptr (no packing): every
+// slot held by other keys, a key that cannot be formed, or the array not resolved yet while s
+// captures a graph (forge_init resolves it outside any capture).
+int8_t* fq_pack_slot(hipStream_t s)
+{
+    int dev = 0;
+    SlotKey key{};
+    if (!slot_device(&dev) || !slot_key(s, &key)) return nullptr;
+    std::lock_guard<std::mutex> lock(g_fq_mu);
+    if (!g_fq_pack_dev[dev] && (key.capture != 0 || !fq_pack_resolve(dev))) return nullptr;
+    const int slot = g_fq_slots.take(dev, key);
+    return slot < 0 ? nullptr : g_fq_pack_dev[dev] + static_cast<size_t>(slot) * kFqPackBytes;
+}
+}  // namespace
+
+int fq_pack_prepare()
+{
+    int dev = 0;
+    if (!slot_device(&dev)) return FORGE_ENODEV;
+    std::lock_guard<std::mutex> lock(g_fq_mu);
+    return fq_pack_resolve(dev) ? FORGE_OK : FORGE_ENODEV;
+}
+
 // Token rows per tile: the tallest of 64 / 48 / 32 whose two buffers and the scale strips fit.
 static int fq_bt(int K, int N) {
     for (int bt : {64, 48, 32}) {
@@ -1596,21 +1671,38 @@ static bool fq_pays(int M, int K, int N) {
     return N % 256 != 0 || K >= 2048;
 }
 
+template <int NBW, int BT, bool PACKED>
+static int launch_fq_kernel(const uint16_t* x, const int8_t* W, const uint32_t* meta, const uint16_t* w_scale,
+                            const uint16_t* bias, uint16_t* out, int M, int K, int N, int cu, hipStream_t s)
+{
+    const size_t lds = fq_lds_bytes(K, N, BT);
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&sparse_fq_kernel<NBW, BT, PACKED>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        kFqLds);
+    if (attr != hipSuccess) return static_cast<int>(attr);
+    const int tiles = divup(M, BT);
+    const int grid = std::min(tiles, cu);     // one 8-wave workgroup per CU
+    sparse_fq_kernel<NBW, BT, PACKED><<<grid, 512, lds, s>>>(x, W, meta, w_scale, bias, out, M, K, N, tiles);
+    return launch_status();
+}
+
 template <int NBW, int BT>
 static int launch_fq(const uint16_t* x, const int8_t* W_comp, const uint32_t* meta, const uint16_t* w_scale,
                      const uint16_t* bias, uint16_t* out, int M, int K, int N, hipStream_t s)
 {
-    const size_t lds = fq_lds_bytes(K, N, BT);
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&sparse_fq_kernel<NBW, BT>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kFqLds);
-    if (attr != hipSuccess) return static_cast<int>(attr);
     int st = FORGE_OK;
     const int cu = device_info(&st).cu_count;
     if (st != FORGE_OK) return st;
-    const int tiles = divup(M, BT);
-    const int grid = std::min(tiles, cu);     // one 8-wave workgroup per CU
-    sparse_fq_kernel<NBW, BT><<<grid, 512, lds, s>>>(x, W_comp, meta, w_scale, bias, out, M, K, N, tiles);
-    return launch_status();
+    int8_t* pk = static_cast<size_t>(N) * K / 2 <= kFqPackBytes ? fq_pack_slot(s) : nullptr;
+    if (!pk) {
+        note_route("fused-quantize");
+        return launch_fq_kernel<NBW, BT, false>(x, W_comp, meta, w_scale, bias, out, M, K, N, cu, s);
+    }
+    note_route("fused-quantize packed");
+    const long long units = static_cast<long long>(N) * (K / 32);
+    fq_pack_weights_kernel<<<static_cast<unsigned>(divupll(units, 256)), 256, 0, s>>>(W_comp, pk, N, K);
+    if ((st = launch_status()) != FORGE_OK) return st;
+    return launch_fq_kernel<NBW, BT, true>(x, pk, meta, w_scale, bias, out, M, K, N, cu, s);
 }
 
 template <int BT>
@@ -1712,7 +1804,6 @@ extern "C" int forge_sparse_int8_linear(const uint16_t* x, const int8_t* W_comp,
     }
     if (fq_fits(x, W_comp, out, K, N_out) &&
         (path == 1 || (path == -1 && split_k <= 1 && fq_pays(M, K, N_out)))) {
-        note_route("fused-quantize");
         return launch_sparse_fq(x, W_comp, w_meta, w_scale, bias, out, M, K, N_out, s);
     }
     int st = launch_quantize(x, scratch_q, scratch_scale, M, K, s);

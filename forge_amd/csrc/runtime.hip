@@ -82,6 +82,7 @@ extern "C" int forge_init(void) {
     device_info(&st);
     if (st != FORGE_OK) return st;
     if ((st = ksplit_prepare()) != FORGE_OK) return st;
+    if ((st = fq_pack_prepare()) != FORGE_OK) return st;
     return noalloc_prepare();
 }
 

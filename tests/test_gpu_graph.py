@@ -155,6 +155,31 @@ def test_graph_sparse_splitk(dev):
         _replay_check(dev, calls, [y])
 
 
+def test_graph_sparse_fq(dev):
+    """The fused quantize + sparse linear with its weight-packing launch: the capture packs into
+    a slot of its own (distinct from the eager slot of the capture stream)."""
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(29)
+    M, K, N = 200, 1280, 320
+    say(f"graph fused sparse linear M={M} K={K} N={N}")
+    W = to_dev(int8_uniform(rng, (N, K)), dev)
+    comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+    raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+    meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+    ops.prune_compress_24(W, comp, raw, N, K)
+    ops.pack_metadata(raw, meta, N, K)
+    x = to_dev(fp16_normal(rng, (M, K)), dev)
+    ws = to_dev(rng.uniform(1e-3, 1e-2, N).astype(np.float16), dev)
+    b = to_dev(fp16_normal(rng, (N,), 0.1), dev)
+    q = torch.empty((M, K), dtype=torch.int8, device=dev)
+    s = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    calls = [lambda: ops.sparse_int8_linear(x, comp, meta, ws, b, q, s, None, 1, 1, out=y)]
+    _replay_check(dev, calls, [y])
+    assert ops.last_route() == "fused-quantize packed"
+
+
 def test_graph_conv(dev):
     """NHWC conv on the DMA gather (C % 128 == 0) and on the register engine (C = 48)."""
     import torch

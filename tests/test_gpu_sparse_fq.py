@@ -5,7 +5,8 @@ Forced (path 1) over every weight-blocks-per-wave variant (N = 16 .. 528, includ
 pass with a partial block set), ragged token counts and K from 128 to the 2048 limit, each
 bit-exact against the oracle's two-pass composition (quantize rows -> sparse INT32 GEMM ->
 dequant epilogue) and against the library's own two-pass path; the scratch buffers stay
-untouched, as the reference documents (int8_sparse.cuh:87-89); and the automatic choice takes
+untouched, as the reference documents (int8_sparse.cuh:87-89), with the weights packed into
+fragment order in the library's own slot or, beyond a slot, read in place; and the automatic choice takes
 the fused kernel for the reference's own example layer (1280 -> 320 at M = 147,456), where its
 output equals the two-pass output bit for bit."""
 import numpy as np
@@ -52,8 +53,38 @@ def test_fq_forced_parity(dev, orc, M, K, N, bias):
     ss.view(torch.int32).fill_(0x5A5A5A5A)
     say(f"fused sparse linear M={M} K={K} N={N} bias={bias}")
     y = ops.sparse_int8_linear(xd, comp, meta, wsd, bd, sq, ss, None, 1, 1)
+    assert ops.last_route() in ("fused-quantize packed", "decode+quantize")
     assert np.array_equal(to_host(y).view(np.uint16), ref)
     # the scratch buffers are not touched on the fused path
+    assert bool((sq == 0x5A).all()) and bool((ss.view(torch.int32) == 0x5A5A5A5A).all())
+    y2 = ops.sparse_int8_linear(xd, comp, meta, wsd, bd, sq, ss, None, 1, 0)
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+
+
+def test_fq_weights_in_place(dev, orc):
+    """Weights beyond a packed-weight slot (N * K / 2 > 1 MiB: 1040 x 2048) are read from W_comp
+    in place, with several passes of weight blocks per consumer wave: bit-exact against the
+    oracle and the two-pass path, scratch untouched."""
+    import torch
+    from forge_amd import ops
+    M, K, N = 100, 2048, 1040
+    rng = np.random.default_rng(1040)
+    W = int8_uniform(rng, (N, K))
+    x = rng.uniform(-2.0, 2.0, (M, K)).astype(np.float16)
+    ws = rng.uniform(0.001, 0.05, N).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
+    cr, mr = orc.prune_compress_24(W)
+    qr, sr = orc.quantize_rows(x)
+    ref = orc.dequant_epilogue(orc.sparse_gemm_s32(cr, qr, mr, N, K), sr, ws, b).view(np.uint16)
+    comp, meta = _prep(dev, W)
+    xd, wsd, bd = to_dev(x, dev), to_dev(ws, dev), to_dev(b, dev)
+    sq = torch.full((M, K), 0x5A, dtype=torch.int8, device=dev)
+    ss = torch.empty((M,), dtype=torch.float32, device=dev)
+    ss.view(torch.int32).fill_(0x5A5A5A5A)
+    say(f"fused sparse linear, weights in place M={M} K={K} N={N}")
+    y = ops.sparse_int8_linear(xd, comp, meta, wsd, bd, sq, ss, None, 1, 1)
+    assert ops.last_route() == "fused-quantize"
+    assert np.array_equal(to_host(y).view(np.uint16), ref)
     assert bool((sq == 0x5A).all()) and bool((ss.view(torch.int32) == 0x5A5A5A5A).all())
     y2 = ops.sparse_int8_linear(xd, comp, meta, wsd, bd, sq, ss, None, 1, 0)
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
@@ -111,6 +142,7 @@ def test_fq_auto_on_reference_layer(dev, orc):
     ss = torch.empty((M,), dtype=torch.float32, device=dev)
     say("fused sparse linear 147456x1280->320 auto vs two-pass")
     y_auto = ops.sparse_int8_linear(xd, comp, meta, wsd, bd, sq, ss, None, 1, -1)
+    assert ops.last_route() == "fused-quantize packed"
     y_two = ops.sparse_int8_linear(xd, comp, meta, wsd, bd, sq, ss, None, 1, 0)
     torch.cuda.synchronize()
     assert torch.equal(y_auto.view(torch.int16), y_two.view(torch.int16))
