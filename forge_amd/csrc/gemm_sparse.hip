@@ -1315,7 +1315,11 @@ constexpr int kFqLds = 160 * 1024;
 // in each of 16 rows -- adjacent lanes then read adjacent 16-byte units, which the texture
 // unit serves several times faster (measured at 147,456 x 1280 -> 320: consumer waves alone
 // 104 -> 64 us).
-template <int NBW, int BT, bool PACKED>
+// NV: 16-byte vectors per lane per token row, at least K / 512 (rows of K / 8 vectors over the
+// 64 lanes of a producer wave): lanes past the row end hold no data but still cost a load slot
+// and registers, so NV follows K (at K = 1280, 3 rather than 4: 147,456 x 1280 -> 320 155 ->
+// 142 us).
+template <int NBW, int BT, bool PACKED, int NV>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void sparse_fq_kernel(
     const uint16_t* __restrict__ x, const int8_t* __restrict__ W_comp, const uint32_t* __restrict__ meta,
     const uint16_t* __restrict__ w_scale, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
@@ -1347,22 +1351,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // use compiled to load -> wait -> use, one memory latency per vector.
     constexpr int kR = kFqRowsInFlight;
     constexpr int kBatches = kRowsPerProducer / kR;
-    auto load_batch = [&](int ln, int m0, int r0, uint4 (&v)[kR][4]) {
+    auto load_batch = [&](int ln, int m0, int r0, uint4 (&v)[kR][NV]) {
 #pragma unroll
         for (int u = 0; u < kR; u++) {
             const int row = min(m0 + r0 + u, M - 1);
             const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<size_t>(row) * K);
 #pragma unroll
-            for (int i = 0; i < 4; i++) v[u][i] = src[min(ln + kWave * i, nvec - 1)];
+            for (int i = 0; i < NV; i++) v[u][i] = src[min(ln + kWave * i, nvec - 1)];
         }
     };
-    auto quantize_batch = [&](int ln, int r0, const uint4 (&v)[kR][4], int8_t* Xs, float* sc) {
+    auto quantize_batch = [&](int ln, int r0, const uint4 (&v)[kR][NV], int8_t* Xs, float* sc) {
         uint32_t mb[kR];
 #pragma unroll
         for (int u = 0; u < kR; u++) {
             mb[u] = 0u;
 #pragma unroll
-            for (int i = 0; i < 4; i++) mb[u] = absbits8(v[u][i], mb[u]);
+            for (int i = 0; i < NV; i++) mb[u] = absbits8(v[u][i], mb[u]);
         }
         uint32_t abits[kR];
 #pragma unroll
@@ -1377,7 +1381,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             if (abits[u] > kHalfInfBits) {       // the row holds a NaN: fp32 max skipping it
                 float a = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 4; i++) a = absmax8(v[u][i], a);
+                for (int i = 0; i < NV; i++) a = absmax8(v[u][i], a);
                 amax = wave_max(a);
             } else {
                 amax = h2f(static_cast<uint16_t>(abits[u]));
@@ -1387,7 +1391,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const float inv = 1.0f / scale;
             if (ln == 0) sc[r] = scale;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
+            for (int i = 0; i < NV; i++) {
                 const int idx = ln + kWave * i;
                 if (idx < nvec) {
                     const int k = 8 * idx;
@@ -1401,7 +1405,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // tile); the last batch's successor load fetches the first batch of tile `after` (a valid
     // tile in any case) into v[(E + kBatches) & 1], so every batch's loads, a tile's first
     // included, are in flight while the batch before it is quantized.
-    auto quantize_tile = [&](auto E, int tile, int buf, int after, int ln, int rp, uint4 (&v)[2][kR][4]) {
+    auto quantize_tile = [&](auto E, int tile, int buf, int after, int ln, int rp, uint4 (&v)[2][kR][NV]) {
         constexpr int e = decltype(E)::value;
         asm volatile("" : "+v"(ln));             // re-made opaque per tile: nothing lane-derived is hoisted
         int8_t* Xs = lds + buf * tileBytes;
@@ -1539,7 +1543,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // store offsets are derived per tile rather than hoisted out of the loop as
         // 4 x kRowsPerProducer live registers.
         int ln = lane;
-        uint4 v[2][kR][4];
+        uint4 v[2][kR][NV];
         // Tile i of this workgroup uses buffer i & 1 and enters with parity (i * kBatches) & 1;
         // the loop is unrolled by two so both are compile-time.
         using P0 = std::integral_constant<int, 0>;
@@ -1671,22 +1675,22 @@ static bool fq_pays(int M, int K, int N) {
     return N % 256 != 0 || K >= 2048;
 }
 
-template <int NBW, int BT, bool PACKED>
+template <int NBW, int BT, bool PACKED, int NV>
 static int launch_fq_kernel(const uint16_t* x, const int8_t* W, const uint32_t* meta, const uint16_t* w_scale,
                             const uint16_t* bias, uint16_t* out, int M, int K, int N, int cu, hipStream_t s)
 {
     const size_t lds = fq_lds_bytes(K, N, BT);
     static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&sparse_fq_kernel<NBW, BT, PACKED>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        reinterpret_cast<const void*>(&sparse_fq_kernel<NBW, BT, PACKED, NV>), hipFuncAttributeMaxDynamicSharedMemorySize,
         kFqLds);
     if (attr != hipSuccess) return static_cast<int>(attr);
     const int tiles = divup(M, BT);
     const int grid = std::min(tiles, cu);     // one 8-wave workgroup per CU
-    sparse_fq_kernel<NBW, BT, PACKED><<<grid, 512, lds, s>>>(x, W, meta, w_scale, bias, out, M, K, N, tiles);
+    sparse_fq_kernel<NBW, BT, PACKED, NV><<<grid, 512, lds, s>>>(x, W, meta, w_scale, bias, out, M, K, N, tiles);
     return launch_status();
 }
 
-template <int NBW, int BT>
+template <int NBW, int BT, int NV>
 static int launch_fq(const uint16_t* x, const int8_t* W_comp, const uint32_t* meta, const uint16_t* w_scale,
                      const uint16_t* bias, uint16_t* out, int M, int K, int N, hipStream_t s)
 {
@@ -1696,33 +1700,50 @@ static int launch_fq(const uint16_t* x, const int8_t* W_comp, const uint32_t* me
     int8_t* pk = static_cast<size_t>(N) * K / 2 <= kFqPackBytes ? fq_pack_slot(s) : nullptr;
     if (!pk) {
         note_route("fused-quantize");
-        return launch_fq_kernel<NBW, BT, false>(x, W_comp, meta, w_scale, bias, out, M, K, N, cu, s);
+        return launch_fq_kernel<NBW, BT, false, NV>(x, W_comp, meta, w_scale, bias, out, M, K, N, cu, s);
     }
     note_route("fused-quantize packed");
     const long long units = static_cast<long long>(N) * (K / 32);
     fq_pack_weights_kernel<<<static_cast<unsigned>(divupll(units, 256)), 256, 0, s>>>(W_comp, pk, N, K);
     if ((st = launch_status()) != FORGE_OK) return st;
-    return launch_fq_kernel<NBW, BT, true>(x, pk, meta, w_scale, bias, out, M, K, N, cu, s);
+    return launch_fq_kernel<NBW, BT, true, NV>(x, pk, meta, w_scale, bias, out, M, K, N, cu, s);
 }
 
-template <int BT>
-static int launch_fq_bt(const uint16_t* x, const int8_t* W_comp, const uint32_t* meta, const uint16_t* w_scale,
-                        const uint16_t* bias, uint16_t* out, int M, int K, int N, hipStream_t s)
+template <int BT, int NV>
+static int launch_fq_nbw(const uint16_t* x, const int8_t* W_comp, const uint32_t* meta, const uint16_t* w_scale,
+                         const uint16_t* bias, uint16_t* out, int M, int K, int N, hipStream_t s)
 {
     // Weight blocks per consumer wave per pass: all of N in one pass up to kMax blocks per wave,
     // several passes of kMax beyond. kMax keeps the accumulators (NBW x BT/16 blocks) and the
     // fragment ring within the 256 registers of a wave at 2 waves per SIMD (no spills).
     constexpr int kMax = BT == 64 ? 4 : (BT == 48 ? 5 : 6);
     const int per_wave = divup(N / 16, 4);
-    if (per_wave <= 1) return launch_fq<1, BT>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
-    if (per_wave <= 2) return launch_fq<2, BT>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
-    if (per_wave <= 3) return launch_fq<3, BT>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
-    if (per_wave <= 4 || kMax == 4) return launch_fq<4, BT>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+    if (per_wave <= 1) return launch_fq<1, BT, NV>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+    if (per_wave <= 2) return launch_fq<2, BT, NV>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+    if (per_wave <= 3) return launch_fq<3, BT, NV>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+    if (per_wave <= 4 || kMax == 4) return launch_fq<4, BT, NV>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
     if constexpr (kMax >= 5) {
-        if (per_wave <= 5 || kMax == 5) return launch_fq<5, BT>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+        if (per_wave <= 5 || kMax == 5)
+            return launch_fq<5, BT, NV>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
     }
-    if constexpr (kMax >= 6) return launch_fq<6, BT>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+    if constexpr (kMax >= 6) return launch_fq<6, BT, NV>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
     return FORGE_EINVAL;
+}
+
+// Vectors per lane (NV) from K: 2 up to K = 1024, 3 up to 1536, 4 up to the 2048 limit. The
+// 64-row tile exists only for K <= 1152 (two tiles in LDS) and the 32-row tile in practice only
+// near K = 2048, so those build the NV values they can meet (a larger NV is always correct).
+template <int BT>
+static int launch_fq_bt(const uint16_t* x, const int8_t* W_comp, const uint32_t* meta, const uint16_t* w_scale,
+                        const uint16_t* bias, uint16_t* out, int M, int K, int N, hipStream_t s)
+{
+    const int nv = K <= 1024 ? 2 : (K <= 1536 ? 3 : 4);
+    if constexpr (BT != 32) {
+        if (nv == 2) return launch_fq_nbw<BT, 2>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+        if (nv == 3) return launch_fq_nbw<BT, 3>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+    }
+    if constexpr (BT != 64) return launch_fq_nbw<BT, 4>(x, W_comp, meta, w_scale, bias, out, M, K, N, s);
+    return FORGE_EINVAL;                         // unreachable: two 64-row tiles need K <= 1152
 }
 
 static int launch_sparse_fq(const uint16_t* x, const int8_t* W_comp, const uint32_t* meta, const uint16_t* w_scale,

@@ -2,7 +2,8 @@
 src/gemm/int8_sparse.cu:250-335, chosen at :1022-1033).
 
 Forced (path 1) over every weight-blocks-per-wave variant (N = 16 .. 528, including a second
-pass with a partial block set), ragged token counts and K from 128 to the 2048 limit, each
+pass with a partial block set), ragged token counts and K from 128 to the 2048 limit (2, 3 and 4
+row vectors per producer lane, each at its largest K and below), each
 bit-exact against the oracle's two-pass composition (quantize rows -> sparse INT32 GEMM ->
 dequant epilogue) and against the library's own two-pass path; the scratch buffers stay
 untouched, as the reference documents (int8_sparse.cuh:87-89), with the weights packed into
@@ -31,7 +32,7 @@ def _prep(dev, W):
 
 @pytest.mark.parametrize("M,K,N,bias", [(65, 128, 16, True), (1, 512, 96, True), (200, 1280, 176, False),
                                         (130, 2048, 256, True), (97, 384, 384, True), (257, 256, 528, True),
-                                        (64, 1280, 320, True)])
+                                        (64, 1280, 320, True), (129, 1152, 64, True), (70, 1536, 112, False)])
 def test_fq_forced_parity(dev, orc, M, K, N, bias):
     import torch
     from forge_amd import ops
