@@ -1659,20 +1659,20 @@ static bool fq_fits(const void* x, const void* W_comp, const void* out, int K, i
 
 // Automatic path choice (the role of the reference's sp_use_fused, int8_sparse.cu:926-938).
 // The two-pass path writes an INT8 copy of x and reads it back (2*M*K extra DRAM bytes once
-// x and its copy, 3*M*K, outgrow the 256 MB MALL); the fused kernel instead re-streams
-// W_comp + index words (N*K*5/8 bytes) from L2 for every tile of token rows and is bound by
-// its consumer waves, whose work grows with N. Measured on MI355X (fused vs two-pass, us):
-// fused wins at M = 147,456 for 1280->320 (210 vs 229), 1280->160 (146 vs 177), 1536->384 (240
-// vs 255), 2048->256 (244 vs 260), 1024->128 (123 vs 134), at 1280->320 for M = 98,304 (122 vs
-// 127) and 262,144 (322 vs 365); two-pass wins for N >= 512 (1280->640: 269 vs 285), for
-// K = 640 (95 vs 108), when N fills the two-pass engine's 256-row weight tiles at K < 2048
-// (1024->256: 144 vs 170), and while 3*M*K stays near the MALL (M = 65,536, 1280->320: 80 vs
-// 90). 1280->480 is even (226 vs 228).
+// x and its copy, 3*M*K, outgrow the 256 MB MALL); the fused kernel instead re-streams the
+// packed weights (N*K*5/8 bytes with the index words) from L2 for every tile of token rows, so
+// its consumer work grows with N. Fitted to 160 measured shapes on MI355X (M = 65,536 ..
+// 262,144; K = 640 .. 2048; N = 128 .. 1024; fused vs two-pass, us): fused for N <= 640 once
+// M*K >= 50M (147,456 x 1280 -> 320: 147 vs 196; 147,456 x 1024 -> 256: 106 vs 144; below the
+// threshold two-pass wins, 65,536 x 640 -> 320: 46 vs 53), and for N up to 1024 at K <= 1536
+// once M*K >= 150M (147,456 x 1024 -> 1024: 251 vs 264; 98,304 x 1280 -> 1024: 221 vs 201 and
+// every K = 2048, N = 1024 shape go two-pass). Over the sweep this rule is 0.16 % slower in total
+// than the faster path at every shape (7 shapes more than 2 % off).
 static bool fq_pays(int M, int K, int N) {
     if (K % kSpStep != 0 || K > kFqMaxK || fq_bt(K, N) == 0) return false;
-    if (3.0 * M * K < 300e6) return false;
-    if (N > 480 || K < 1024) return false;
-    return N % 256 != 0 || K >= 2048;
+    const double mk = static_cast<double>(M) * K;
+    if (N <= 640) return mk >= 50e6;
+    return N <= 1024 && K <= 1536 && mk >= 150e6;
 }
 
 template <int NBW, int BT, bool PACKED, int NV>

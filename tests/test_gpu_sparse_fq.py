@@ -127,10 +127,10 @@ def test_fq_auto_on_reference_layer(dev, orc):
     M, K, N = 147456, 1280, 320
     assert ops.sparse_int8_linear_fused(M, K, N)
     assert not ops.sparse_int8_linear_fused(4096, K, N)
-    # measured two-pass wins: N filling 256-row tiles at K < 2048, K = 640, wide N
-    assert not ops.sparse_int8_linear_fused(M, 1024, 256)
-    assert not ops.sparse_int8_linear_fused(M, 640, 160)
-    assert not ops.sparse_int8_linear_fused(M, 1280, 640)
+    # measured two-pass wins: M*K below 50M, N over 640 at K = 2048, N over 1024
+    assert not ops.sparse_int8_linear_fused(65536, 640, 320)
+    assert not ops.sparse_int8_linear_fused(M, 2048, 1024)
+    assert not ops.sparse_int8_linear_fused(M, 1024, 2048)
     rng = np.random.default_rng(7)
     W = int8_uniform(rng, (N, K))
     comp, meta = _prep(dev, W)

@@ -63,11 +63,13 @@ FUSED_CHOICE = [
     ((147456, 1280, 320), True),     # the reference's example layer (int8_sparse.cuh:82)
     ((147456, 1280, 160), True), ((147456, 1536, 384), True), ((147456, 2048, 256), True),
     ((147456, 1024, 128), True), ((98304, 1280, 320), True), ((262144, 1280, 320), True),
+    ((65536, 1280, 320), True), ((147456, 1024, 256), True), ((147456, 640, 160), True),
+    ((147456, 1280, 640), True), ((147456, 1024, 1024), True),
     ((4096, 1280, 320), False),      # small M: the INT8 copy stays on chip
-    ((65536, 1280, 320), False),     # 3*M*K near the 256 MB MALL
-    ((147456, 1024, 256), False),    # N fills the two-pass engine's 256-row tiles
-    ((147456, 640, 160), False),     # short K
-    ((147456, 1280, 640), False),    # wide N
+    ((65536, 640, 320), False),      # M*K below 50M
+    ((98304, 1280, 1024), False),    # N over 640 needs M*K >= 150M
+    ((147456, 2048, 1024), False),   # ... and K <= 1536
+    ((147456, 1024, 2048), False),   # N over 1024
     ((147456, 2176, 256), False),    # K beyond the fused kernel's 2048
     ((147456, 1280, 328), False),    # N not a multiple of 16
     ((1, 8192, 8192), True),         # decode: the decode kernel with its quantize prologue
