@@ -19,7 +19,7 @@ DENSE = [(1, 128, 32), (3, 1152, 96), (16, 2048, 50), (7, 4096, 200), (16, 1024,
 # K % 256 == 0 runs the register kernel; K % 256 == 128 the DMA-ring kernel.
 SPARSE = [(1, 128, 32), (5, 1152, 48), (16, 2048, 208), (9, 4096, 1024), (16, 1024, 16),
           (1, 256, 32), (5, 1280, 48), (8, 2048, 208), (3, 768, 16), (4, 8192, 1024),
-          (12, 1152, 48), (16, 640, 64), (13, 256, 80)]
+          (12, 1152, 48), (16, 640, 64), (13, 256, 80), (3, 1024, 48), (15, 3072, 96), (2, 2048, 64)]
 
 
 @pytest.mark.parametrize("M,K,N", DENSE)
