@@ -5,7 +5,7 @@
 // rows (H*W, C_in) with the repacked weights (4*C_out, C_in), row co*4 + kh*2 + kw, followed
 // by a scatter to NCHW. The reference runs transpose -> quantize -> GEMM to an FP16 buffer
 // -> scatter + bias, one image at a time. Here, for C_in in {32, 64, 128, 256} and
-// H*W % 8 == 0, convt_fused_kernel does all of it in one pass per 64-pixel tile (described at
+// H*W % 8 == 0, convt_fused_kernel does all of it in one pass per 32-pixel tile (described at
 // the kernel): input read once, INT8 activations kept in LDS, output written once, one launch
 // for all images, no workspace traffic. Every other shape takes two kernels:
 //   1. quantize_pixels_nchw reads the NCHW image once and writes the INT8 pixel rows and
@@ -29,19 +29,22 @@ namespace forge_amd {
 
 static size_t up256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 
-// Single-pass kernel for C_in = 32 * KC (KC = 1, 2, 4, 8), H*W % 8 == 0: one workgroup takes
-// 64 consecutive pixels of one image and writes their whole (C_out, 2x2) output, so the INT8
-// activations never leave the chip and the input is read once.
-//   1. Thread t loads pixels 8*(t%8) .. +8 of channels t/8 + 32k as 16-byte rows (KC loads
+// Single-pass kernel for C_in = 32 * KC (KC = 1, 2, 4, 8), H*W % 8 == 0: one workgroup (2 waves)
+// takes 32 consecutive pixels of one image and writes their whole (C_out, 2x2) output, so the
+// INT8 activations never leave the chip and the input is read once. Tiles of 32 pixels (one MFMA
+// row block) rather than 64 give twice the workgroups, whose load, compute and store phases then
+// overlap across a CU's workgroups instead of running in step (measured (1,64,270,480) -> 32:
+// 22.5 -> 21.1 us; (2,128,128,128) -> 64: 16.0 -> 14.4 us); 128-pixel tiles were slower still.
+//   1. Thread t loads pixels 8*(t%4) .. +8 of channels t/4 + 32k as 16-byte rows (KC loads
 //      in flight; the wave's first MFMA item's weight rows and scales load behind them, later
 //      items one item ahead), takes the per-pixel absmax over its channels on fp16 bit patterns
 //      (one packed u16 maximum per two pixels; the fp32 maximum for a pixel holding a NaN),
-//      then over the wave's 8 channel groups (lane shuffles) and the 4 waves (LDS): the row
+//      then over the wave's 16 channel groups (lane shuffles) and the 2 waves (LDS): the row
 //      arithmetic of quantize_rows on each pixel's C_in values.
-//   2. The quantized pixels form the A tile in LDS (64 x C_in bytes, 16-byte chunks swizzled
+//   2. The quantized pixels form the A tile in LDS (32 x C_in bytes, 16-byte chunks swizzled
 //      by row so the MFMA row reads spread over the banks).
-//   3. Work items (m-block i of 32 pixels, n-block j of 32 GEMM columns) go round-robin to the
-//      4 waves; B fragments are the weight rows, read from L2 straight into registers; K is
+//   3. Work items (n-block j of 32 GEMM columns for the tile's 32 pixels) go round-robin to the
+//      2 waves; B fragments are the weight rows, read from L2 straight into registers; K is
 //      KC steps of v_mfma_i32_32x32x32_i8.
 //   4. A lane's accumulators are one pixel x 4 consecutive columns n = co*4 + (kh, kw): the
 //      2x2 output block of one channel, so the dequant (act_scale * w_scale[co], no bias,
@@ -49,13 +52,13 @@ static size_t up256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 //      (rows 2h and 2h + 1) happen in registers; adjacent lanes are adjacent pixels, so each
 //      store instruction writes 128-byte runs.
 template <int KC>
-__global__ __launch_bounds__(256) void convt_fused_kernel(
+__global__ __launch_bounds__(128) void convt_fused_kernel(
     const uint16_t* __restrict__ x, const int8_t* __restrict__ w, const uint16_t* __restrict__ w_scale,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int HW, int W, int C_out, int tiles)
 {
     constexpr int C = 32 * KC;
     constexpr int kNch = C / 16;
-    constexpr int PT = 64;                           // pixels per tile (128 measured slower)
+    constexpr int PT = 32;                           // pixels per tile
     constexpr int kNW = PT / 16;                     // waves: 4 * PT threads
     constexpr int kPG = PT / 8;                      // 8-pixel groups per tile
     constexpr int kMB = PT / 32;                     // 32-pixel MFMA row blocks
@@ -242,10 +245,10 @@ static int launch_convt_fused(const uint16_t* input, const int8_t* weight, const
                               const uint16_t* bias, uint16_t* output, int N, int HW, int W, int C_out,
                               hipStream_t s)
 {
-    const int tiles = divup(HW, 64);
+    const int tiles = divup(HW, 32);
     const long long blocks = static_cast<long long>(N) * tiles;
     if (blocks > 0x7FFFFFFFLL) return FORGE_EINVAL;
-    convt_fused_kernel<KC><<<static_cast<unsigned>(blocks), 256, 0, s>>>(input, weight, w_scale, bias, output, HW, W,
+    convt_fused_kernel<KC><<<static_cast<unsigned>(blocks), 128, 0, s>>>(input, weight, w_scale, bias, output, HW, W,
                                                                         C_out, tiles);
     return launch_status();
 }
