@@ -1323,7 +1323,7 @@ template <int NBW, int BT, bool PACKED, int NV>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void sparse_fq_kernel(
     const uint16_t* __restrict__ x, const int8_t* __restrict__ W_comp, const uint32_t* __restrict__ meta,
     const uint16_t* __restrict__ w_scale, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out,
-    int M, int K, int N, int tiles)
+    int M, int K, int N, int tiles, int stg)
 {
     constexpr int kTB = BT / 16;                 // 16-token blocks per tile
     constexpr int kRowsPerProducer = BT / 4;
@@ -1335,6 +1335,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     float* sscale = reinterpret_cast<float*>(lds + 2 * tileBytes);          // [2][BT]
     uint16_t* sws = reinterpret_cast<uint16_t*>(sscale + 2 * BT);          // N
     uint16_t* sbias = sws + N;                                              // N
+    // stg: each consumer wave's outputs of a pass go through its own LDS strip (BT rows x NBW
+    // blocks of 16 columns) and leave as 16-byte stores of whole row runs: stored from the
+    // accumulators directly, a lane quad writes 4 different rows, which costs the texture unit
+    // several times the cycles of a contiguous quad (147,456 x 1280 -> 320: the output stores
+    // took 15-17 us of the kernel).
+    constexpr int kStgPitch = NBW * 16;                                     // halves per staged row
+    uint16_t* sstg = reinterpret_cast<uint16_t*>(lds + ((2 * tileBytes + 8 * BT + 4 * N + 15) & ~15));
     const int t = threadIdx.x, lane = t & (kWave - 1), wave = t >> 6;
     const int KS = K / kSpStep, Kc = K / 2, cpr = K / 32, NB = N / 16;
     const bool has_bias = bias != nullptr;
@@ -1501,6 +1508,39 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             for (int d = 0; d < kFqAhead; d++)
                 if (s0 + kFqAhead + d < KS) step(s0 + kFqAhead + d, fa[d], fi[d]);
             // epilogue: lane holds C[16 blk + 4 g + e][16 j + r16]
+            if (stg && wb0 + NBW <= NB) {
+                uint16_t* sw = sstg + cw * (BT * kStgPitch);
+#pragma unroll
+                for (int i = 0; i < NBW; i++) {
+                    const int n = 16 * (wb0 + i) + 4 * g;
+                    float ws[4], bv[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        ws[e] = h2f(sws[n + e]);
+                        bv[e] = h2f(sbias[n + e]);
+                    }
+#pragma unroll
+                    for (int j = 0; j < kTB; j++) {
+                        const float as = sc[16 * j + r16];
+                        uint16_t h[4];
+#pragma unroll
+                        for (int e = 0; e < 4; e++) h[e] = dequant_gemm(acc[i][j][e], as, ws[e], bv[e], has_bias);
+                        *reinterpret_cast<uint2*>(sw + (16 * j + r16) * kStgPitch + 16 * i + 4 * g) =
+                            make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16),
+                                       h[2] | (static_cast<uint32_t>(h[3]) << 16));
+                    }
+                }
+                // The strip is this wave's own and a wave's LDS accesses complete in order, so
+                // the rows can be read back without a barrier.
+                constexpr int kCpr = 2 * NBW;    // 16-byte chunks per staged row
+                for (int q = ln; q < BT * kCpr; q += kWave) {
+                    const int r = q / kCpr, c = q - r * kCpr;
+                    if (m0 + r < M)
+                        *reinterpret_cast<uint4*>(out + static_cast<size_t>(m0 + r) * N + 16 * wb0 + 8 * c) =
+                            *reinterpret_cast<const uint4*>(sw + r * kStgPitch + 8 * c);
+                }
+                continue;
+            }
 #pragma unroll
             for (int i = 0; i < NBW; i++) {
                 const int blk = wb0 + i;
@@ -1679,14 +1719,19 @@ template <int NBW, int BT, bool PACKED, int NV>
 static int launch_fq_kernel(const uint16_t* x, const int8_t* W, const uint32_t* meta, const uint16_t* w_scale,
                             const uint16_t* bias, uint16_t* out, int M, int K, int N, int cu, hipStream_t s)
 {
-    const size_t lds = fq_lds_bytes(K, N, BT);
+    // The output staging strips when they fit beside the token tiles (and the output takes
+    // 16-byte stores).
+    const size_t base = (fq_lds_bytes(K, N, BT) + 15) & ~static_cast<size_t>(15);
+    const size_t strips = 4 * static_cast<size_t>(BT) * NBW * 16 * sizeof(uint16_t);
+    const int stg = aligned(out, 16) && base + strips <= static_cast<size_t>(kFqLds) ? 1 : 0;
+    const size_t lds = stg ? base + strips : fq_lds_bytes(K, N, BT);
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(&sparse_fq_kernel<NBW, BT, PACKED, NV>), hipFuncAttributeMaxDynamicSharedMemorySize,
         kFqLds);
     if (attr != hipSuccess) return static_cast<int>(attr);
     const int tiles = divup(M, BT);
     const int grid = std::min(tiles, cu);     // one 8-wave workgroup per CU
-    sparse_fq_kernel<NBW, BT, PACKED, NV><<<grid, 512, lds, s>>>(x, W, meta, w_scale, bias, out, M, K, N, tiles);
+    sparse_fq_kernel<NBW, BT, PACKED, NV><<<grid, 512, lds, s>>>(x, W, meta, w_scale, bias, out, M, K, N, tiles, stg);
     return launch_status();
 }
 

@@ -91,6 +91,35 @@ def test_fq_weights_in_place(dev, orc):
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
 
 
+def test_fq_output_8_byte_aligned(dev, orc):
+    """An output 8 but not 16 bytes aligned (a view 4 halves into a buffer) takes the per-lane
+    stores instead of the LDS-staged 16-byte row runs: bit-exact against the oracle, and the
+    halves around the view untouched."""
+    import torch
+    from forge_amd import ops
+    M, K, N = 150, 1280, 320
+    rng = np.random.default_rng(808)
+    W = int8_uniform(rng, (N, K))
+    x = rng.uniform(-2.0, 2.0, (M, K)).astype(np.float16)
+    ws = rng.uniform(0.001, 0.05, N).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
+    cr, mr = orc.prune_compress_24(W)
+    qr, sr = orc.quantize_rows(x)
+    ref = orc.dequant_epilogue(orc.sparse_gemm_s32(cr, qr, mr, N, K), sr, ws, b).view(np.uint16)
+    comp, meta = _prep(dev, W)
+    sq = torch.empty((M, K), dtype=torch.int8, device=dev)
+    ss = torch.empty((M,), dtype=torch.float32, device=dev)
+    buf = torch.full((M * N + 8,), 0x5A5A, dtype=torch.int16, device=dev)
+    out = buf[4:4 + M * N].view(torch.float16).view(M, N)
+    assert out.data_ptr() % 16 == 8
+    say(f"fused sparse linear, 8-byte aligned output M={M} K={K} N={N}")
+    ops.sparse_int8_linear(to_dev(x, dev), comp, meta, to_dev(ws, dev), to_dev(b, dev), sq, ss, None, 1, 1, out=out)
+    assert ops.last_route().startswith("fused-quantize")
+    assert np.array_equal(to_host(out).view(np.uint16), ref)
+    h = to_host(buf).view(np.uint16)
+    assert (h[:4] == 0x5A5A).all() and (h[4 + M * N:] == 0x5A5A).all()
+
+
 @pytest.mark.parametrize("M,K,N", [(64, 1280, 320), (101, 512, 96), (48, 2048, 64)])
 def test_fq_special_values(dev, orc, M, K, N):
     """The fused kernel's on-chip quantization on NaN payloads (skipped by the absmax, quantized
