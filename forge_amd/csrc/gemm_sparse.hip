@@ -1340,7 +1340,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // accumulators directly, a lane quad writes 4 different rows, which costs the texture unit
     // several times the cycles of a contiguous quad (147,456 x 1280 -> 320: the output stores
     // took 15-17 us of the kernel).
-    constexpr int kStgPitch = NBW * 16;                                     // halves per staged row
+    constexpr int kStgPitch = NBW * 16 + 8;   // halves per staged row (+16 bytes: rows spread over the banks)
     uint16_t* sstg = reinterpret_cast<uint16_t*>(lds + ((2 * tileBytes + 8 * BT + 4 * N + 15) & ~15));
     const int t = threadIdx.x, lane = t & (kWave - 1), wave = t >> 6;
     const int KS = K / kSpStep, Kc = K / 2, cpr = K / 32, NB = N / 16;
@@ -1631,7 +1631,7 @@ __global__ __launch_bounds__(256) void fq_pack_weights_kernel(const int8_t* __re
 // fused path allocates nothing and leaves the caller's scratch buffers untouched (the
 // reference's contract for it). A launch without a slot, or with weights beyond a slot, reads
 // W_comp in place (same bits).
-constexpr int kFqPackSlots = 8;
+constexpr int kFqPackSlots = 32;   // one per stream and per graph capture, as the decode K split's
 constexpr size_t kFqPackBytes = size_t(1) << 20;   // N * K / 2: 1280 x 1638, 2048 x 1024
 static __device__ __align__(16) int8_t g_fq_pack[kFqPackSlots * kFqPackBytes];
 
@@ -1719,11 +1719,14 @@ template <int NBW, int BT, bool PACKED, int NV>
 static int launch_fq_kernel(const uint16_t* x, const int8_t* W, const uint32_t* meta, const uint16_t* w_scale,
                             const uint16_t* bias, uint16_t* out, int M, int K, int N, int cu, hipStream_t s)
 {
-    // The output staging strips when they fit beside the token tiles (and the output takes
-    // 16-byte stores).
+    // The output staging strips from K = 1024 on, when they fit beside the token tiles and the
+    // output takes 16-byte stores. Measured at M = 147,456 (without -> with, us): 1280 -> 320
+    // 141 -> 136, 2048 -> 256 180 -> 177, 1024 -> 320 even; at K = 640, where the producer's
+    // share of each tile is largest, they cost time (640 -> 320 97.5 -> 99, 640 -> 480 at
+    // M = 98,304 66.4 -> 70.5).
     const size_t base = (fq_lds_bytes(K, N, BT) + 15) & ~static_cast<size_t>(15);
-    const size_t strips = 4 * static_cast<size_t>(BT) * NBW * 16 * sizeof(uint16_t);
-    const int stg = aligned(out, 16) && base + strips <= static_cast<size_t>(kFqLds) ? 1 : 0;
+    const size_t strips = 4 * static_cast<size_t>(BT) * (NBW * 16 + 8) * sizeof(uint16_t);
+    const int stg = K >= 1024 && aligned(out, 16) && base + strips <= static_cast<size_t>(kFqLds) ? 1 : 0;
     const size_t lds = stg ? base + strips : fq_lds_bytes(K, N, BT);
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(&sparse_fq_kernel<NBW, BT, PACKED, NV>), hipFuncAttributeMaxDynamicSharedMemorySize,
