@@ -85,7 +85,8 @@ def traffic_probe() -> int:
     c2 = the configs[1] dequant GEMM (4096^3, FP16 out); c3 sparse / dense = configs[2]
     (4096 x 11008 x 4096, INT32 out) on the 2:4 and the dense engine; c5 = configs[4] NHWC
     conv (INT32 out; 256-row and 192-row tiles in one launch); c4 = configs[3] M = 16 decode GEMMs
-    (N = K = 8192, pre-quantized tokens, FP16 out) dense and 2:4; then a COPY_PROBE_BYTES
+    (N = K = 8192, pre-quantized tokens, FP16 out) dense and 2:4; f1 = the fused quantize + 2:4
+    sparse linear on the reference's example layer (1280 -> 320 at M = 147,456); then a COPY_PROBE_BYTES
     device-to-device copy, the calibration of known size for FETCH_SIZE / WRITE_SIZE."""
     import torch
     import forge_amd
@@ -139,6 +140,19 @@ def traffic_probe() -> int:
     reps("c4_sparse_M16", lambda: ops.sparse_int8_gemm(comp, q16, meta, s16, ws8, b8, out=y16))
     del W, comp, meta
 
+    # the reference's fused-quantize example layer: sparse_int8_linear 1280 -> 320 at M = 147,456
+    M, K, N = 147456, 1280, 320
+    W = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+    comp, meta = _prep_sparse(ops, W)
+    xf = torch.randn((M, K), generator=g, device=dev).half()
+    wsf = (torch.rand((N,), generator=g, device=dev) * 9e-3 + 1e-3).half()
+    bf = (torch.randn((N,), generator=g, device=dev) * 0.1).half()
+    qf = torch.empty((M, K), dtype=torch.int8, device=dev)
+    sf = torch.empty((M,), dtype=torch.float32, device=dev)
+    yf = torch.empty((M, N), dtype=torch.float16, device=dev)
+    reps("f1_fq", lambda: ops.sparse_int8_linear(xf, comp, meta, wsf, bf, qf, sf, None, 1, 1, out=yf))
+    del W, comp, meta, xf, qf, yf
+
     src = torch.empty((COPY_PROBE_BYTES,), dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     src.fill_(1)
@@ -168,6 +182,7 @@ PROBE_KERNELS = {
     "c5_conv": ("gemm_dma_tail_kernel<false, forge_amd::DmaConv>",),
     "c4_dense_M16": ("decode_dense_kernel<true",),
     "c4_sparse_M16": ("decode_sparse_reg_kernel<true",),
+    "f1_fq": ("sparse_fq_kernel<5, 48, true",),
     "copy": ("copyBuffer",),
 }
 _C4_TOK = 16 * 8192
@@ -181,6 +196,8 @@ PROBE_WORK = {
     "c4_dense_M16": (2.0 * 16 * 8192 * 8192, 8192 * 8192 + _C4_TOK + 16 * 8192 * 2 + 8192 * 4 + 16 * 4, 5000.0),
     "c4_sparse_M16": (2.0 * 16 * 8192 * 8192, 8192 * 8192 // 2 + 8192 * 8192 // 8 + _C4_TOK + 16 * 8192 * 2
                       + 8192 * 4 + 16 * 4, 10000.0),
+    "f1_fq": (2.0 * 147456 * 320 * 1280, 2 * 147456 * 1280 + 2 * 147456 * 320 + 320 * 1280 * 5 // 8 + 4 * 320,
+              10000.0),
 }
 SIMDS = 256 * 4          # MI355X: 256 CUs x 4 SIMDs
 XCDS = 8
@@ -295,6 +312,7 @@ PROBE_TITLES = {
     "c5_conv": "configs[4] NHWC conv, INT32 out (`gemm_dma_tail_kernel<false,DmaConv>`: 256- and 192-row tiles, one launch)",
     "c4_dense_M16": "configs[3] M=16 dense decode GEMM (`decode_dense_kernel`)",
     "c4_sparse_M16": "configs[3] M=16 2:4 decode GEMM (`decode_sparse_reg_kernel`)",
+    "f1_fq": "fused quantize + 2:4 sparse linear 1280->320 at M=147,456 (`sparse_fq_kernel<5,48,true,3>`)",
 }
 
 
