@@ -438,9 +438,12 @@ struct SpDmaTile {
 // [32*(l/32), +32) of the 64-deep step, pair q = group q, indexed by nibble q of the lane's
 // own word; B lane l holds token l%32, bytes 0-15 = K [16*(l/32), +16) and bytes 16-31 =
 // K [32 + 16*(l/32), +16); the accumulator is the 32x32 MFMA layout (row = weight).
-struct SpDmaTile32 {
-    static constexpr int BNW = 256, BMT = 256;
-    static constexpr int kTN = 4, kTM = 4;             // 32-row weight / 32-token blocks per wave
+// BMT_ (tokens per tile) is 256, or 192 for the tail wave of sparse_dma32_tail_kernel.
+template <int BMT_>
+struct SpDmaTile32B {
+    static constexpr int BNW = 256, BMT = BMT_;
+    static_assert(BMT % 64 == 0, "two waves of 32-token blocks");
+    static constexpr int kTN = 4, kTM = BMT / 64;      // 32-row weight / 32-token blocks per wave
     static constexpr int kWBytes = BNW * 64;
     static constexpr int kXBytes = BMT * 128;
     static constexpr int kIBytes = BNW / 16 * 256;
@@ -573,9 +576,11 @@ struct SpDmaTile32 {
 // 4 (kt & 1) + 3. Slot reuse: the weights of stages (kt + 2, kt + 3) are issued at stage kt's
 // barrier (kt even); their slot held stages (kt - 2, kt - 1), last read before stage kt - 1's
 // barrier.
-struct SpDmaTile32W {
-    static constexpr int BNW = 256, BMT = 256;
-    static constexpr int kTN = 4, kTM = 4;
+template <int BMT_>
+struct SpDmaTile32WB {
+    static constexpr int BNW = 256, BMT = BMT_;
+    static_assert(BMT % 64 == 0, "two waves of 32-token blocks");
+    static constexpr int kTN = 4, kTM = BMT / 64;
     static constexpr int kWBytes = BNW * 128;          // one weight slot: two stages
     static constexpr int kXBytes = BMT * 128;
     static constexpr int kIBytes = BNW / 16 * 256;
@@ -715,6 +720,9 @@ struct SpDmaTile32W {
     }
 };
 
+using SpDmaTile32 = SpDmaTile32B<256>;
+using SpDmaTile32W = SpDmaTile32WB<256>;
+
 template <bool DEQUANT, class Tile>
 __global__ __launch_bounds__(256) void sparse_dma32_kernel(const int8_t* __restrict__ W, const int8_t* __restrict__ X,
                                                            const uint32_t* __restrict__ meta, GemmEpilogue ep,
@@ -747,6 +755,65 @@ static int launch_sparse_dma32_tile(const int8_t* W, const int8_t* X, const uint
     return launch_status();
 }
 
+// The tail split in one launch: workgroups [0, n1) run the whole waves as 256 x 256 tiles over
+// the first nb1 weight blocks, the rest the remaining weight blocks as one wave of 192-token
+// tiles. configs[2] (4096 x 11008 x 4096): 688 tiles on 256 CUs are 2.69 waves, of which the
+// third runs 69 % full; as 512 tiles + 242 tiles of 192 tokens it takes 2 + ~0.85 tile times.
+template <bool DEQUANT, int BMT2, template <int> class TileT>
+__global__ __launch_bounds__(256) void sparse_dma32_tail_kernel(const int8_t* __restrict__ W,
+                                                                const int8_t* __restrict__ X,
+                                                                const uint32_t* __restrict__ meta, GemmEpilogue ep,
+                                                                int n1, int nb1, int tiles_n, int tiles_m,
+                                                                int tiles_m2, int K)
+{
+    extern __shared__ __align__(16) int8_t lds[];
+    int tn, tm;
+    if (static_cast<int>(blockIdx.x) < n1) {
+        tile_coords(blockIdx.x, nb1, tiles_m, tn, tm);
+        TileT<256> t;
+        t.run(W, X, meta, ep.M, ep.N, K, tn * 256, tm * 256, lds);
+        store_tile<256, 256, DEQUANT>(t.acc, ep, tm * 256, tn * 256, lds);
+    } else {
+        tile_coords(static_cast<int>(blockIdx.x) - n1, tiles_n - nb1, tiles_m2, tn, tm);
+        const int n0 = (nb1 + tn) * 256, m0 = tm * BMT2;
+        TileT<BMT2> t;
+        t.run(W, X, meta, ep.M, ep.N, K, n0, m0, lds);
+        store_tile<BMT2, 256, DEQUANT>(t.acc, ep, m0, n0, lds);
+    }
+}
+
+// Runs the tail split when the grid is more than one wave, not whole waves, its token tiles
+// divide the CU count (so whole waves are whole weight blocks) and the remaining weight blocks
+// fit one wave of 192-token tiles; -1 otherwise.
+template <bool DEQUANT, template <int> class TileT>
+static int launch_sparse_dma32_tail(const int8_t* W, const int8_t* X, const uint32_t* meta, const GemmEpilogue& ep,
+                                    int K, hipStream_t s)
+{
+    constexpr int kTail = 192;
+    int st = FORGE_OK;
+    const int cu = device_info(&st).cu_count;
+    if (st != FORGE_OK || cu <= 0) return -1;
+    const int tiles_n = divup(ep.N, 256), tiles_m = divup(ep.M, 256);
+    const long long tiles = static_cast<long long>(tiles_n) * tiles_m;
+    if (tiles <= cu || tiles % cu == 0 || cu % tiles_m != 0 || ep.M < kTail) return -1;
+    const int nb1 = static_cast<int>((tiles / cu) * cu / tiles_m);
+    const int tiles_m2 = divup(ep.M, kTail);
+    const long long tail = static_cast<long long>(tiles_n - nb1) * tiles_m2;
+    if (nb1 <= 0 || nb1 >= tiles_n || tail > cu) return -1;
+    constexpr int e1 = epilogue_lds_bytes<256, 256, DEQUANT>(), e2 = epilogue_lds_bytes<kTail, 256, DEQUANT>();
+    constexpr int l1 = TileT<256>::kLdsBytes > e1 ? TileT<256>::kLdsBytes : e1;
+    constexpr int l2 = TileT<kTail>::kLdsBytes > e2 ? TileT<kTail>::kLdsBytes : e2;
+    constexpr int lds = l1 > l2 ? l1 : l2;
+    auto kern = sparse_dma32_tail_kernel<DEQUANT, kTail, TileT>;
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (attr != hipSuccess) return static_cast<int>(attr);
+    const int n1 = nb1 * tiles_m;
+    kern<<<static_cast<unsigned>(n1 + tail), 256, lds, s>>>(W, X, meta, ep, n1, nb1, tiles_n, tiles_m, tiles_m2, K);
+    note_route("dma256x256+tail192");
+    return launch_status();
+}
+
 // 256 x 256 SMFMAC engine: 256-deep weight stages (full 128-byte lines) for INT32 outputs when
 // K % 256 == 0 (configs[2]: 175 -> 160 us, measured in one run); the FP16 epilogue's registers
 // do not fit beside them (the kernel spills), so dequantizing outputs keep 128-deep stages.
@@ -754,9 +821,16 @@ template <bool DEQUANT>
 static int launch_sparse_dma32(const int8_t* W, const int8_t* X, const uint32_t* meta, const GemmEpilogue& ep,
                                int K, hipStream_t s)
 {
-    if (!DEQUANT && K % 256 == 0 && static_cast<long long>(ep.N) * (K / 2) < (1LL << 31) &&
-        static_cast<long long>(ep.M) * K < (1LL << 31) && static_cast<long long>(ep.N) * (K / 32) * 4 < (1LL << 31))
-        return launch_sparse_dma32_tile<DEQUANT, SpDmaTile32W>(W, X, meta, ep, K, s);
+    if constexpr (!DEQUANT) {
+        if (K % 256 == 0 && static_cast<long long>(ep.N) * (K / 2) < (1LL << 31) &&
+            static_cast<long long>(ep.M) * K < (1LL << 31) && static_cast<long long>(ep.N) * (K / 32) * 4 < (1LL << 31)) {
+            const int r = launch_sparse_dma32_tail<DEQUANT, SpDmaTile32WB>(W, X, meta, ep, K, s);
+            if (r != -1) return r;
+            return launch_sparse_dma32_tile<DEQUANT, SpDmaTile32W>(W, X, meta, ep, K, s);
+        }
+    }
+    const int r = launch_sparse_dma32_tail<DEQUANT, SpDmaTile32B>(W, X, meta, ep, K, s);
+    if (r != -1) return r;
     return launch_sparse_dma32_tile<DEQUANT, SpDmaTile32>(W, X, meta, ep, K, s);
 }
 

@@ -222,6 +222,41 @@ def test_sparse_auto_engines(dev, orc, M, K, N, tile, engine):
     assert np.array_equal(to_host(Y)[rows].view(np.uint16), ref)
 
 
+# The tail split of the 256 x 256 engines: whole waves of 256 x 256 tiles over the first weight
+# blocks, then the remaining weight blocks as one wave of 192-token tiles (one launch). (1000,
+# 4096, 17904): 280 tiles = 256 + 6 weight blocks x 6 token tiles of 192 (the last 40 rows, the
+# last weight block 240 rows); (512, 4096, 35008): 128 blocks x 2 + 9 x 3. INT32 (256-deep weight
+# stages) and FP16 (128-deep) outputs, every one against the oracle.
+@pytest.mark.parametrize("M,K,N", [(1000, 4096, 17904), (512, 4096, 35008)])
+def test_sparse_256x256_tail_split(dev, orc, M, K, N):
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(M + K + N + 1)
+    W = int8_uniform(rng, (N, K))
+    x = int8_uniform(rng, (M, K))
+    act = rng.uniform(0.001, 0.05, M).astype(np.float32)
+    ws = rng.uniform(0.001, 0.05, N).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
+    cr, mr = orc.prune_compress_24(W)
+    ref = orc.sparse_gemm_s32(cr, x, mr, N, K, threads=orc.cpu_threads())
+    comp, raw, meta = _prep(dev, W)
+    say(f"sparse 256x256 tail split M={M} K={K} N={N}")
+    xd = to_dev(x, dev)
+    C = torch.empty((M, N), dtype=torch.int32, device=dev)
+    poison(C, 0x7B)
+    got = to_host(ops.sparse_int8_gemm_s32(comp, xd, meta, out=C))
+    assert ops.last_route() == "dma256x256+tail192"
+    bad = int((got != ref).sum())
+    assert bad == 0, f"INT32: {bad} of {got.size} outputs differ"
+    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    poison(Y, 0x7B)
+    ops.sparse_int8_gemm(comp, xd, meta, to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev), split_k=0, out=Y)
+    assert ops.last_route() == "dma256x256+tail192"
+    refy = orc.dequant_epilogue(ref, act, ws, b).view(np.uint16)
+    bad = int((to_host(Y).view(np.uint16) != refy).sum())
+    assert bad == 0, f"FP16: {bad} of {Y.numel()} outputs differ"
+
+
 # The 256 x 256 SMFMAC engine with 256-deep weight stages (INT32 out, K % 256 == 0): one and
 # three weight double-stages, ragged token and weight tiles; every output against the oracle.
 # The grid is large enough that the engine choice takes 256 x 256 tiles (checked by route).
