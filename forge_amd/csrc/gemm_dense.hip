@@ -17,6 +17,7 @@
 #include "forge/gemm/int8_dp4a.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace forge_amd {
 
@@ -189,6 +190,60 @@ static int launch_dma_tail_split(const OpA& opa, const DmaRowMajor& opb, const G
     return launch_status();
 }
 
+// The tail split over weight columns in one launch, for grids of several 256-column tiles
+// (configs[2]: 16 x 43 = 688 tiles, 2.69 waves): workgroups [0, n1) run whole waves of 256 x
+// 256 tiles over the first nb1 tile columns (every row tile of them), the rest the remaining
+// columns as one wave of 192-row tiles (3/4 of a tile's work each, ~0.85 of its time): 2.85
+// tile times instead of 3 there. Workgroups start in index order, so each CU takes a 192-row
+// tile as soon as its last 256-row tile ends.
+template <bool DEQUANT>
+__global__ __launch_bounds__(kGemmThreads) void gemm_dma_coltail_kernel(
+    DmaRowMajor opa, DmaRowMajor opb, GemmEpilogue ep, int n1, int nb1, int tiles_m, int tiles_m2, int tiles_n,
+    int K)
+{
+    extern __shared__ __align__(16) int8_t lds[];
+    int tm, tn;
+    const int bid = static_cast<int>(blockIdx.x);
+    if (bid < n1) {
+        tile_coords(bid, tiles_m, nb1, tm, tn);
+        DmaTile<256, 256> t;
+        t.run(opa, opb, K, tm * 256, tn * 256, lds);
+        store_tile<256, 256, DEQUANT>(t.acc, ep, tm * 256, tn * 256, lds);
+    } else {
+        tile_coords(bid - n1, tiles_m2, tiles_n - nb1, tm, tn);
+        const int n0 = (nb1 + tn) * 256;
+        DmaTile<192, 256> t;
+        t.run(opa, opb, K, tm * 192, n0, lds);
+        store_tile<192, 256, DEQUANT>(t.acc, ep, tm * 192, n0, lds);
+    }
+}
+
+// Runs the column tail split when the grid is more than one wave, not whole waves, its row
+// tiles divide the CU count (so the first columns make whole waves) and the remaining columns'
+// 192-row tiles fit one wave. Returns -1 when it does not apply.
+template <bool DEQUANT>
+static int launch_dma_col_tail(const DmaRowMajor& opa, const DmaRowMajor& opb, const GemmEpilogue& ep, int M, int N,
+                               int K, int cu, hipStream_t s)
+{
+    const int tiles_m = divup(M, 256), tiles_n = divup(N, 256);
+    const long long tiles = static_cast<long long>(tiles_m) * tiles_n;
+    if (tiles <= cu || tiles % cu == 0 || cu % tiles_m != 0 || M < 192 || ep.up_w != 0) return -1;
+    const int nb1 = static_cast<int>(tiles / cu * cu / tiles_m);
+    const int tiles_m2 = divup(M, 192);
+    if (nb1 >= tiles_n || static_cast<long long>(tiles_n - nb1) * tiles_m2 > cu) return -1;
+    const int n1 = nb1 * tiles_m;
+    const int total = n1 + (tiles_n - nb1) * tiles_m2;
+    constexpr int l1 = tile_lds_bytes<DmaTile<256, 256>, 256, 256, DEQUANT>();
+    constexpr int l2 = tile_lds_bytes<DmaTile<192, 256>, 192, 256, DEQUANT>();
+    constexpr int lds = l1 > l2 ? l1 : l2;
+    auto kern = gemm_dma_coltail_kernel<DEQUANT>;
+    static const int attr = allow_lds(kern, lds);
+    if (attr != FORGE_OK) return attr;
+    gemm_dma_coltail_kernel<DEQUANT><<<static_cast<unsigned>(total), kGemmThreads, lds, s>>>(
+        opa, opb, ep, n1, nb1, tiles_m, tiles_m2, tiles_n, K);
+    return launch_status();
+}
+
 template <class OpA>
 static int dispatch_dma(const OpA& opa, const DmaRowMajor& opb, const GemmEpilogue& ep, int M, int N, int K,
                         hipStream_t s)
@@ -202,9 +257,14 @@ static int dispatch_dma(const OpA& opa, const DmaRowMajor& opb, const GemmEpilog
     const bool out16 = ep.c16 != nullptr;
     if (t == TileCfg::k256) {
         note_route("dma256x256+tail192");
-        const int r = out16 ? launch_dma_tail_split<true>(opa, opb, ep, M, N, K, cu, s)
-                            : launch_dma_tail_split<false>(opa, opb, ep, M, N, K, cu, s);
+        int r = out16 ? launch_dma_tail_split<true>(opa, opb, ep, M, N, K, cu, s)
+                      : launch_dma_tail_split<false>(opa, opb, ep, M, N, K, cu, s);
         if (r != -1) return r;
+        if constexpr (std::is_same<OpA, DmaRowMajor>::value) {
+            r = out16 ? launch_dma_col_tail<true>(opa, opb, ep, M, N, K, cu, s)
+                      : launch_dma_col_tail<false>(opa, opb, ep, M, N, K, cu, s);
+            if (r != -1) return r;
+        }
         note_route("dma256x256");
         return out16 ? launch_dma<256, 256, true>(opa, opb, ep, M, N, K, s) : launch_dma<256, 256, false>(opa, opb, ep, M, N, K, s);
     }

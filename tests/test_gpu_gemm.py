@@ -156,3 +156,36 @@ def test_gemm_tail_split(dev, orc, N):
     ops.int8_gemm_dequant(Ad, Bd, to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev), out=Y)
     refy = orc.dequant_epilogue(ref, act[rows], ws, b)
     assert np.array_equal(to_host(Y)[rows].view(np.uint16), refy.view(np.uint16))
+
+
+@pytest.mark.parametrize("M,K,N", [(1000, 1024, 17900), (512, 1024, 35000), (4096, 4096, 11008)])
+def test_gemm_column_tail_split(dev, orc, M, K, N):
+    """Grids of several 256-column tiles that are more than one wave but not whole waves: whole
+    waves of 256 x 256 tiles over the first tile columns, the remaining columns as one wave of
+    192-row tiles, in one launch. (1000, 1024, 17900): 280 tiles = 64 columns x 4 + 6 x 6
+    (ragged rows and last column); (512, 1024, 35000): 128 x 2 + 9 x 3; (4096, 4096, 11008):
+    configs[2]'s shape, 32 x 16 + 11 x 22. Every INT32 and FP16 output against the oracle."""
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(M + K + N + 3)
+    A = int8_uniform(rng, (M, K))
+    B = int8_uniform(rng, (N, K))
+    ref = orc.gemm_s32(A, B, threads=orc.cpu_threads())
+    say(f"gemm column tail split M={M} K={K} N={N}")
+    Ad, Bd = to_dev(A, dev), to_dev(B, dev)
+    out = torch.empty((M, N), dtype=torch.int32, device=dev)
+    poison(out, 0x7B)
+    C = to_host(ops.int8_gemm_s32(Ad, Bd, out=out))
+    assert ops.last_route() == "dma256x256+tail192"
+    bad = int((C != ref).sum())
+    assert bad == 0, f"INT32: {bad} of {C.size} outputs differ"
+    act = rng.uniform(0.001, 0.05, M).astype(np.float32)
+    ws = rng.uniform(0.001, 0.05, N).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
+    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    poison(Y, 0x7B)
+    ops.int8_gemm_dequant(Ad, Bd, to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev), out=Y)
+    assert ops.last_route() == "dma256x256+tail192"
+    refy = orc.dequant_epilogue(ref, act, ws, b).view(np.uint16)
+    bad = int((to_host(Y).view(np.uint16) != refy).sum())
+    assert bad == 0, f"FP16: {bad} of {Y.numel()} outputs differ"
