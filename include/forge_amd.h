@@ -76,8 +76,9 @@ int forge_ksplit_reset(void* stream);
 
 /* The engine of the calling thread's last GEMM launch made through this library (no
  * counterpart in the reference; its benchmark prints the plan it computes itself,
- * benchmarks/bench_int8_sparse.cu:164-170): e.g. "dma256x256", "ring64x64", "decode",
- * "decode+quantize", "token-block", "fused-quantize", "regstaged tile1 s3"
+ * benchmarks/bench_int8_sparse.cu:164-170): e.g. "dma256x256", "dma256x256+tail192"
+ * (whole waves of 256 x 256 tiles, then one wave of 192-row tiles, in one launch),
+ * "ring64x64", "decode", "decode+quantize", "token-block", "fused-quantize", "regstaged tile1 s3"
  * (tile = the reference's kSparseTile* index, s = split-K parts). "none" before any launch.
  * The string belongs to the library and stays valid until the thread's next GEMM call. */
 const char* forge_last_route(void);
