@@ -189,3 +189,8 @@ def test_gemm_column_tail_split(dev, orc, M, K, N):
     refy = orc.dequant_epilogue(ref, act, ws, b).view(np.uint16)
     bad = int((to_host(Y).view(np.uint16) != refy).sum())
     assert bad == 0, f"FP16: {bad} of {Y.numel()} outputs differ"
+    poison(Y, 0x5A)
+    ops.int8_gemm_dequant(Ad, Bd, to_dev(act, dev), to_dev(ws, dev), None, out=Y)
+    refy = orc.dequant_epilogue(ref, act, ws, None).view(np.uint16)
+    bad = int((to_host(Y).view(np.uint16) != refy).sum())
+    assert bad == 0, f"FP16 without bias: {bad} of {Y.numel()} outputs differ"

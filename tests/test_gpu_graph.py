@@ -155,6 +155,45 @@ def test_graph_sparse_splitk(dev):
         _replay_check(dev, calls, [y])
 
 
+def test_graph_tail_splits(dev):
+    """The one-launch tail splits of the 256 x 256 engines (whole tile waves, then one wave of
+    192-row tiles): dense over weight columns (512 x 1024 x 35000: 128 x 2 + 9 x 3 tiles) and
+    2:4 sparse (512 x 4096 x 35008), INT32 and FP16 out."""
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(31)
+    M, K, N = 512, 1024, 35000
+    say(f"graph dense column tail M={M} K={K} N={N}")
+    A = to_dev(int8_uniform(rng, (M, K)), dev)
+    B = to_dev(int8_uniform(rng, (N, K)), dev)
+    act = to_dev(rng.uniform(1e-3, 5e-2, M).astype(np.float32), dev)
+    ws = to_dev(rng.uniform(1e-3, 1e-2, N).astype(np.float16), dev)
+    b = to_dev(fp16_normal(rng, (N,), 0.1), dev)
+    c = torch.empty((M, N), dtype=torch.int32, device=dev)
+    y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    calls = [lambda: ops.int8_gemm_s32(A, B, out=c), lambda: ops.int8_gemm_dequant(A, B, act, ws, b, out=y)]
+    _replay_check(dev, calls, [c, y])
+    assert ops.last_route() == "dma256x256+tail192"
+    M, K, N = 512, 4096, 35008
+    say(f"graph sparse tail M={M} K={K} N={N}")
+    W = to_dev(int8_uniform(rng, (N, K)), dev)
+    comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+    raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+    meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+    ops.prune_compress_24(W, comp, raw, N, K)
+    ops.pack_metadata(raw, meta, N, K)
+    x = to_dev(int8_uniform(rng, (M, K)), dev)
+    act = to_dev(rng.uniform(1e-3, 5e-2, M).astype(np.float32), dev)
+    ws = to_dev(rng.uniform(1e-3, 1e-2, N).astype(np.float16), dev)
+    b = to_dev(fp16_normal(rng, (N,), 0.1), dev)
+    c = torch.empty((M, N), dtype=torch.int32, device=dev)
+    y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    calls = [lambda: ops.sparse_int8_gemm_s32(comp, x, meta, out=c),
+             lambda: ops.sparse_int8_gemm(comp, x, meta, act, ws, b, split_k=0, out=y)]
+    _replay_check(dev, calls, [c, y])
+    assert ops.last_route() == "dma256x256+tail192"
+
+
 def test_graph_sparse_fq(dev):
     """The fused quantize + sparse linear with its weight-packing launch: the capture packs into
     a slot of its own (distinct from the eager slot of the capture stream)."""

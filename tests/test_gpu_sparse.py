@@ -255,6 +255,12 @@ def test_sparse_256x256_tail_split(dev, orc, M, K, N):
     refy = orc.dequant_epilogue(ref, act, ws, b).view(np.uint16)
     bad = int((to_host(Y).view(np.uint16) != refy).sum())
     assert bad == 0, f"FP16: {bad} of {Y.numel()} outputs differ"
+    poison(Y, 0x5A)
+    ops.sparse_int8_gemm(comp, xd, meta, to_dev(act, dev), to_dev(ws, dev), None, split_k=0, out=Y)
+    assert ops.last_route() == "dma256x256+tail192"
+    refy = orc.dequant_epilogue(ref, act, ws, None).view(np.uint16)
+    bad = int((to_host(Y).view(np.uint16) != refy).sum())
+    assert bad == 0, f"FP16 without bias: {bad} of {Y.numel()} outputs differ"
 
 
 # The 256 x 256 SMFMAC engine with 256-deep weight stages (INT32 out, K % 256 == 0): one and
