@@ -148,6 +148,32 @@ __device__ __forceinline__ float block_row_scale(float amax, uint16_t* w_scale, 
     return scale;
 }
 
+// Chunk c (32 values) of weight row n: quantized with the row's scale, pruned 2:4, its 16
+// compressed bytes and gfx950 index word stored.
+__device__ __forceinline__ void prep_chunk(int8_t* __restrict__ comp, uint32_t* __restrict__ meta, int n, int c,
+                                           int N, int K, const float (&v)[32], float scale)
+{
+    const int cpr = K / 32;
+    uint32_t cw[4] = {0u, 0u, 0u, 0u};
+    uint32_t word = 0;
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+        int8_t q[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) q[i] = quant_weight(v[4 * g + i], scale);
+        int8_t c0, c1;
+        uint8_t nib;
+        prune4(q, c0, c1, nib);
+        const uint32_t pair = static_cast<uint32_t>(static_cast<uint8_t>(c0)) |
+                              (static_cast<uint32_t>(static_cast<uint8_t>(c1)) << 8);
+        cw[g >> 1] |= pair << (16 * (g & 1));
+        word |= static_cast<uint32_t>(nib) << (4 * g);
+    }
+    *reinterpret_cast<uint4*>(comp + static_cast<size_t>(n) * (K / 2) + 16 * static_cast<size_t>(c)) =
+        make_uint4(cw[0], cw[1], cw[2], cw[3]);
+    meta[meta_pos(n, c, N, cpr)] = word;
+}
+
 template <bool F16>
 __global__ __launch_bounds__(256) void prepare_sparse_weight_kernel(
     const void* __restrict__ w, int8_t* __restrict__ comp, uint32_t* __restrict__ meta,
@@ -157,6 +183,19 @@ __global__ __launch_bounds__(256) void prepare_sparse_weight_kernel(
     const int cpr = K / 32;
     const size_t row = static_cast<size_t>(n) * K;
     float amax = 0.0f;
+    if (cpr <= 256) {
+        // At most one chunk per thread (K <= 8192): it stays in registers between the row
+        // absmax and the quantization, so the row is read once.
+        float v[32];
+        if (t < cpr) {
+            wload32<F16>(w, row + 32 * static_cast<size_t>(t), v);
+#pragma unroll
+            for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+        }
+        const float scale = block_row_scale(amax, w_scale, n);
+        if (t < cpr) prep_chunk(comp, meta, n, t, N, K, v, scale);
+        return;
+    }
     for (int c = t; c < cpr; c += 256) {
         float v[32];
         wload32<F16>(w, row + 32 * static_cast<size_t>(c), v);
@@ -167,25 +206,35 @@ __global__ __launch_bounds__(256) void prepare_sparse_weight_kernel(
     for (int c = t; c < cpr; c += 256) {
         float v[32];
         wload32<F16>(w, row + 32 * static_cast<size_t>(c), v);
-        uint32_t cw[4] = {0u, 0u, 0u, 0u};
-        uint32_t word = 0;
-#pragma unroll
-        for (int g = 0; g < 8; g++) {
-            int8_t q[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) q[i] = quant_weight(v[4 * g + i], scale);
-            int8_t c0, c1;
-            uint8_t nib;
-            prune4(q, c0, c1, nib);
-            const uint32_t pair = static_cast<uint32_t>(static_cast<uint8_t>(c0)) |
-                                  (static_cast<uint32_t>(static_cast<uint8_t>(c1)) << 8);
-            cw[g >> 1] |= pair << (16 * (g & 1));
-            word |= static_cast<uint32_t>(nib) << (4 * g);
-        }
-        *reinterpret_cast<uint4*>(comp + static_cast<size_t>(n) * (K / 2) + 16 * static_cast<size_t>(c)) =
-            make_uint4(cw[0], cw[1], cw[2], cw[3]);
-        meta[meta_pos(n, c, N, cpr)] = word;
+        prep_chunk(comp, meta, n, c, N, K, v, scale);
     }
+}
+
+// Rows of at most 128 chunks (K <= 4096): two rows per workgroup, 128 threads (two waves) per
+// row, one chunk per thread held in registers between the row absmax and the quantization.
+template <bool F16>
+__global__ __launch_bounds__(256) void prepare_sparse_weight2_kernel(
+    const void* __restrict__ w, int8_t* __restrict__ comp, uint32_t* __restrict__ meta,
+    uint16_t* __restrict__ w_scale, int N, int K)
+{
+    __shared__ float red[4];
+    const int t = threadIdx.x, wave = t / kWave, c = t & 127;
+    const int n = 2 * blockIdx.x + (t >> 7);
+    const int cpr = K / 32;
+    const bool on = n < N && c < cpr;
+    float v[32];
+    float amax = 0.0f;
+    if (on) {
+        wload32<F16>(w, static_cast<size_t>(n) * K + 32 * static_cast<size_t>(c), v);
+#pragma unroll
+        for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+    }
+    amax = wave_max(amax);
+    if ((t & (kWave - 1)) == 0) red[wave] = amax;
+    __syncthreads();
+    const float scale = row_scale(fmaxf(red[wave & ~1], red[wave | 1]));
+    if (c == 0 && n < N) w_scale[n] = f2h(scale);
+    if (on) prep_chunk(comp, meta, n, c, N, K, v, scale);
 }
 
 template <bool F16>
@@ -301,7 +350,14 @@ extern "C" int forge_prepare_sparse_weight(const void* w, int w_fp16, int8_t* W_
         !aligned(w_meta, 4))
         return FORGE_EINVAL;
     hipStream_t s = as_stream(stream);
-    if (w_fp16) prepare_sparse_weight_kernel<true><<<N, 256, 0, s>>>(w, W_comp, w_meta, w_scale, N, K);
-    else        prepare_sparse_weight_kernel<false><<<N, 256, 0, s>>>(w, W_comp, w_meta, w_scale, N, K);
+    if (K / 32 <= 128) {
+        const unsigned g2 = static_cast<unsigned>((N + 1) / 2);
+        if (w_fp16) prepare_sparse_weight2_kernel<true><<<g2, 256, 0, s>>>(w, W_comp, w_meta, w_scale, N, K);
+        else        prepare_sparse_weight2_kernel<false><<<g2, 256, 0, s>>>(w, W_comp, w_meta, w_scale, N, K);
+    } else if (w_fp16) {
+        prepare_sparse_weight_kernel<true><<<N, 256, 0, s>>>(w, W_comp, w_meta, w_scale, N, K);
+    } else {
+        prepare_sparse_weight_kernel<false><<<N, 256, 0, s>>>(w, W_comp, w_meta, w_scale, N, K);
+    }
     return launch_status();
 }
