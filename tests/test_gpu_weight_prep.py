@@ -20,7 +20,8 @@ def _weights(rng, N, K, f16):
     return w.astype(np.float16) if f16 else w
 
 
-@pytest.mark.parametrize("N,K,f16", [(64, 256, False), (33, 100, False), (7, 4097, True), (128, 1024, True)])
+@pytest.mark.parametrize("N,K,f16", [(64, 256, False), (33, 100, False), (7, 4097, True), (128, 1024, True),
+                                     (11, 4096, False), (9, 4112, True), (5, 48, True)])
 def test_quantize_weight_rows(dev, orc, N, K, f16):
     from forge_amd import ops
     rng = np.random.default_rng(N * 7 + K)
