@@ -219,7 +219,15 @@ __global__ __launch_bounds__(256) void prepare_sparse_weight2_kernel(
 {
     __shared__ float red[4];
     const int t = threadIdx.x, wave = t / kWave, c = t & 127;
-    const int n = 2 * blockIdx.x + (t >> 7);
+    // Row pair of this workgroup. With N % 128 == 0 the 8 pairs of each 16-row block go to
+    // workgroups of one XCD (workgroup ids are dealt round-robin over the 8 XCDs), so the
+    // block's interleaved index words (16 rows per 256-byte group) meet in one L2.
+    int pair = static_cast<int>(blockIdx.x);
+    if (N % 128 == 0) {
+        const int xcd = pair & 7, k = pair >> 3;
+        pair = 8 * (8 * (k >> 3) + xcd) + (k & 7);
+    }
+    const int n = 2 * pair + (t >> 7);
     const int cpr = K / 32;
     const bool on = n < N && c < cpr;
     float v[32];

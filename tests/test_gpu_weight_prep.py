@@ -34,7 +34,8 @@ def test_quantize_weight_rows(dev, orc, N, K, f16):
 
 
 @pytest.mark.parametrize("N,K,f16", [(48, 256, False), (16, 64, True), (37, 1280, False), (5, 8192, True),
-                                     (300, 96, False), (3, 16384, False), (2, 8256, True)])
+                                     (300, 96, False), (3, 16384, False), (2, 8256, True), (256, 1024, False),
+                                     (1152, 4096, True)])
 def test_prepare_sparse_weight(dev, orc, N, K, f16):
     from forge_amd import ops
     rng = np.random.default_rng(N * 5 + K)
