@@ -38,6 +38,32 @@ def test_prune_golden(dev):
     assert np.array_equal(to_host(comp), g["comp"]) and np.array_equal(to_host(raw), g["nibbles"])
 
 
+
+def test_prune_every_tie_pattern(dev, orc):
+    """Every group of 4 drawn from a tie-rich alphabet (magnitudes 0-3, 127 and 128 with both
+    signs: 10^4 groups) through the vector and the exported per-group kernels, against the
+    oracle's restatement of the reference's strict-< scan (prune_compress.cu:39-50)."""
+    import itertools
+    import torch
+    from forge_amd import ops
+    vals = [-128, -127, -3, -2, -1, 0, 1, 2, 3, 127]
+    groups = np.array(list(itertools.product(vals, repeat=4)), dtype=np.int8)    # 10,000 x 4
+    W = groups.reshape(625, 64)                                                   # K % 16 == 0
+    comp_ref, nib_ref = orc.prune_compress_24(W)
+    say("prune every tie pattern 625x64")
+    N, K = W.shape
+    comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
+    raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
+    ops.prune_compress_24(to_dev(W, dev), comp, raw, N, K)
+    assert np.array_equal(to_host(comp), comp_ref) and np.array_equal(to_host(raw), nib_ref)
+    W2 = groups                                                                   # K = 4: per-group kernel
+    comp_ref2, nib_ref2 = orc.prune_compress_24(W2)
+    comp2 = torch.empty((10000, 2), dtype=torch.int8, device=dev)
+    raw2 = torch.empty((10000,), dtype=torch.uint8, device=dev)
+    ops.prune_compress_24(to_dev(W2, dev), comp2, raw2, 10000, 4)
+    assert np.array_equal(to_host(comp2), comp_ref2) and np.array_equal(to_host(raw2), nib_ref2)
+
+
 @pytest.mark.parametrize("N,K", [(32, 128), (11008, 4096), (7, 20), (48, 1040)])
 def test_prune_random(dev, orc, N, K):
     import torch
