@@ -69,6 +69,33 @@ __global__ __launch_bounds__(256) void prune_compress_vec_kernel(
     }
 }
 
+// forge_pack_metadata's kernel: one thread per packed word in output order, so each store
+// instruction writes 256 contiguous bytes (the gfx950 layout interleaves 16 rows, and walking it
+// in input order scatters 4-byte stores 64 bytes apart). Word o of 16-row block b is chunk
+// c = o' / rows of row 16b + o' % rows (o' = o - 16 b cpr; rows = 16 except in a last partial
+// block); its 8 nibble bytes are one 8-byte load. N * K / 32 < 2^31 (the host checks).
+__global__ __launch_bounds__(256) void pack_metadata_out_kernel(const uint8_t* __restrict__ raw,
+                                                                uint32_t* __restrict__ packed, int N, int K)
+{
+    const int cpr = K / 32;
+    const int total = N * cpr;
+    const int o = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+    if (o >= total) return;
+    const int per_blk = 16 * cpr;
+    const int blk = o / per_blk;
+    const int rows = min(16, N - 16 * blk);
+    const int oi = o - blk * per_blk;
+    const int c = oi / rows, n = 16 * blk + (oi - c * rows);
+    const uint2 r = *reinterpret_cast<const uint2*>(raw + static_cast<size_t>(n) * (K / 4) + static_cast<size_t>(c) * 8);
+    uint32_t w = 0;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        w |= ((r.x >> (8 * g)) & 0xFu) << (4 * g);
+        w |= ((r.y >> (8 * g)) & 0xFu) << (4 * (g + 4));
+    }
+    packed[o] = w;
+}
+
 __global__ __launch_bounds__(256) void unpack_metadata_kernel(
     const uint32_t* __restrict__ packed, uint8_t* __restrict__ raw, int N, int K)
 {
@@ -366,8 +393,13 @@ extern "C" int forge_pack_metadata(const uint8_t* meta_raw, uint32_t* meta_packe
     if (N <= 0 || K <= 0) return FORGE_OK;
     if (!meta_raw || !meta_packed || K % 32 != 0) return FORGE_EINVAL;
     const long long total = static_cast<long long>(N) * (K / 32);
-    forge::sparsity::pack_metadata_kernel<<<static_cast<unsigned>(divupll(total, 256)), 256, 0,
-                                            as_stream(stream)>>>(meta_raw, meta_packed, N, K);
+    if (total < (1LL << 31) && aligned(meta_raw, 8)) {
+        pack_metadata_out_kernel<<<static_cast<unsigned>(divupll(total, 256)), 256, 0, as_stream(stream)>>>(
+            meta_raw, meta_packed, N, K);
+    } else {
+        forge::sparsity::pack_metadata_kernel<<<static_cast<unsigned>(divupll(total, 256)), 256, 0,
+                                                as_stream(stream)>>>(meta_raw, meta_packed, N, K);
+    }
     return launch_status();
 }
 

@@ -95,6 +95,21 @@ def test_pack_golden_and_roundtrip(dev, which):
     assert np.array_equal(to_host(back), raw)
 
 
+@pytest.mark.parametrize("N,K", [(37, 4096), (11008, 256), (5, 32)])
+def test_pack_random_vs_oracle(dev, orc, N, K):
+    """Random raw nibbles (one byte per group, values 0-15) packed into the gfx950 word order;
+    (37, 4096): two whole 16-row blocks and a 5-row one; (5, 32): one partial block."""
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(N * 3 + K)
+    raw = rng.integers(0, 16, N * K // 4).astype(np.uint8)
+    say(f"pack random N={N} K={K}")
+    meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)
+    poison(meta, 0x7B)
+    ops.pack_metadata(to_dev(raw, dev), meta, N, K)
+    assert np.array_equal(to_host(meta).view(np.uint32), orc.pack_metadata_gfx950(raw, N, K))
+
+
 # tests/test_int8_sparse_gemm.cu:275-284
 REF_SHAPES = [(1, 64, 16), (32, 128, 64), (37, 192, 208), (100, 640, 272), (300, 1280, 384),
               (1000, 1536, 512), (2050, 512, 400), (129, 4096, 96)]
