@@ -259,6 +259,28 @@ __global__ __launch_bounds__(256) void splitk_reduce_f32_kernel(
     }
 }
 
+// Four columns per thread (N % 4 == 0, 16-byte workspace, 8-byte out and bias, M * N / 4 <
+// 2^31): the same sums as splitk_reduce_f32_kernel, one 16-byte load, one 8-byte bias load and
+// one 8-byte store per thread.
+__global__ __launch_bounds__(256) void splitk_reduce_vec4_kernel(
+    const float4* __restrict__ ws, const uint16_t* __restrict__ bias, uint2* __restrict__ out, int n4, int total4)
+{
+    const int stride = static_cast<int>(gridDim.x) * 256;
+    for (int i = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x); i < total4; i += stride) {
+        const float4 f = ws[i];
+        float v[4] = {f.x, f.y, f.z, f.w};
+        if (bias) {
+            const int n = (i - (i / n4) * n4) * 4;
+            const uint2 bv = *reinterpret_cast<const uint2*>(bias + n);
+            const uint32_t br[4] = {bv.x & 0xFFFFu, bv.x >> 16, bv.y & 0xFFFFu, bv.y >> 16};
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] += h2f(static_cast<uint16_t>(br[j]));
+        }
+        out[i] = make_uint2(f2h(v[0]) | (static_cast<uint32_t>(f2h(v[1])) << 16),
+                            f2h(v[2]) | (static_cast<uint32_t>(f2h(v[3])) << 16));
+    }
+}
+
 // ---- DMA-fed sparse engine (256 weight rows x BMT tokens, 128-deep dense K stages) -------
 //
 // The operands stream into a 2-slot LDS ring with global_load_lds_dwordx4 (mfma_tile.h):
@@ -1961,6 +1983,15 @@ extern "C" int forge_splitk_reduce(const float* workspace, const uint16_t* bias,
     if (M <= 0 || N_out <= 0) return FORGE_OK;
     if (!workspace || !out) return FORGE_EINVAL;
     const long long total = static_cast<long long>(M) * N_out;
+    if (N_out % 4 == 0 && total / 4 < (1LL << 31) && aligned(workspace, 16) && aligned(out, 8) &&
+        (!bias || aligned(bias, 8))) {
+        const long long total4 = total / 4;
+        const int blocks = static_cast<int>(std::min<long long>(divupll(total4, 256), 16384));
+        splitk_reduce_vec4_kernel<<<blocks, 256, 0, as_stream(stream)>>>(
+            reinterpret_cast<const float4*>(workspace), bias, reinterpret_cast<uint2*>(out), N_out / 4,
+            static_cast<int>(total4));
+        return launch_status();
+    }
     const int blocks = static_cast<int>(std::min<long long>(divupll(total, 256), 8192));
     splitk_reduce_f32_kernel<<<blocks, 256, 0, as_stream(stream)>>>(workspace, bias, out, N_out, total);
     return launch_status();

@@ -229,24 +229,30 @@ __device__ __forceinline__ uint16_t dequant_standalone(int acc, float as, float 
 }
 
 // Vectorised launcher kernel: 4 outputs per thread, grid-stride over the (M,N) range.
+// Four columns per thread: 16 bytes of INT32 sums, the columns' w_scale and bias as one 8-byte
+// load each (N % 4 == 0, 8-byte-aligned vectors), 8 bytes of FP16 out; 32-bit indices
+// (M * N / 4 < 2^31, checked by the host).
 __global__ __launch_bounds__(256) void dequantize_vec4_kernel(
     const int4* __restrict__ acc, const float* __restrict__ act_scale,
     const uint16_t* __restrict__ w_scale, const uint16_t* __restrict__ bias,
-    uint2* __restrict__ out, int N, long long total4)
+    uint2* __restrict__ out, int n4, int total4)
 {
-    const int n4 = N >> 2;
-    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < total4;
-         i += static_cast<long long>(gridDim.x) * blockDim.x) {
-        const int m = static_cast<int>(i / n4);
-        const int n = static_cast<int>(i - static_cast<long long>(m) * n4) * 4;
+    const int stride = static_cast<int>(gridDim.x) * 256;
+    for (int i = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x); i < total4; i += stride) {
+        const int m = i / n4;
+        const int n = (i - m * n4) * 4;
         const int4 a = acc[i];
         const float as = act_scale[m];
+        const uint2 wv = *reinterpret_cast<const uint2*>(w_scale + n);
+        const uint2 bv = bias ? *reinterpret_cast<const uint2*>(bias + n) : make_uint2(0u, 0u);
         const int av[4] = {a.x, a.y, a.z, a.w};
+        const uint32_t wr[4] = {wv.x & 0xFFFFu, wv.x >> 16, wv.y & 0xFFFFu, wv.y >> 16};
+        const uint32_t br[4] = {bv.x & 0xFFFFu, bv.x >> 16, bv.y & 0xFFFFu, bv.y >> 16};
         uint16_t h[4];
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            h[j] = dequant_standalone(av[j], as, h2f(w_scale[n + j]), bias ? h2f(bias[n + j]) : 0.0f,
-                                      bias != nullptr);
+            h[j] = dequant_standalone(av[j], as, h2f(static_cast<uint16_t>(wr[j])),
+                                      bias ? h2f(static_cast<uint16_t>(br[j])) : 0.0f, bias != nullptr);
         out[i] = make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16),
                             h[2] | (static_cast<uint32_t>(h[3]) << 16));
     }
@@ -378,12 +384,13 @@ extern "C" int forge_dequantize_bias(const int32_t* acc, const float* act_scale,
     if (M <= 0 || N <= 0) return FORGE_OK;
     if (!acc || !act_scale || !w_scale || !out) return FORGE_EINVAL;
     hipStream_t s = as_stream(stream);
-    if (N % 4 == 0 && aligned(acc, 16) && aligned(out, 8)) {
-        const long long total4 = static_cast<long long>(M) * (N / 4);
-        const int blocks = static_cast<int>(std::min<long long>(divupll(total4, 256), 8192));
+    const long long total4 = static_cast<long long>(M) * (N / 4);
+    if (N % 4 == 0 && total4 < (1LL << 31) && aligned(acc, 16) && aligned(out, 8) && aligned(w_scale, 8) &&
+        (!bias || aligned(bias, 8))) {
+        const int blocks = static_cast<int>(std::min<long long>(divupll(total4, 256), 16384));
         dequantize_vec4_kernel<<<blocks, 256, 0, s>>>(reinterpret_cast<const int4*>(acc), act_scale,
                                                      w_scale, bias, reinterpret_cast<uint2*>(out),
-                                                     N, total4);
+                                                     N / 4, static_cast<int>(total4));
     } else {
         forge::quant::fused_dequantize_bias_kernel<<<M, 256, 0, s>>>(
             acc, act_scale, reinterpret_cast<const __half*>(w_scale),

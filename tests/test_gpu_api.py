@@ -57,7 +57,8 @@ def test_int8_gemm_dispatch(dev, orc, M, K, N, bias):
     assert np.array_equal(g1, ref)
 
 
-@pytest.mark.parametrize("M,N,bias", [(1, 16, True), (37, 1000, True), (37, 1000, False), (513, 4112, True)])
+@pytest.mark.parametrize("M,N,bias", [(1, 16, True), (37, 1000, True), (37, 1000, False), (513, 4112, True),
+                                      (7, 1002, True)])
 def test_splitk_reduce(dev, orc, M, N, bias):
     import torch
     from forge_amd import ops

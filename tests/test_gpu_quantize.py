@@ -117,7 +117,8 @@ def test_dequant_golden(dev, orc):
     assert np.array_equal(out.view(np.uint16), ref.view(np.uint16))
 
 
-@pytest.mark.parametrize("M,N,bias", [(16, 64, True), (16, 64, False), (33, 63, True), (5, 1000, False)])
+@pytest.mark.parametrize("M,N,bias", [(16, 64, True), (16, 64, False), (33, 63, True), (5, 1000, False),
+                                      (257, 4100, True)])
 def test_dequant_random(dev, orc, M, N, bias):
     import torch
     from forge_amd import ops
