@@ -192,9 +192,12 @@ __global__ __launch_bounds__(128) void convt_fused_kernel(
     }
     __syncthreads();
 
-    // 3./4. MFMA items and the in-register scatter
-    const size_t plane = 4 * static_cast<size_t>(HW);
-    const size_t W2 = 2 * static_cast<size_t>(W);
+    // 3./4. MFMA items and the in-register scatter, stored through a buffer resource over this
+    // image's output (under 2^31 bytes, checked by the host) with 32-bit byte offsets.
+    const uint32_t plane_b = 8u * static_cast<uint32_t>(HW);     // bytes of one output channel
+    const uint32_t row_b = 4u * static_cast<uint32_t>(W);        // bytes of one output row
+    const __amdgpu_buffer_rsrc_t yr =
+        buf_rsrc(y + static_cast<size_t>(img) * C_out * 4 * static_cast<size_t>(HW), plane_b * static_cast<uint32_t>(C_out));
     for (int it = wave; it < items; it += kNW) {
         const int i = it % kMB, j = it / kMB;
         v4i fb[KC];
@@ -220,7 +223,7 @@ __global__ __launch_bounds__(128) void convt_fused_kernel(
         if (row < np) {
             const int p = p0 + row, h = p / W, wc = p - h * W;
             const float as = ascale[row];
-            uint16_t* ybase = y + static_cast<size_t>(img) * C_out * plane + 2 * h * W2 + 2 * wc;
+            const uint32_t pix_b = 2u * static_cast<uint32_t>(h) * row_b + 4u * static_cast<uint32_t>(wc);
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 const int co = 8 * j + 2 * g + hi;     // columns 4co .. 4co + 3
@@ -232,9 +235,9 @@ __global__ __launch_bounds__(128) void convt_fused_kernel(
                     if (has_bias) r = f2h(h2f(r) + bv[g]);
                     hv[q] = r;
                 }
-                uint16_t* o = ybase + co * plane;
-                *reinterpret_cast<uint32_t*>(o) = hv[0] | (hv[1] << 16);        // kh = 0, kw = 0, 1
-                *reinterpret_cast<uint32_t*>(o + W2) = hv[2] | (hv[3] << 16);   // kh = 1
+                const uint32_t off = pix_b + static_cast<uint32_t>(co) * plane_b;
+                __builtin_amdgcn_raw_buffer_store_b32(hv[0] | (hv[1] << 16), yr, off, 0, 0);          // kh = 0
+                __builtin_amdgcn_raw_buffer_store_b32(hv[2] | (hv[3] << 16), yr, off + row_b, 0, 0);  // kh = 1
             }
         }
     }
@@ -275,7 +278,8 @@ extern "C" int forge_int8_conv_transpose2d_k2s2_forward(const uint16_t* input, c
     const long long HW = static_cast<long long>(H) * W;
     if (HW > 0x7FFFFFFFLL || 4LL * C_out > 0x7FFFFFFFLL) return FORGE_EINVAL;
     hipStream_t s = as_stream(stream);
-    if (HW % 8 == 0 && aligned(input, 16) && aligned(weight, 16) && aligned(output, 4)) {
+    if (HW % 8 == 0 && 8LL * C_out * HW < (1LL << 31) && aligned(input, 16) && aligned(weight, 16) &&
+        aligned(output, 4)) {
         const int hw = static_cast<int>(HW);
         switch (C_in) {
             case 32:  return launch_convt_fused<1>(input, weight, w_scale, bias, output, N, hw, W, C_out, s);
