@@ -51,8 +51,15 @@ static size_t up256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 //      rounded to FP16), the bias (added in fp32 and rounded again) and two 4-byte stores
 //      (rows 2h and 2h + 1) happen in registers; adjacent lanes are adjacent pixels, so each
 //      store instruction writes 128-byte runs.
+// Up to 64 input channels the kernel is asked for 6 waves per SIMD: the compiler then keeps the
+// 16 accumulators in VGPRs beside the rest (67 at C_in = 64, 7 waves; 86 registers and 5 waves
+// otherwise), (1,64,270,480)->32 20.5 -> 19.0-19.1 us, (1,32,540,960)->16 33 -> 29.7-30.3 us. At 128
+// and 256 channels that limit spills, so those keep the default.
 template <int KC>
-__global__ __launch_bounds__(128) void convt_fused_kernel(
+constexpr int convt_min_waves() { return KC <= 2 ? 6 : 1; }
+
+template <int KC>
+__global__ __launch_bounds__(128, convt_min_waves<KC>()) void convt_fused_kernel(
     const uint16_t* __restrict__ x, const int8_t* __restrict__ w, const uint16_t* __restrict__ w_scale,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int HW, int W, int C_out, int tiles)
 {
