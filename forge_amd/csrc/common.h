@@ -147,9 +147,12 @@ constexpr uint32_t kHalfInfBits = 0x7C00u;
 // the product to an integer held in the low mantissa bits (round to nearest even, as rintf,
 // for |v| < 2^22), whose low byte is the two's complement int8; a NaN's low byte is 0 (fp16
 // NaN payloads land 13 bits up; the default NaN is 0x7FC00000). The asm keeps the product
-// rounded on its own (a fused multiply-add would round once).
+// rounded on its own (a fused multiply-add would round once). The product is taken as
+// fma(x, inv, +0), which rounds x * inv once just as the plain product does (only the sign of a
+// zero result can differ, and the add erases it): with the fp16 operand widened inside, that is
+// one v_fma_mix_f32 in place of a conversion and a multiply.
 __device__ __forceinline__ uint32_t qrow_bits(uint16_t h, float inv) {
-    float p = h2f(h) * inv;
+    float p = __builtin_fmaf(__half2float(__ushort_as_half(h)), inv, 0.0f);
     asm("" : "+v"(p));
     return __float_as_uint(p + 12582912.0f);
 }
