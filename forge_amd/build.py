@@ -39,6 +39,7 @@ SOURCES = [
     "gemm_skinny.hip",
     "gemm_decode.hip",
     "gemm_sparse.hip",
+    "gemm_sparse_wide.hip",
     "conv.hip",
     "conv_transpose.hip",
     "conv_depthwise.hip",

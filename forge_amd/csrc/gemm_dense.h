@@ -71,6 +71,18 @@ int launch_dense_tb(const int8_t* W, const int8_t* X, const GemmEpilogue& ep, in
 int launch_skinny_tb(const int8_t* W, const uint32_t* meta, const int8_t* X, const GemmEpilogue& ep, int K, int cu,
                      hipStream_t s, int kp = 0);
 
+// Wide-tile 2:4 sparse GEMM with INT32 output (gemm_sparse_wide.hip): 256 tokens x 8-11 32-row
+// weight blocks per tile, every CU the same number of weight blocks per 256-token block, as T
+// tiles. The plan: TB token blocks, c CUs per token block, q blocks per CU (q + 1 for the first r),
+// XCD grouping gt token blocks x gc block runs per XCD (gc = 0: none). Needs K % 512 == 0,
+// N % 16 == 0, M * K, N * K / 2 and M * N * 4 < 2^31, 16-byte aligned operands.
+struct SpWidePlan {
+    int TB, c, q, r, T, gc, gt;
+};
+bool sparse_wide_plan(int M, int N, int K, int cu, SpWidePlan* out);
+int launch_sparse_wide_s32(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, int32_t* C, int M, int K,
+                           int N, const SpWidePlan& p, hipStream_t s);
+
 // Implicit-GEMM NHWC conv through the dense tile engine (conv.hip supplies the geometry).
 int launch_conv_gemm(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep, int Co, bool vec,
                      hipStream_t s);

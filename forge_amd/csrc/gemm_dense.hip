@@ -251,8 +251,12 @@ static int dispatch_dma(const OpA& opa, const DmaRowMajor& opb, const GemmEpilog
     int st = FORGE_OK;
     const int cu = cu_count(&st);
     if (st != FORGE_OK) return st;
-    // both operands as buffer resources with 32-bit offsets
-    if (static_cast<long long>(opb.rows) * K >= (1LL << 31) || static_cast<long long>(M) * K >= (1LL << 31)) return -1;
+    // Both operands as buffer resources with 32-bit offsets. A row-major A is addressed over
+    // M * K bytes; the conv operand over its image, whose size the caller has checked.
+    if (static_cast<long long>(opb.rows) * K >= (1LL << 31)) return -1;
+    if constexpr (std::is_same<OpA, DmaRowMajor>::value) {
+        if (static_cast<long long>(M) * K >= (1LL << 31)) return -1;
+    }
     const TileCfg t = pick_tile(M, N, cu);
     const bool out16 = ep.c16 != nullptr;
     if (t == TileCfg::k256) {
@@ -311,7 +315,10 @@ int launch_conv_gemm(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep,
     // (and the image fits one buffer resource, the taps one 32-bit mask).
     const long long img_bytes = static_cast<long long>(g.rows / (g.Ho * g.Wo)) * g.H * g.W * g.C;
     const int taps = g.K / g.C;
-    if (vec && g.C % kBK == 0 && aligned(w, 16) && img_bytes < (1LL << 31) && taps <= 32) {
+    // The stage split st -> (tap, channel run) divides by the magic multipliers, exact while
+    // stages * cps < 2^32 (udiv_magic's range).
+    if (vec && g.C % kBK == 0 && aligned(w, 16) && img_bytes < (1LL << 31) && taps <= 32 &&
+        static_cast<long long>(K / kBK) * (g.C / kBK) < (1LL << 32)) {
         DmaConv a;
         static_cast<ConvGeom&>(a) = g;
         a.x_bytes = static_cast<uint32_t>(img_bytes);

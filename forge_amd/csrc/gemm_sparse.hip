@@ -261,16 +261,18 @@ __global__ __launch_bounds__(256) void splitk_reduce_f32_kernel(
 
 // Four columns per thread (N % 4 == 0, 16-byte workspace, 8-byte out and bias, M * N / 4 <
 // 2^31): the same sums as splitk_reduce_f32_kernel, one 16-byte load, one 8-byte bias load and
-// one 8-byte store per thread.
+// one 8-byte store per thread. Unsigned index: total4 < 2^31 plus a stride of at most 2^22
+// stays below 2^32, so the last increment cannot wrap.
 __global__ __launch_bounds__(256) void splitk_reduce_vec4_kernel(
-    const float4* __restrict__ ws, const uint16_t* __restrict__ bias, uint2* __restrict__ out, int n4, int total4)
+    const float4* __restrict__ ws, const uint16_t* __restrict__ bias, uint2* __restrict__ out, uint32_t n4,
+    uint32_t total4)
 {
-    const int stride = static_cast<int>(gridDim.x) * 256;
-    for (int i = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x); i < total4; i += stride) {
+    const uint32_t stride = gridDim.x * 256u;
+    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total4; i += stride) {
         const float4 f = ws[i];
         float v[4] = {f.x, f.y, f.z, f.w};
         if (bias) {
-            const int n = (i - (i / n4) * n4) * 4;
+            const uint32_t n = (i - (i / n4) * n4) * 4;
             const uint2 bv = *reinterpret_cast<const uint2*>(bias + n);
             const uint32_t br[4] = {bv.x & 0xFFFFu, bv.x >> 16, bv.y & 0xFFFFu, bv.y >> 16};
 #pragma unroll
@@ -1288,6 +1290,26 @@ static SpEngine sparse_pick_engine(int M, int N, int K, int cu)
     return e;
 }
 
+// Whether the wide-tile engine's plan beats 256 x 256 tiles, by bytes streamed per CU (both
+// engines run at the same LDS-DMA byte rate): a 256-token tile of NJ 32-row blocks moves 32 KB
+// of tokens + 2.5 KB per block each 128-deep stage, a 256 x 256 tile 52 KB; the 256 x 256 grid
+// takes whole tile waves, the last one a 192-token tail wave (~0.85 of a tile) where
+// launch_sparse_dma32_tail applies. Measured at configs[2] (4096 x 11008 x 4096): 2 x 11-block
+// tiles 115 us vs 2.85 tile times of 256 x 256 126 us; at exact 256 x 256 waves with 8-block
+// wide tiles (4096 x 8192) the two are level by bytes, so the 256 x 256 engine keeps them.
+static bool sparse_wide_pays(int M, int N, int cu, const SpWidePlan& p)
+{
+    const int nbmax = p.q + (p.r > 0 ? 1 : 0);
+    const int njmax = divup(nbmax, p.T);
+    const double wide = p.T * (32.0 + 2.5 * njmax) / 52.0;
+    const int tiles_m = divup(M, 256);
+    const long long tiles = static_cast<long long>(divup(N, 256)) * tiles_m;
+    const long long waves = divupll(tiles, cu);
+    const bool tail = tiles > cu && tiles % cu != 0 && cu % tiles_m == 0 && M >= 192;
+    const double d256 = static_cast<double>(waves) - (tail ? 0.15 : 0.0);
+    return wide < 0.95 * d256;
+}
+
 int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, const float* act_scale,
                 const uint16_t* w_scale, const uint16_t* bias, uint16_t* out16, int32_t* out32, int M,
                 int K, int N, int32_t* ws, int split_k, int tile, hipStream_t s)
@@ -1353,6 +1375,14 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
                    : e == SpEngine::kRing  ? "ring64x64"
                    : e == SpEngine::k128x128 ? "dma128x128"
                                              : "dma256x128");
+        // INT32 output where 256 x 256 tiles would run: the wide-tile engine when its per-CU
+        // plan applies (fewer token bytes per output, every CU the same weight blocks).
+        SpWidePlan wp;
+        if (e == SpEngine::k256x256 && !out16 && tile == FORGE_SPARSE_TILE_AUTO &&
+            sparse_wide_plan(M, N, K, cu_count_or_default(), &wp) && sparse_wide_pays(M, N, cu_count_or_default(), wp)) {
+            note_route("wide256", wp.T);
+            return launch_sparse_wide_s32(W_comp, x, meta, out32, M, K, N, wp, s);
+        }
         if (e == SpEngine::k256x256)
             return out16 ? launch_sparse_dma32<true>(W_comp, x, meta, ep, K, s)
                          : launch_sparse_dma32<false>(W_comp, x, meta, ep, K, s);
@@ -1988,8 +2018,8 @@ extern "C" int forge_splitk_reduce(const float* workspace, const uint16_t* bias,
         const long long total4 = total / 4;
         const int blocks = static_cast<int>(std::min<long long>(divupll(total4, 256), 16384));
         splitk_reduce_vec4_kernel<<<blocks, 256, 0, as_stream(stream)>>>(
-            reinterpret_cast<const float4*>(workspace), bias, reinterpret_cast<uint2*>(out), N_out / 4,
-            static_cast<int>(total4));
+            reinterpret_cast<const float4*>(workspace), bias, reinterpret_cast<uint2*>(out),
+            static_cast<uint32_t>(N_out / 4), static_cast<uint32_t>(total4));
         return launch_status();
     }
     const int blocks = static_cast<int>(std::min<long long>(divupll(total, 256), 8192));

@@ -231,16 +231,18 @@ __device__ __forceinline__ uint16_t dequant_standalone(int acc, float as, float 
 // Vectorised launcher kernel: 4 outputs per thread, grid-stride over the (M,N) range.
 // Four columns per thread: 16 bytes of INT32 sums, the columns' w_scale and bias as one 8-byte
 // load each (N % 4 == 0, 8-byte-aligned vectors), 8 bytes of FP16 out; 32-bit indices
-// (M * N / 4 < 2^31, checked by the host).
+// (M * N / 4 < 2^31, checked by the host). The index is unsigned: with total4 < 2^31 and a
+// stride of at most 2^22 (16384 workgroups of 256), i + stride stays below 2^32, so the last
+// increment cannot wrap into the range again.
 __global__ __launch_bounds__(256) void dequantize_vec4_kernel(
     const int4* __restrict__ acc, const float* __restrict__ act_scale,
     const uint16_t* __restrict__ w_scale, const uint16_t* __restrict__ bias,
-    uint2* __restrict__ out, int n4, int total4)
+    uint2* __restrict__ out, uint32_t n4, uint32_t total4)
 {
-    const int stride = static_cast<int>(gridDim.x) * 256;
-    for (int i = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x); i < total4; i += stride) {
-        const int m = i / n4;
-        const int n = (i - m * n4) * 4;
+    const uint32_t stride = gridDim.x * 256u;
+    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total4; i += stride) {
+        const uint32_t m = i / n4;
+        const uint32_t n = (i - m * n4) * 4;
         const int4 a = acc[i];
         const float as = act_scale[m];
         const uint2 wv = *reinterpret_cast<const uint2*>(w_scale + n);
@@ -390,7 +392,7 @@ extern "C" int forge_dequantize_bias(const int32_t* acc, const float* act_scale,
         const int blocks = static_cast<int>(std::min<long long>(divupll(total4, 256), 16384));
         dequantize_vec4_kernel<<<blocks, 256, 0, s>>>(reinterpret_cast<const int4*>(acc), act_scale,
                                                      w_scale, bias, reinterpret_cast<uint2*>(out),
-                                                     N / 4, static_cast<int>(total4));
+                                                     static_cast<uint32_t>(N / 4), static_cast<uint32_t>(total4));
     } else {
         forge::quant::fused_dequantize_bias_kernel<<<M, 256, 0, s>>>(
             acc, act_scale, reinterpret_cast<const __half*>(w_scale),

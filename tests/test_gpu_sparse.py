@@ -210,6 +210,7 @@ def test_config3_full_size(dev, orc):
     out = torch.empty((M, N), dtype=torch.int32, device=dev)
     poison(out, 0x7B)
     C = to_host(ops.sparse_int8_gemm_s32(comp, to_dev(x, dev), meta, out=out))
+    assert ops.last_route() == "wide256 tile2"
     bad = int((C != ref).sum())
     assert bad == 0, f"{bad} of {C.size} outputs differ"
 
@@ -267,9 +268,12 @@ def test_sparse_auto_engines(dev, orc, M, K, N, tile, engine):
 # blocks, then the remaining weight blocks as one wave of 192-token tiles (one launch). (1000,
 # 4096, 17904): 280 tiles = 256 + 6 weight blocks x 6 token tiles of 192 (the last 40 rows, the
 # last weight block 240 rows); (512, 4096, 35008): 128 blocks x 2 + 9 x 3. INT32 (256-deep weight
-# stages) and FP16 (128-deep) outputs, every one against the oracle.
-@pytest.mark.parametrize("M,K,N", [(1000, 4096, 17904), (512, 4096, 35008)])
-def test_sparse_256x256_tail_split(dev, orc, M, K, N):
+# stages) and FP16 (128-deep) outputs, every one against the oracle. With K % 512 == 0 the INT32
+# output takes the wide-tile engine instead (its per-CU plan applies at both shapes); K = 3840
+# keeps the 256 x 256 tail split for INT32 too.
+@pytest.mark.parametrize("M,K,N,route32", [(1000, 4096, 17904, "wide256 tile1"), (512, 4096, 35008, "wide256 tile1"),
+                                           (1000, 3840, 17904, "dma256x256+tail192")])
+def test_sparse_256x256_tail_split(dev, orc, M, K, N, route32):
     import torch
     from forge_amd import ops
     rng = np.random.default_rng(M + K + N + 1)
@@ -286,7 +290,7 @@ def test_sparse_256x256_tail_split(dev, orc, M, K, N):
     C = torch.empty((M, N), dtype=torch.int32, device=dev)
     poison(C, 0x7B)
     got = to_host(ops.sparse_int8_gemm_s32(comp, xd, meta, out=C))
-    assert ops.last_route() == "dma256x256+tail192"
+    assert ops.last_route() == route32
     bad = int((got != ref).sum())
     assert bad == 0, f"INT32: {bad} of {got.size} outputs differ"
     Y = torch.empty((M, N), dtype=torch.float16, device=dev)
