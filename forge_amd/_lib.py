@@ -25,6 +25,7 @@ SIGNATURES = {
     "forge_init": (_I, []),
     "forge_ksplit_last": (_I, [_P, _P]),
     "forge_ksplit_reset": (_I, [_P]),
+    "forge_slots_in_use": (_I, [_P, _P, _P, _P]),
     "forge_last_route": (ctypes.c_char_p, []),
     "forge_get_compute_capability": (_I, [_I, _P]),
     "forge_has_int8_matrix_cores": (_I, [_I, _P]),

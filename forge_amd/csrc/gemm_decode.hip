@@ -883,7 +883,7 @@ __global__ __launch_bounds__(WV * kWave) __attribute__((amdgpu_waves_per_eu(1, 2
 // Measured at M = 16, K = 8192 (128 and 32 row blocks of 32 rows): N = 4096
 // 13.6 -> 9.9 us, N = 1000 13.2 -> 8.8 us. Where the row blocks already fill the chip the split
 // only adds the hand-off (N = 8192: 14.4 -> 15.2 us), so it is not used there.
-constexpr int kKSplitSlots = 32;
+constexpr int kKSplitSlots = kKSplitSlotCount;
 constexpr int kKSplitMaxBlocks = 512;   // 16-row blocks per slot (N <= 8192)
 constexpr int kKSplitMaxParts = 8;
 constexpr size_t kKSplitAccPerSlot = static_cast<size_t>(kKSplitMaxBlocks) * 4 * kWave;
@@ -915,6 +915,12 @@ bool ksplit_resolve(int dev)
 }
 
 }  // namespace
+
+int ksplit_slots_used(int dev)
+{
+    std::lock_guard<std::mutex> lock(g_ks_mu);
+    return g_ks_slots.used(dev);
+}
 
 int ksplit_prepare()
 {
@@ -1494,6 +1500,18 @@ extern "C" int forge_ksplit_last(int* slot, int* parts)
     if (!slot || !parts) return FORGE_EINVAL;
     *slot = t_ks_last_slot;
     *parts = t_ks_last_kp;
+    return FORGE_OK;
+}
+
+extern "C" int forge_slots_in_use(int* ksplit_used, int* ksplit_total, int* fq_pack_used, int* fq_pack_total)
+{
+    if (!ksplit_used || !ksplit_total || !fq_pack_used || !fq_pack_total) return FORGE_EINVAL;
+    int dev = 0;
+    if (!slot_device(&dev)) return FORGE_ENODEV;
+    *ksplit_used = ksplit_slots_used(dev);
+    *ksplit_total = kKSplitSlotCount;
+    *fq_pack_used = fq_pack_slots_used(dev);
+    *fq_pack_total = kFqPackSlotCount;
     return FORGE_OK;
 }
 

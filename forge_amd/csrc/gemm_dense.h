@@ -60,6 +60,12 @@ int ksplit_prepare();
 int fq_pack_prepare();
 // Resolves the device address of forge_int8_linear_noalloc's array on the current device.
 int noalloc_prepare();
+// Slots of device dev held by launch keys: the decode K split's (of kKSplitSlotCount) and the
+// fused sparse linear's packed-weight slots (of kFqPackSlotCount).
+constexpr int kKSplitSlotCount = 32;
+constexpr int kFqPackSlotCount = 32;
+int ksplit_slots_used(int dev);
+int fq_pack_slots_used(int dev);
 
 constexpr int kSkinnyTbMaxM = 64;
 bool skinny_tb_supported(int M, int K);

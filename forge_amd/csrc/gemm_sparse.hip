@@ -1757,7 +1757,7 @@ __global__ __launch_bounds__(256) void fq_pack_weights_kernel(const int8_t* __re
 // fused path allocates nothing and leaves the caller's scratch buffers untouched (the
 // reference's contract for it). A launch without a slot, or with weights beyond a slot, reads
 // W_comp in place (same bits).
-constexpr int kFqPackSlots = 32;   // one per stream and per graph capture, as the decode K split's
+constexpr int kFqPackSlots = kFqPackSlotCount;   // one per stream and per graph capture, as the decode K split's
 constexpr size_t kFqPackBytes = size_t(1) << 20;   // N * K / 2: 1280 x 1638, 2048 x 1024
 static __device__ __align__(16) int8_t g_fq_pack[kFqPackSlots * kFqPackBytes];
 
@@ -1793,6 +1793,12 @@ int8_t* fq_pack_slot(hipStream_t s)
     return slot < 0 ? nullptr : g_fq_pack_dev[dev] + static_cast<size_t>(slot) * kFqPackBytes;
 }
 }  // namespace
+
+int fq_pack_slots_used(int dev)
+{
+    std::lock_guard<std::mutex> lock(g_fq_mu);
+    return g_fq_slots.used(dev);
+}
 
 int fq_pack_prepare()
 {

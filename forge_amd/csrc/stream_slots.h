@@ -63,6 +63,9 @@ public:
         return used_[dev]++;
     }
 
+    // Slots of device dev held by some key (they are never released).
+    int used(int dev) const { return used_[dev]; }
+
 private:
     SlotKey owner_[kSlotMaxDev][kN] = {};
     int used_[kSlotMaxDev] = {};

@@ -100,6 +100,16 @@ def ksplit_reset() -> None:
     _call("forge_ksplit_reset", _stream())
 
 
+def slots_in_use() -> Tuple[int, int, int, int]:
+    """(K-split slots held, K-split slots, packed-weight slots held, packed-weight slots) of
+    the current device (forge_slots_in_use). Slots are never released; once all are held, a
+    new stream or graph capture runs the unsplit decode / in-place fused path (same bits)."""
+    import ctypes
+    v = [ctypes.c_int() for _ in range(4)]
+    _call("forge_slots_in_use", *[ctypes.addressof(x) for x in v])
+    return tuple(x.value for x in v)
+
+
 # ---- device queries (int8_gemm.cuh:18-24) ----------------------------------------
 
 def get_compute_capability(device: int = 0) -> int:

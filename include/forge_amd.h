@@ -74,6 +74,15 @@ int forge_init(void);
 int forge_ksplit_last(int* slot, int* parts);
 int forge_ksplit_reset(void* stream);
 
+/* Extension, no counterpart in the reference: how many of the current device's static slots
+ * are held, and how many there are -- the decode K split's (forge_ksplit_last) and the fused
+ * sparse linear's packed-weight slots. Each slot belongs for the rest of the process to the
+ * first key that takes it (a stream for eager launches, a stream + capture for launches
+ * recorded into a graph); once all are held, launches of a new key run the path that needs
+ * none (unsplit decode, W_comp read in place), with the same results. For serving stacks
+ * that capture many graphs: they can see when captures start recording those paths. */
+int forge_slots_in_use(int* ksplit_used, int* ksplit_total, int* fq_pack_used, int* fq_pack_total);
+
 /* The engine of the calling thread's last GEMM launch made through this library (no
  * counterpart in the reference; its benchmark prints the plan it computes itself,
  * benchmarks/bench_int8_sparse.cu:164-170): e.g. "dma256x256", "dma256x256+tail192"

@@ -73,6 +73,12 @@ int main()
     }
     EXPECT_ERR(forge_init());
     EXPECT_ERR(forge_ksplit_reset(st));
+    EXPECT_EQ(forge_slots_in_use(nullptr, nullptr, nullptr, nullptr), FORGE_EINVAL);
+    {
+        int a = 0, b2 = 0, c = 0, d = 0;
+        EXPECT_EQ(forge_slots_in_use(&a, &b2, nullptr, &d), FORGE_EINVAL);
+        EXPECT_ERR(forge_slots_in_use(&a, &b2, &c, &d));   // no device here
+    }
     EXPECT_EQ(forge_get_compute_capability(0, nullptr), FORGE_EINVAL);
     EXPECT_EQ(forge_has_int8_matrix_cores(0, nullptr), FORGE_EINVAL);
     {

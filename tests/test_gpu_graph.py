@@ -5,6 +5,8 @@ so every launcher must be capturable: no synchronisation, allocation, attribute 
 inside the capture, and no memset nodes (the split-K workspace is cleared by a kernel). Each graph
 is replayed several times with eager work and synchronisations between the replays, and every
 replay is compared bit-for-bit with the eager result of the same calls."""
+import os
+
 import numpy as np
 import pytest
 
@@ -279,3 +281,35 @@ def test_graph_weight_prep(dev):
     say("graph weight prep")
     calls = [prep, lambda: ops.quantize_weight_rows(w, q, qs)]
     _replay_check(dev, calls, [comp, meta, sc, q, qs])
+
+
+def _fresh_process(mode):
+    """Runs tests/fresh_process_checks.py MODE in a child process (it needs the library's
+    per-process slot and no-alloc state untouched) and returns its JSON line."""
+    import json
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    say(f"fresh process check: {mode}")
+    r = subprocess.run([sys.executable, os.path.join(here, "fresh_process_checks.py"), mode], capture_output=True,
+                       text=True, timeout=240)
+    assert r.returncode == 0, r.stderr[-3000:]
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def test_graph_slot_exhaustion():
+    """The K-split slots are held for good by the first 32 launch keys (streams for eager
+    launches, captures for graph launches). In a fresh process the eager stream takes one, 31
+    captures of a K-split decode record split launches on 31 more distinct slots, and the next
+    capture -- the 33rd key -- records the unsplit decode (no slot); forge_slots_in_use then
+    reports all 32 held. Every replay is bit-identical to eager."""
+    r = _fresh_process("slots")
+    assert r["eager"][0] >= 0 and r["eager"][1] == 8, r["eager"]
+    total, rec = r["total"], r["recorded"]
+    assert total == 32 and len(rec) == total - r["used0"] + 1
+    split = rec[:-1]
+    assert all(s >= 0 and p == 8 for s, p in split), split
+    assert len({s for s, _ in split}) == len(split)
+    assert rec[-1] == [-1, 1], rec[-1]
+    assert r["after"][0] == total and r["after"][1] == total
+    assert all(r["equal"])

@@ -54,3 +54,24 @@ def test_noalloc_limits(dev):
     assert _call_noalloc(lib, x, w, ws, None, out, 4097, 4096, 16, stream) == _lib.FORGE_ERANGE
     assert _call_noalloc(lib, x, w, ws, None, out, 65537, 16, 16, stream) == _lib.FORGE_ERANGE
     assert lib.forge_int8_linear_noalloc(None, None, None, None, None, 4, 64, 16, stream) == _lib.FORGE_EINVAL
+
+
+def test_noalloc_graph_capture(dev):
+    """Under graph capture (in a process of its own, so that forge_init has not run yet): a
+    first call inside a capture is rejected with FORGE_EINVAL (the array's address is resolved
+    outside captures); after forge_init, two calls of different shapes captured into one graph
+    replay three times, with eager work in between, to the bits of eager forge_int8_linear."""
+    import json
+    import os
+    import subprocess
+    import sys
+    here = os.path.dirname(os.path.abspath(__file__))
+    say("fresh process check: noalloc under graph capture")
+    r = subprocess.run([sys.executable, os.path.join(here, "fresh_process_checks.py"), "noalloc"],
+                       capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stderr[-3000:]
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out["before_init"] == out["EINVAL"]
+    assert out["init"] == out["OK"]
+    assert out["statuses"] == [out["OK"], out["OK"]]
+    assert all(all(e) for e in out["equal"]), out["equal"]
