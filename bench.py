@@ -14,8 +14,9 @@ algorithmic ops 2*M*N*K per launch against MI355X's dense INT8 peak (5.0 POP/s).
 cpu_baseline: the oracle's INT32 loop + dequant epilogue (oracle/) over the whole configs[1]
 workload, split over output rows on up to 16 threads (the box's CPU share per GPU), timed on
 this host; the single-threaded rate is in its sample text.
-roofline.traffic / roofline.mfma_busy: HBM bytes per launch of the GEMM and its matrix-core
-busy fraction, read from COUNTERS_FILE (profiles/kernel_counters.json), which `--counter-summary`
+roofline.traffic / roofline.mfma_busy: L2-miss bytes per launch of the GEMM (reads and writes
+between the L2s and the memory fabric: HBM plus what the 256 MB MALL serves, so an upper bound
+of HBM bytes) and its matrix-core busy fraction, read from COUNTERS_FILE (profiles/kernel_counters.json), which `--counter-summary`
 writes from rocprofv3 --pmc runs of `bench.py --traffic-probe` (FETCH_SIZE and WRITE_SIZE scaled
 by what the same counters read for a device copy of known size in the same runs; MFMA busy
 cycles; see profiles/kernel_counters.md).
@@ -65,9 +66,9 @@ def _c2_counters():
 
 
 def measured_traffic():
-    """HBM-side bytes per launch of the configs[1] GEMM from the committed counter runs
-    (FETCH_SIZE and WRITE_SIZE, scaled by the counters' reading for a device copy of known
-    size), or None."""
+    """L2-miss bytes per launch of the configs[1] GEMM (L2 <-> memory fabric, HBM plus MALL
+    hits) from the committed counter runs (FETCH_SIZE and WRITE_SIZE, scaled by the counters'
+    reading for a device copy of known size), or None."""
     v = _c2_counters().get("traffic_bytes")
     return int(v) if v else None
 
@@ -177,7 +178,7 @@ def _prep_sparse(ops, W):
 PROBE_KERNELS = {
     # probe: (kernel-name substrings, any of which marks a dispatch of the probe)
     "c2_gemm": ("gemm_dma_kernel<256, 256, true, forge_amd::DmaRowMajor>",),
-    "c3_sparse": ("sparse_dma32_tail_kernel<false,", "sparse_dma32_kernel<false,"),
+    "c3_sparse": ("sparse_wide_s32_kernel", "sparse_dma32_tail_kernel<false,", "sparse_dma32_kernel<false,"),
     "c3_dense": ("gemm_dma_coltail_kernel<false>", "gemm_dma_kernel<256, 256, false, forge_amd::DmaRowMajor>"),
     "c5_conv": ("gemm_dma_tail_kernel<false, forge_amd::DmaConv>",),
     "c4_dense_M16": ("decode_dense_kernel<true",),
@@ -335,12 +336,14 @@ def _counter_markdown(out) -> str:
           "`v_smfmac_i32_32x32x64_i8` (checked: c2 = 2,097,152 MFMAs x 32); `at clock` divides by 1024 SIMDs x "
           "clock x duration instead.",
           "- peak at clock = the 2.4 GHz peak (dense INT8 5.0 POP/s, 2:4 10.0) scaled to the measured clock.",
-          f"- HBM bytes = FETCH_SIZE x {cal['fetch_scale']:.3f} + WRITE_SIZE x {cal['write_scale']:.3f} (KiB x 1024), "
+          f"- L2-miss bytes = FETCH_SIZE x {cal['fetch_scale']:.3f} + WRITE_SIZE x {cal['write_scale']:.3f} (KiB x 1024), "
           f"the factors that make a {COPY_PROBE_BYTES >> 20} MiB device copy in the same runs read and write its size "
-          f"(FETCH_SIZE {cal['copy_fetch_kib']:.1f} KiB, WRITE_SIZE {cal['copy_write_kib']:.1f} KiB).",
+          f"(FETCH_SIZE {cal['copy_fetch_kib']:.1f} KiB, WRITE_SIZE {cal['copy_write_kib']:.1f} KiB). These count "
+          "traffic between the L2s and the memory fabric: HBM plus what the 256 MB MALL serves, an upper bound of "
+          "HBM bytes; `alg.` is the algorithmic bytes (operands read once, output written once).",
           "- L2 read latency = TCP_TCC_READ_REQ_LATENCY_sum / TCP_TCC_READ_REQ_sum (cycles); TA busy = "
           "TA_TA_BUSY_sum / 256 / (clock x duration).", "",
-          "| probe | us (counter run) | clock GHz | MFMA busy (at clock) | peak at clock | HBM MB (alg.) | L2 hit | "
+          "| probe | us (counter run) | clock GHz | MFMA busy (at clock) | peak at clock | L2-miss MB (alg.) | L2 hit | "
           "L2 lat. | TA busy | LDS confl./active |",
           "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
     for p, e in out["kernels"].items():
@@ -445,6 +448,157 @@ def spin(fn, seconds: float) -> None:
         e.synchronize()
         if s.elapsed_time(e) >= seconds * 1e3:
             return
+
+
+def _probe_lib():
+    """libforge_probes.so (forge_amd.build builds it beside the product library)."""
+    import ctypes
+    path = os.path.join(ROOT, "forge_amd", "lib", "libforge_probes.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} missing: build first (python -m forge_amd.build)")
+    return ctypes.CDLL(path)
+
+
+# The dense engine's loop at 8192^3 work: 1024 workgroups (the 32 x 32 tiles of 256 x 256) x
+# 64 stages of 128-deep K each, on one 64 KB stage of operands loaded once per workgroup.
+MFMA_PROBE_WGS, MFMA_PROBE_STAGES = 1024, 64
+STREAM_PROBE_BYTES, STREAM_PROBE_BUFS = 256 << 20, 3     # 3 x 256 MiB rotate past the 256 MB MALL
+
+
+def _probe_setup(dev):
+    """Device buffers of the probes: random and constant INT8 stages for probe_mfma_lds, the
+    rotating streaming buffers, the DMA probe's rows."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    tiles = 64
+    rnd = [torch.randint(-127, 128, (tiles * 256 * 128,), generator=g, device=dev, dtype=torch.int8) for _ in range(2)]
+    one = torch.ones((tiles * 256 * 128,), dtype=torch.int8, device=dev)
+    bufs = [torch.randint(-127, 128, (STREAM_PROBE_BYTES,), generator=g, device=dev, dtype=torch.int8)
+            for _ in range(STREAM_PROBE_BUFS)]
+    dma = torch.randint(-127, 128, (256 * 256 * 8192,), generator=g, device=dev, dtype=torch.int8)
+    out = torch.zeros((4096,), dtype=torch.int32, device=dev)
+    return {"rnd": rnd, "one": one, "tiles": tiles, "bufs": bufs, "dma": dma, "out": out}
+
+
+def _probe_calls(P, bufs):
+    """name -> (one launch of the probe, its work: ('ops', n) or ('bytes', n))."""
+    import ctypes
+    import torch
+    st = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    V = ctypes.c_void_p
+    A, B = bufs["rnd"]
+    one, out, tiles = bufs["one"], bufs["out"], bufs["tiles"]
+    ops = 2.0 * MFMA_PROBE_WGS * 256 * 256 * 128 * MFMA_PROBE_STAGES
+
+    def mfma(a, b, reads):
+        return lambda: P.probe_mfma_lds(V(a.data_ptr()), V(b.data_ptr()), V(out.data_ptr()), MFMA_PROBE_WGS,
+                                        MFMA_PROBE_STAGES, tiles, reads, st())
+    calls = {
+        "mfma_lds_random": (mfma(A, B, 1), ("ops", ops)),
+        "mfma_lds_const": (mfma(one, one, 1), ("ops", ops)),
+        "mfma_only_random": (mfma(A, B, 0), ("ops", ops)),
+        "mfma_only_const": (mfma(one, one, 0), ("ops", ops)),
+    }
+    state = {"i": 0}
+
+    def stream():
+        b = bufs["bufs"][state["i"] % len(bufs["bufs"])]
+        state["i"] += 1
+        return P.probe_stream(V(b.data_ptr()), ctypes.c_size_t(b.numel()), 2048, V(out.data_ptr()), st())
+    calls["stream"] = (stream, ("bytes", STREAM_PROBE_BYTES))
+    dma = bufs["dma"]
+    for share in (1, 4, 8, 32):
+        for half in (0, 1):
+            for ldsr in (0, 1):
+                if half and ldsr:
+                    continue
+                calls[f"dma_s{share}_h{half}_r{ldsr}"] = (
+                    lambda share=share, half=half, ldsr=ldsr: P.probe_dma(
+                        V(dma.data_ptr()), ctypes.c_uint32(dma.numel()), 4096 if half else 8192, share, half, ldsr,
+                        V(out.data_ptr()), st()),
+                    ("bytes", 256 * 256 * 8192))
+    return calls
+
+
+def run_probes() -> int:
+    """bench.py --probes: every probe timed with HIP events (settled clocks: each runs 0.5 s
+    first); one JSON line. MFMA probes in TOPS (the 8192^3 GEMM's work), the streaming read in
+    TB/s, the DMA probe in bytes per CU per clock at the clock the rest of the line reports is not
+    known, so in GB/s per CU. Also the vendor library (hipBLASLt through torch._int_mm, INT32
+    out) at 4096^3 and 8192^3 next to forge_int8_gemm_s32, checked bit-equal."""
+    import torch
+    import forge_amd
+    from forge_amd import ops
+    forge_amd.load()
+    dev = torch.device("cuda:0")
+    P = _probe_lib()
+    bufs = _probe_setup(dev)
+    res = {}
+    for name, (fn, (kind, work)) in _probe_calls(P, bufs).items():
+        assert fn() == 0, name
+        torch.cuda.synchronize()
+        spin(fn, 0.5)
+        t = min(events_time_ms(fn, 10) for _ in range(3))
+        if kind == "ops":
+            res[name] = {"us": round(t * 1e3, 2), "TOPS": round(work / t / 1e9, 1)}
+        elif name == "stream":
+            res[name] = {"us": round(t * 1e3, 2), "TBs": round(work / t / 1e9, 3)}
+        else:
+            res[name] = {"us": round(t * 1e3, 2), "GBs_per_CU": round(work / 256 / t / 1e6, 1)}
+        print(f"probe {name}: {res[name]}", flush=True)
+    res["vendor_hipblaslt"] = vendor_gemm_compare(dev)
+    print(json.dumps({"probes": res}), flush=True)
+    return 0
+
+
+def run_one_probe(name: str) -> int:
+    """bench.py --probe NAME: that probe PROBE_REPS times (for rocprofv3 --pmc runs)."""
+    import torch
+    dev = torch.device("cuda:0")
+    P = _probe_lib()
+    calls = _probe_calls(P, _probe_setup(dev))
+    if name not in calls:
+        raise SystemExit(f"unknown probe {name}; one of {', '.join(calls)}")
+    fn = calls[name][0]
+    for _ in range(PROBE_REPS):
+        assert fn() == 0
+    torch.cuda.synchronize()
+    print(f"probe {name} done", flush=True)
+    return 0
+
+
+def vendor_gemm_compare(dev):
+    """hipBLASLt (torch._int_mm, INT32 out) next to forge_int8_gemm_s32 at 4096^3 and 8192^3:
+    a vendor reference point, not part of the product; outputs checked bit-equal."""
+    import torch
+    from forge_amd import ops
+    g = torch.Generator(device=dev)
+    g.manual_seed(13)
+    out = {}
+    for n in (4096, 8192):
+        A = torch.randint(-127, 128, (n, n), generator=g, device=dev, dtype=torch.int8)
+        B = torch.randint(-127, 128, (n, n), generator=g, device=dev, dtype=torch.int8)
+        Bt = B.t()
+        C = torch.empty((n, n), dtype=torch.int32, device=dev)
+        ref = torch._int_mm(A, Bt)
+        ops.int8_gemm_s32(A, B, out=C)
+        torch.cuda.synchronize()
+        equal = bool(torch.equal(ref, C))
+        f_lt = lambda: torch._int_mm(A, Bt)
+        f_fg = lambda: ops.int8_gemm_s32(A, B, out=C)
+        spin(lambda: (f_lt(), f_fg()), 0.5)
+        t_lt, t_fg = [], []
+        for _ in range(3):
+            t_lt.append(events_time_ms(f_lt, 10))
+            t_fg.append(events_time_ms(f_fg, 10))
+        ops_ = 2.0 * n ** 3
+        out[str(n)] = {"hipblaslt_us": round(min(t_lt) * 1e3, 2), "forge_us": round(min(t_fg) * 1e3, 2),
+                       "hipblaslt_tops": round(ops_ / min(t_lt) / 1e9, 1), "forge_tops": round(ops_ / min(t_fg) / 1e9, 1),
+                       "bit_equal": equal}
+        del A, B, C, ref
+    torch.cuda.empty_cache()
+    return out
 
 
 def bench_reference_sweep(dev):
@@ -808,9 +962,15 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true")
     ap.add_argument("--counter-summary", metavar="DIR", default=None)
+    ap.add_argument("--probes", action="store_true", help="run the measurement probes (libforge_probes.so)")
+    ap.add_argument("--probe", metavar="NAME", default=None, help="one probe, PROBE_REPS launches (for rocprofv3)")
     args = ap.parse_args()
     if args.traffic_probe:
         return traffic_probe()
+    if args.probes:
+        return run_probes()
+    if args.probe:
+        return run_one_probe(args.probe)
     if args.counter_summary:
         return counter_summary(args.counter_summary)
     if args.gpus != 1:

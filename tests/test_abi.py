@@ -178,3 +178,25 @@ def test_cpp_caller_links_and_reports_errors(lib):
     caller = ctypes.CDLL(path)
     caller.caller_last_error_after_bad_call.restype = ctypes.c_int
     assert caller.caller_last_error_after_bad_call() == _lib.FORGE_EINVAL
+
+
+def test_probe_library_loads_and_checks_arguments():
+    """libforge_probes.so (the measurement probes behind bench.py --probes) is a separate
+    library: it exports the three probes, rejects bad arguments before any launch, and the
+    product library does not carry them."""
+    from forge_amd import build
+    if not os.path.exists(build.PROBE_LIB):
+        pytest.skip("probe library not built")
+    P = ctypes.CDLL(build.PROBE_LIB)
+    fake = ctypes.c_void_p(4096)
+    P.probe_stream.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    P.probe_dma.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                            ctypes.c_void_p, ctypes.c_void_p]
+    assert P.probe_mfma_lds(None, fake, fake, 4, 4, 1, 1, None) == -1
+    assert P.probe_mfma_lds(fake, fake, fake, 0, 4, 1, 1, None) == -1
+    assert P.probe_stream(fake, 1000, 4, fake, None) == -1                      # not a multiple of 16 * wgs
+    assert P.probe_dma(fake, 1 << 30, 8192, 3, 0, 0, fake, None) == -1          # share not a power of two <= 32
+    assert P.probe_dma(fake, 1 << 20, 8192, 1, 0, 0, fake, None) == -1          # rows do not fit in `bytes`
+    assert P.probe_dma(fake, 1 << 30, 8000, 1, 0, 0, fake, None) == -1          # K % 128
+    import forge_amd
+    assert not hasattr(forge_amd.load(), "probe_mfma_lds")
