@@ -308,7 +308,7 @@ COUNTER_SETS = [
 ]
 PROBE_TITLES = {
     "c2_gemm": "configs[1] GEMM 4096^3, FP16 out (`gemm_dma_kernel<256,256,true>`)",
-    "c3_sparse": "configs[2] 2:4 sparse 4096x11008x4096, INT32 out (`sparse_dma32_tail_kernel<false,192,SpDmaTile32WB>`: 256- and 192-row tiles, one launch)",
+    "c3_sparse": "configs[2] 2:4 sparse 4096x11008x4096, INT32 out (`sparse_wide_s32_kernel`: 256 tokens x 320-352 weight rows per tile, 2 tiles per CU)",
     "c3_dense": "configs[2] shape dense, INT32 out (`gemm_dma_coltail_kernel<false>`: 256- and 192-row tiles, one launch)",
     "c5_conv": "configs[4] NHWC conv, INT32 out (`gemm_dma_tail_kernel<false,DmaConv>`: 256- and 192-row tiles, one launch)",
     "c4_dense_M16": "configs[3] M=16 dense decode GEMM (`decode_dense_kernel`)",
