@@ -11,6 +11,7 @@
 #include "forge/quant/quantize.h"
 #include "forge/quant/dequantize.h"
 #include "forge/gemm/int8_dense.h"
+#include "forge/gemm/int8_dp4a.h"
 #include "forge/gemm/int8_sparse.h"
 
 extern "C" int caller_quantize_kernel(const void* x, void* q, float* scales, int M, int K, int threads,
@@ -44,6 +45,26 @@ extern "C" int caller_int8_linear(const void* x, const int8_t* w, const void* w_
     forge::gemm::int8_linear(static_cast<const __half*>(x), w, static_cast<const __half*>(w_scale),
                              static_cast<const __half*>(bias), static_cast<__half*>(out), M, K, N, scratch_q,
                              scratch_s, static_cast<hipStream_t>(stream));
+    return forge::last_error();
+}
+
+// The dp4a entry points (the reference's fallback for GPUs without INT8 tensor cores); here they
+// forward to the matrix-core path, so their results must equal the oracle's.
+extern "C" int caller_dp4a_gemm_dequant(const int8_t* A, const int8_t* B, const float* act_scale, const void* w_scale,
+                                        const void* bias, void* out, int M, int K, int N, void* stream)
+{
+    forge::gemm::int8_dp4a_gemm_dequant(A, B, act_scale, static_cast<const __half*>(w_scale),
+                                        static_cast<const __half*>(bias), static_cast<__half*>(out), M, K, N,
+                                        static_cast<hipStream_t>(stream));
+    return forge::last_error();
+}
+
+extern "C" int caller_dp4a_linear(const void* x, const int8_t* w, const void* w_scale, const void* bias, void* out,
+                                  int M, int K, int N, int8_t* scratch_q, float* scratch_s, void* stream)
+{
+    forge::gemm::int8_dp4a_linear(static_cast<const __half*>(x), w, static_cast<const __half*>(w_scale),
+                                  static_cast<const __half*>(bias), static_cast<__half*>(out), M, K, N, scratch_q,
+                                  scratch_s, static_cast<hipStream_t>(stream));
     return forge::last_error();
 }
 

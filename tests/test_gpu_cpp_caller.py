@@ -29,6 +29,8 @@ def caller(dev):
         "caller_dequantize_bias": [_P, _P, _P, _P, _P, _I, _I, _P],
         "caller_int8_linear": [_P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P],
         "caller_sparse_int8_linear": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P],
+        "caller_dp4a_gemm_dequant": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+        "caller_dp4a_linear": [_P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P],
         "caller_last_error_after_bad_call": [],
     }
     for name, args in sigs.items():
@@ -87,6 +89,38 @@ def test_cpp_int8_linear(dev, orc, caller, M, K, N):
                                      _stream()) == 0
     assert np.array_equal(to_host(y).view(np.uint16), ref.view(np.uint16))
     assert np.array_equal(to_host(sq), qr)
+
+
+# The reference's dp4a test shapes include K = 7 and K = 28 (tests/test_int8_dp4a_gemm.cu:180-196);
+# here the dp4a names forward to the matrix-core path, which must give the oracle's bits.
+@pytest.mark.parametrize("M,K,N", [(5, 7, 9), (33, 28, 40), (64, 256, 96), (129, 1000, 300), (4, 4096, 512)])
+def test_cpp_dp4a_forwards(dev, orc, caller, M, K, N):
+    import torch
+    rng = np.random.default_rng(M * 3 + K + N)
+    A = int8_uniform(rng, (M, K))
+    W = int8_uniform(rng, (N, K))
+    act = rng.uniform(1e-3, 5e-2, M).astype(np.float32)
+    ws = rng.uniform(1e-3, 1e-2, N).astype(np.float16)
+    b = (rng.standard_normal(N) * 0.1).astype(np.float16)
+    say(f"C++ forge::gemm::int8_dp4a_gemm_dequant / int8_dp4a_linear M={M} K={K} N={N}")
+    Ad, Wd, actd, wsd, bd = to_dev(A, dev), to_dev(W, dev), to_dev(act, dev), to_dev(ws, dev), to_dev(b, dev)
+    y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    poison(y, 0x7B)
+    assert caller.caller_dp4a_gemm_dequant(_p(Ad), _p(Wd), _p(actd), _p(wsd), _p(bd), _p(y), M, K, N,
+                                           _stream()) == 0
+    ref = orc.gemm_dequant(A, W, act, ws, b, threads=orc.cpu_threads())
+    assert np.array_equal(to_host(y).view(np.uint16), ref.view(np.uint16))
+    x = fp16_normal(rng, (M, K))
+    ref2, qr, sr = orc.linear(x, W, ws, b, threads=orc.cpu_threads())
+    xd = to_dev(x, dev)
+    sq = torch.empty((M, K), dtype=torch.int8, device=dev)
+    ss = torch.empty((M,), dtype=torch.float32, device=dev)
+    poison(y, 0x7B)
+    assert caller.caller_dp4a_linear(_p(xd), _p(Wd), _p(wsd), _p(bd), _p(y), M, K, N, _p(sq), _p(ss),
+                                     _stream()) == 0
+    assert np.array_equal(to_host(y).view(np.uint16), ref2.view(np.uint16))
+    assert np.array_equal(to_host(sq), qr)
+    assert np.array_equal(to_host(ss).view(np.uint32), sr.view(np.uint32))
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 8192, 1024), (16, 2048, 208), (600, 1024, 512)])

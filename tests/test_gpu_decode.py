@@ -148,7 +148,8 @@ TB_SPARSE = [(17, 256, 48), (32, 768, 208), (33, 1280, 16), (48, 2048, 96), (64,
 
 
 def _check_cols(N):
-    return np.arange(N) if N <= 512 else np.unique(np.r_[0:40, N // 2 - 20:N // 2 + 20, N - 40:N])
+    """Every output column (the oracle runs on the host's cores)."""
+    return np.arange(N)
 
 
 @pytest.mark.parametrize("M,K,N", TB_DENSE)
@@ -162,7 +163,7 @@ def test_token_blocks_dense(dev, orc, M, K, N):
     ws = rng.uniform(0.001, 0.05, N).astype(np.float16)
     b = rng.uniform(-0.5, 0.5, N).astype(np.float16)
     cols = _check_cols(N)
-    acc = orc.gemm_s32(A, B[cols])
+    acc = orc.gemm_s32(A, B[cols], threads=orc.cpu_threads())
     say(f"token-block dense M={M} K={K} N={N}")
     Ad, Bd = to_dev(A, dev), to_dev(B, dev)
     C = torch.empty((M, N), dtype=torch.int32, device=dev)
@@ -191,7 +192,7 @@ def test_token_blocks_sparse(dev, orc, M, K, N):
     cols = _check_cols(N)
     cr, mr = orc.prune_compress_24(W)
     Wp = orc.decompress_24(cr, mr, N, K)
-    acc = orc.gemm_s32(x, Wp[cols])
+    acc = orc.gemm_s32(x, Wp[cols], threads=orc.cpu_threads())
     comp = torch.empty((N, K // 2), dtype=torch.int8, device=dev)
     raw = torch.empty((N * K // 4,), dtype=torch.uint8, device=dev)
     meta = torch.empty((N * K // 32,), dtype=torch.int32, device=dev)

@@ -1,7 +1,7 @@
 """GPU: forge_int8_linear_noalloc (the no-allocation form of forge_int8_linear, whose quantized
 activations live in the library's per-GPU device array) against forge_int8_linear with caller
-scratch, through the C ABI: two calls in a row, the second with a smaller input, bit-identical
-outputs; sizes beyond the array's limits are rejected with FORGE_ERANGE before any launch."""
+scratch and against the oracle, through the C ABI: two calls in a row, the second with a smaller
+input, bit-identical outputs; sizes beyond the array's limits are rejected with FORGE_ERANGE before any launch."""
 import ctypes
 
 import numpy as np
@@ -39,6 +39,10 @@ def test_noalloc_matches_int8_linear(dev, orc):
         say(f"int8_linear_noalloc M={M} K={K} N={N} bias={bias}")
         assert _call_noalloc(lib, x, w, ws, b, got, M, K, N, stream) == _lib.FORGE_OK
         assert np.array_equal(to_host(got).view(np.uint16), to_host(want).view(np.uint16))
+        # and against the oracle's quantize + INT32 GEMM + epilogue directly
+        ref, _, _ = orc.linear(to_host(x), to_host(w), to_host(ws), None if b is None else to_host(b),
+                               threads=orc.cpu_threads())
+        assert np.array_equal(to_host(got).view(np.uint16), ref.view(np.uint16))
 
 
 def test_noalloc_limits(dev):
