@@ -31,7 +31,11 @@ input + output bytes (rotating over more than 256 MB of inputs and outputs, grap
 reference's NCHW FP16 int8_conv2d_forward on a (1, 32, 540, 960) 3x3 layer (one fused launch); and SparseLinear's weight preparation at 11008 x 4096 fp32, one pass
 against the reference's separate quantize / prune+compress / pack steps; and
 extra.reference_sweep: the reference's own sparse benchmark (bench_int8_sparse.cu shapes and
-protocol) with the dense path beside it.
+protocol) with the dense path beside it; extra.vendor_hipblaslt: hipBLASLt (torch._int_mm, INT32
+out) next to forge_int8_gemm_s32 at 4096^3 and 8192^3 on the same inputs, checked bit-equal -- a
+vendor reference point, not part of the product.
+    python bench.py --probes            (the measurement probes of libforge_probes.so, one JSON line)
+    python bench.py --probe NAME        (one probe, repeated, for rocprofv3 --pmc runs)
 """
 from __future__ import annotations
 
@@ -1048,6 +1052,7 @@ def main() -> int:
     if not args.no_extra:
         line["extra"] = {k: round(v, 3) for k, v in bench_extra(dev).items()}
         line["extra"]["reference_sweep"] = bench_reference_sweep(dev)
+        line["extra"]["vendor_hipblaslt"] = vendor_gemm_compare(dev)
     print(json.dumps(line))
     return 0
 
