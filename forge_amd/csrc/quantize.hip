@@ -239,6 +239,8 @@ __global__ __launch_bounds__(256) void dequantize_vec4_kernel(
     const uint16_t* __restrict__ w_scale, const uint16_t* __restrict__ bias,
     uint2* __restrict__ out, uint32_t n4, uint32_t total4)
 {
+    // total4 < 2^31 and stride <= 16384 * 256 = 2^22 (host guards), so i + stride < 2^32: the
+    // unsigned counter never wraps.
     const uint32_t stride = gridDim.x * 256u;
     for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total4; i += stride) {
         const uint32_t m = i / n4;
