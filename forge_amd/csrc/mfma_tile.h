@@ -821,13 +821,14 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[BN / 64][BM / 64], 
 
 // Tile index -> (tile_m, tile_n): consecutive workgroups land on different XCDs
 // (dispatch is round-robin over the 8 XCDs), so the linear id is first regrouped so each
-// XCD receives a contiguous run, then runs are rasterised in groups of kGroupM tile-rows:
-// an XCD's L2 then holds a few A row-blocks and B col-blocks instead of all of them.
+// XCD receives a contiguous run (xcd_contiguous, a bijection for any tile count; a tail
+// grid whose first id is not a multiple of 8 shifts which XCD gets which run, not the
+// grouping), then runs are rasterised in groups of kGroupM tile-rows: an XCD's L2 then
+// holds a few A row-blocks and B col-blocks instead of all of them.
 __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
-    constexpr int kXcd = 8, kGroupM = 4;
+    constexpr int kGroupM = 4;
     const int total = tiles_m * tiles_n;
-    int t = bid;
-    if (total % kXcd == 0) t = (bid % kXcd) * (total / kXcd) + bid / kXcd;
+    const int t = xcd_contiguous(bid, total);
     const int per_group = kGroupM * tiles_n;
     const int group = t / per_group;
     const int first_m = group * kGroupM;
