@@ -91,7 +91,8 @@ def traffic_probe() -> int:
     (4096 x 11008 x 4096, INT32 out) on the 2:4 and the dense engine; c5 = configs[4] NHWC
     conv (INT32 out; 256-row and 192-row tiles in one launch); c4 = configs[3] M = 16 decode GEMMs
     (N = K = 8192, pre-quantized tokens, FP16 out) dense and 2:4; f1 = the fused quantize + 2:4
-    sparse linear on the reference's example layer (1280 -> 320 at M = 147,456); then a COPY_PROBE_BYTES
+    sparse linear on the reference's example layer (1280 -> 320 at M = 147,456); f2 = the NCHW FP16
+    conv API on (1, 32, 540, 960) 3x3 -> 32 (one launch); then a COPY_PROBE_BYTES
     device-to-device copy, the calibration of known size for FETCH_SIZE / WRITE_SIZE."""
     import torch
     import forge_amd
@@ -158,6 +159,18 @@ def traffic_probe() -> int:
     reps("f1_fq", lambda: ops.sparse_int8_linear(xf, comp, meta, wsf, bf, qf, sf, None, 1, 1, out=yf))
     del W, comp, meta, xf, qf, yf
 
+    # the reference's NCHW FP16 conv API on an upscaler-style 3x3 layer (1, 32, 540, 960) -> 32
+    xn = (torch.rand((1, 32, 540, 960), generator=g, device=dev) * 2 - 1).half()
+    wn = torch.randint(-127, 128, (32, 32 * 9), generator=g, device=dev, dtype=torch.int8)
+    wsn = (torch.rand((32,), generator=g, device=dev) * 0.045 + 0.005).half()
+    bn = (torch.rand((32,), generator=g, device=dev) - 0.5).half()
+    yn = torch.empty((1, 32, 540, 960), dtype=torch.float16, device=dev)
+    wspn = torch.empty((ops.int8_conv2d_workspace_size(32, 540, 960, 32, 3, 3, 1, 1, 1, 1),), dtype=torch.uint8,
+                       device=dev)
+    reps("f2_conv_nchw", lambda: ops.int8_conv2d_forward(xn, wn, wsn, bn, 3, 3, (1, 1), (1, 1), (1, 1),
+                                                         workspace=wspn, out=yn))
+    del xn, yn, wspn
+
     src = torch.empty((COPY_PROBE_BYTES,), dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     src.fill_(1)
@@ -188,6 +201,7 @@ PROBE_KERNELS = {
     "c4_dense_M16": ("decode_dense_kernel<true",),
     "c4_sparse_M16": ("decode_sparse_reg_kernel<true",),
     "f1_fq": ("sparse_fq_kernel<5, 48, true",),
+    "f2_conv_nchw": ("conv_nchw_cl_kernel",),
     "copy": ("copyBuffer",),
 }
 _C4_TOK = 16 * 8192
@@ -203,6 +217,7 @@ PROBE_WORK = {
                       + 8192 * 4 + 16 * 4, 10000.0),
     "f1_fq": (2.0 * 147456 * 320 * 1280, 2 * 147456 * 1280 + 2 * 147456 * 320 + 320 * 1280 * 5 // 8 + 4 * 320,
               10000.0),
+    "f2_conv_nchw": (2.0 * 540 * 960 * 32 * 288, 2 * 2 * 32 * 540 * 960 + 32 * 288 + 4 * 32, 5000.0),
 }
 SIMDS = 256 * 4          # MI355X: 256 CUs x 4 SIMDs
 XCDS = 8

@@ -610,6 +610,530 @@ static bool conv_nchw_fused_plan(ConvNchwArgs& a, int N, size_t* lds_bytes, bool
     return true;
 }
 
+// ---- NCHW FP16 conv on a channel-last window (one launch, 128-pixel tiles) --------------
+//
+// conv_nchw_cl_kernel gives the same bits as conv_nchw_fused_kernel (the reference pipeline's:
+// per-patch-row quantize of the im2col rows, exact INT32 sums, the GEMM's dequant epilogue),
+// with the work spread evenly over the four waves and fewer instructions per tap:
+//   * The input window is kept channel-last in LDS ([window row][column][channel], channels
+//     padded to Cp = 16k with zeros), so the 16 channels of one tap are 32 contiguous bytes:
+//     two ds_read_b128 give a lane 16 taps, where the NCHW window needs 16 ds_read_u16 and
+//     16 address adds. Window rows load as 16-byte buffer loads of 8 columns, 8 channels per
+//     lane (zeros outside the image and past C), transposed in registers by v_perm.
+//   * The GEMM's K order is free (the INT32 sums are exact in any order), so the patch row is
+//     taken as k' = (kh kW + kw) Cp + c; each workgroup holds its weights permuted to that
+//     order in LDS once (zero for padded channels and rows), where the reference's (C_out, K)
+//     rows have k = c kH kW + kh kW + kw.
+//   * Wave w owns pixels 32w .. 32w + 31 of the tile. Lane l quantizes taps 16 (2 ks + l / 32)
+//     .. + 15 of pixel l % 32 for K step ks: exactly its B fragment of
+//     v_mfma_i32_32x32x32_i8, which it feeds straight to the MFMA (no INT8 tile in LDS, no
+//     barrier between quantize and MFMA), for every 32-channel block of C_out.
+//   * The per-pixel scale is the max over the pixel's kH x kW window positions of each
+//     position's channel absmax (fp16 bit patterns, as the one-launch NCHW kernel takes them),
+//     computed once per position by the whole workgroup.
+// A tile is R output rows x Wt columns (R Wt <= 128); workgroups are persistent and walk their
+// XCD's contiguous range of tiles, with the next tile's window loads in flight during the
+// current tile (when a wave has at most one load instruction per tile).
+struct ConvClArgs {
+    const uint16_t* x;
+    const int8_t* w;
+    const uint16_t* w_scale;
+    const uint16_t* bias;
+    uint16_t* y;
+    int C, H, W, Co, kH, kW, padH, padW, sH, sW, dH, dW, Ho, Wo, K;
+    int Cp, CQ, nch, ksteps;   // channels padded to 16, 16-channel chunks per tap, chunks, 32-deep K steps
+    int R, Wt, npix, IH, IW;   // tile rows / columns / pixels; window rows / columns read
+    int G, IWr, Pp;            // 8-column load groups per window row; LDS row pitch (positions); position bytes
+    int rpi, nrows, ninst;     // load rows (8 channels of one window row) per instruction; rows; instructions
+    int KWp;                   // row pitch of the permuted weights (bytes)
+    int w_off, m1_off, koff_off, ws_off;   // LDS offsets (bytes)
+    int tiles_h, tiles_w, tiles, N;
+    int nw;                    // waves per workgroup (32 output pixels each)
+    uint32_t mg_wt, mg_rpi, mg_ih, mg_iw;  // udiv_magic multipliers
+    uint32_t mg_tiles, mg_tw;              // tile -> (image, tile row, tile column)
+    uint32_t mg_c;                         // weight fill: (output, input channel) pair -> output channel
+    int wpad;                              // the permuted weight block has padding
+    uint32_t x_bytes, y_bytes;
+};
+
+
+// 16 fp16 taps (8 dwords, two per dword, lower address in the low half) -> 16 INT8 values:
+// per tap one v_fma_mix_f32 (the rounded product, as qrow_bits_mix) and one SDWA add of
+// 1.5 * 2^23 whose low result byte (the INT8 value) goes straight into its byte of the
+// fragment dword (dst_sel:BYTE_k; the first write of a dword zero-pads it, the others keep
+// the bytes already there). The 16 adds cycle over the 4 dwords, so no add reads a dword the
+// add just before it wrote (a byte-select write read by the next VALU instruction needs a
+// wait state on this architecture), and the block ends with one for the MFMA that reads them.
+__device__ __forceinline__ v4i quant16_cl(uint4 h0, uint4 h1, float inv) {
+    const uint32_t w[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+    float p[16];
+#pragma unroll
+    for (int d = 0; d < 8; d++) {
+        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(p[2 * d]) : "v"(w[d]), "v"(inv));
+        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(p[2 * d + 1]) : "v"(w[d]), "v"(inv));
+    }
+    const float magic = 12582912.0f;
+    uint32_t q0, q1, q2, q3;
+    asm("v_add_f32_sdwa %0, %4, %20 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %1, %8, %20 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %2, %12, %20 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %3, %16, %20 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %0, %5, %20 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %1, %9, %20 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %2, %13, %20 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %3, %17, %20 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %0, %6, %20 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %1, %10, %20 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %2, %14, %20 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %3, %18, %20 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %0, %7, %20 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %1, %11, %20 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %2, %15, %20 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %3, %19, %20 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "s_nop 0"
+        : "=&v"(q0), "=&v"(q1), "=&v"(q2), "=&v"(q3)
+        : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5]), "v"(p[6]), "v"(p[7]), "v"(p[8]),
+          "v"(p[9]), "v"(p[10]), "v"(p[11]), "v"(p[12]), "v"(p[13]), "v"(p[14]), "v"(p[15]), "v"(magic));
+    return v4i{static_cast<int>(q0), static_cast<int>(q1), static_cast<int>(q2), static_cast<int>(q3)};
+}
+
+template <int NCB, bool PF, int NW>
+__global__ __launch_bounds__(64 * NW, (NCB == 1 ? 16 : NCB == 2 ? 12 : 8) / NW) void conv_nchw_cl_kernel(
+    ConvClArgs a)
+{
+    constexpr int kThr = 64 * NW;
+    extern __shared__ __align__(16) int8_t lds[];
+    int8_t* win = lds;
+    int8_t* wl = lds + a.w_off;
+    float* s_m1 = reinterpret_cast<float*>(lds + a.m1_off);
+    int* koff = reinterpret_cast<int*>(lds + a.koff_off);
+    float* s_ws = reinterpret_cast<float*>(lds + a.ws_off);
+    float* s_b = s_ws + 32 * NCB;
+    constexpr int kCop = 32 * NCB;
+
+    const int t = threadIdx.x, lane = t & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int l31 = lane & 31, hi = lane >> 5;
+    const int HW = a.H * a.W;
+    const int khw = a.kH * a.kW;
+    const uint32_t plane2 = 2u * static_cast<uint32_t>(a.Ho * a.Wo);
+    const bool has_bias = a.bias != nullptr;
+
+    ConvTileWalk walk = conv_tile_walk(a.tiles * a.N);
+    if (walk.next >= walk.end) return;
+
+    struct Geo {
+        int n, ho0, wo0, hb, a0, s0;
+    };
+    auto geo_of = [&](int tile) {
+        Geo g;
+        g.n = udiv_magic(tile, a.mg_tiles);
+        const int rem = tile - g.n * a.tiles;
+        const int th = udiv_magic(rem, a.mg_tw), tw = rem - th * a.tiles_w;
+        g.ho0 = th * a.R;
+        g.wo0 = tw * a.Wt;
+        g.hb = g.ho0 * a.sH - a.padH;
+        const int wb = g.wo0 * a.sW - a.padW;
+        g.a0 = wb & ~7;                                  // 8-aligned global column of window position 0
+        g.s0 = wb - g.a0;                                // the first column read sits at position s0
+        return g;
+    };
+
+    // 1. window loads: lane l of an instruction takes load row i rpi + l % rpi, 8-column
+    //    group l / rpi (lanes past rpi G idle); load row r holds channels 8 (r / IH) .. + 7 of
+    //    window row r % IH. W % 8 == 0, so a group is wholly inside or outside the image;
+    //    offsets past the buffer's range read as zeros (outside the image, channels past C).
+    //    The row runs fastest over the lanes for the LDS writes: a lane writes 8 positions of
+    //    its group, and lanes of different groups (8 positions apart) would hit the same banks,
+    //    while different rows (channel groups, window rows of odd pitch) spread over them.
+    const int grp = udiv_magic(lane, a.mg_rpi), slot = lane - grp * a.rpi;
+    const bool lok = grp < a.G;
+    auto issue_rows = [&](const Geo& g, int i, v4i* v) {
+        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x + static_cast<size_t>(g.n) * a.C * HW, a.x_bytes);
+        const int r = i * a.rpi + slot;
+        const int cg = udiv_magic(r, a.mg_ih), ih = r - cg * a.IH;
+        const int col = g.a0 + 8 * grp, h = g.hb + ih;
+        // (bitwise &, not &&: selects rather than branches)
+        const bool ok = lok & (r < a.nrows) & (col >= 0) & (col < a.W) &
+                        (static_cast<unsigned>(h) < static_cast<unsigned>(a.H));
+        const int cleft = a.C - 8 * cg;   // channels of this load row inside the image
+        const uint32_t base = 2u * static_cast<uint32_t>(8 * cg * HW + h * a.W + col);
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            v[u] = __builtin_amdgcn_raw_buffer_load_b128(
+                rx, (ok & (u < cleft)) ? base + static_cast<uint32_t>(2 * u * HW) : 0x80000000u, 0, 0);
+    };
+    // the 8 x 8 block transposed by v_perm into 8 positions of 8 channels (16 bytes each)
+    auto write_rows = [&](int i, const v4i* v) {
+        const int r = i * a.rpi + slot;
+        if (!lok || r >= a.nrows) return;
+        const int cg = udiv_magic(r, a.mg_ih), ih = r - cg * a.IH;
+        int8_t* dst = win + (ih * a.IWr + 8 * grp) * a.Pp + 16 * cg;
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++) {
+            const int d = jj >> 1;
+            const uint32_t sel = (jj & 1) ? 0x07060302u : 0x05040100u;
+            uint4 o;
+            o.x = __builtin_amdgcn_perm(static_cast<uint32_t>(v[1][d]), static_cast<uint32_t>(v[0][d]), sel);
+            o.y = __builtin_amdgcn_perm(static_cast<uint32_t>(v[3][d]), static_cast<uint32_t>(v[2][d]), sel);
+            o.z = __builtin_amdgcn_perm(static_cast<uint32_t>(v[5][d]), static_cast<uint32_t>(v[4][d]), sel);
+            o.w = __builtin_amdgcn_perm(static_cast<uint32_t>(v[7][d]), static_cast<uint32_t>(v[6][d]), sel);
+            *reinterpret_cast<uint4*>(dst + jj * a.Pp) = o;
+        }
+    };
+
+    Geo cur = geo_of(walk.next);
+    v4i pf[PF ? 8 : 1];
+    if constexpr (PF) {
+        if (wave < a.ninst) issue_rows(cur, wave, pf);   // in flight during the set-up
+    }
+
+    // 0. once per workgroup, while the first tile's window loads are in flight: the weights
+    //    in the k' order; the window offset of each 16-channel chunk (chunks past the patch
+    //    point at offset 0: their weights are zero); w_scale / bias.
+    //    The weights: zeros first where the permuted block has padding (channels past C, rows
+    //    past C_out, the half step past the last chunk), then per (output, input channel) pair
+    //    of the reference's rows its kH kW contiguous bytes (k = c kH kW + tap) scattered to
+    //    k' = tap Cp + c (taps past kH kW re-read the pair's last byte and store nothing).
+    {
+        if (a.wpad) {
+            for (int i = t; i < (kCop * a.KWp) >> 4; i += kThr)
+                *reinterpret_cast<uint4*>(wl + 16 * i) = make_uint4(0u, 0u, 0u, 0u);
+            __syncthreads();
+        }
+        // up to 9 taps: the reads of 4 pairs in flight together; more taps: per pair, 9 at a time
+        constexpr int kTapB = 9, kPairB = 4;
+        {
+            const int8_t* wsrc = a.w;
+            const int np = a.Co * a.C;
+            if (khw <= kTapB) {
+                for (int p0 = t; p0 < np; p0 += kPairB * kThr) {
+                    int8_t v[kPairB][kTapB];
+                    int dofs[kPairB];
+#pragma unroll
+                    for (int q = 0; q < kPairB; q++) {
+                        const int pi = min(p0 + kThr * q, np - 1);
+                        const int co = udiv_magic(pi, a.mg_c), c = pi - co * a.C;
+                        const int8_t* src = wsrc + static_cast<size_t>(co) * a.K + c * khw;
+                        dofs[q] = co * a.KWp + c;
+#pragma unroll
+                        for (int u = 0; u < kTapB; u++) v[q][u] = src[min(u, khw - 1)];
+                    }
+#pragma unroll
+                    for (int q = 0; q < kPairB; q++) {
+                        if (p0 + kThr * q >= np) break;
+#pragma unroll
+                        for (int u = 0; u < kTapB; u++)
+                            if (u < khw) wl[dofs[q] + u * a.Cp] = v[q][u];
+                    }
+                }
+            } else {
+                for (int pi = t; pi < np; pi += kThr) {
+                    const int co = udiv_magic(pi, a.mg_c), c = pi - co * a.C;
+                    const int8_t* src = wsrc + static_cast<size_t>(co) * a.K + c * khw;
+                    int8_t* dst = wl + co * a.KWp + c;
+                    for (int tp0 = 0; tp0 < khw; tp0 += kTapB) {
+                        int8_t v[kTapB];
+#pragma unroll
+                        for (int u = 0; u < kTapB; u++) v[u] = src[min(tp0 + u, khw - 1)];
+#pragma unroll
+                        for (int u = 0; u < kTapB; u++)
+                            if (tp0 + u < khw) dst[(tp0 + u) * a.Cp] = v[u];
+                    }
+                }
+            }
+        }
+        for (int j = t; j < 2 * a.ksteps + 4; j += kThr) {
+            int off = 0;
+            if (j < a.nch) {
+                const int tap = j / a.CQ, cc = j - tap * a.CQ;
+                const int kh = tap / a.kW, kw = tap - kh * a.kW;
+                off = (kh * a.dH * a.IWr + kw * a.dW) * a.Pp + 32 * cc;
+            }
+            koff[j] = off;
+        }
+        // Without a bias the strip holds -0: fma(acc, s, -0) is acc * s rounded once, zeros'
+        // signs included, i.e. the reference epilogue's product.
+        for (int c = t; c < kCop; c += kThr) {
+            s_ws[c] = c < a.Co ? h2f(a.w_scale[c]) : 0.0f;
+            s_b[c] = c < a.Co && has_bias ? h2f(a.bias[c]) : -0.0f;
+        }
+    }
+
+    while (true) {
+        // the current tile's window into LDS (the previous tile's readers are past the
+        // barrier at the end of the loop)
+        if constexpr (PF) {
+            if (wave < a.ninst) write_rows(wave, pf);
+        } else {
+            for (int i = wave; i < a.ninst; i += NW) {
+                v4i v[8];
+                issue_rows(cur, i, v);
+                write_rows(i, v);
+            }
+        }
+        const int nxt = walk.next + walk.stride;
+        const bool has_next = nxt < walk.end;
+        Geo ng = cur;
+        if (has_next) ng = geo_of(nxt);
+        __syncthreads();
+        if constexpr (PF) {
+            if (has_next && wave < a.ninst) issue_rows(ng, wave, pf);   // in flight while this tile computes
+        }
+
+        // 2. per window position (IH rows x IW columns from s0) the channel absmax on fp16
+        //    magnitude bit patterns; a maximum above 0x7C00 is a NaN, and the position then
+        //    takes the fp32 maximum, which skips NaN as the reference quantizer's reduction does
+        //    The maxima are stored as fp32 bit patterns: never NaN and never negative, they
+        //    order as unsigned integers.
+        uint32_t* s_m1u = reinterpret_cast<uint32_t*>(s_m1);
+        for (int q = t; q < a.IH * a.IW; q += kThr) {
+            const int ih = udiv_magic(q, a.mg_iw), iw = q - ih * a.IW;
+            const int8_t* src = win + (ih * a.IWr + cur.s0 + iw) * a.Pp;
+            uint32_t mb = 0u;
+            for (int c8 = 0; c8 < a.Cp; c8 += 16) {   // Cp % 16 == 0: two 16-byte reads in flight
+                const uint4 v0 = *reinterpret_cast<const uint4*>(src + 2 * c8);
+                const uint4 v1 = *reinterpret_cast<const uint4*>(src + 2 * c8 + 16);
+                mb = absbits8(v1, absbits8(v0, mb));
+            }
+            const uint32_t m16 = max(mb & 0xFFFFu, mb >> 16);
+            float m = h2f(static_cast<uint16_t>(m16));
+            if (m16 > kHalfInfBits) {
+                m = 0.0f;
+                for (int c = 0; c < a.Cp; c++)
+                    m = fmaxf(m, fabsf(h2f(*reinterpret_cast<const uint16_t*>(src + 2 * c))));
+            }
+            s_m1u[q] = __float_as_uint(m);
+        }
+        __syncthreads();
+
+        // 3./4./5. per wave: 32 pixels' scales, the quantized B fragments fed to the MFMAs,
+        //    the dequant epilogue stored to NCHW (2-byte buffer stores; pixels outside the
+        //    image and channels past C_out carry offsets past the range and are dropped)
+        if (32 * wave < a.npix) {
+            const int p0 = 32 * wave + l31;
+            const int p = p0 < a.npix ? p0 : a.npix - 1;
+            const int pr = udiv_magic(p, a.mg_wt), pc = p - pr * a.Wt;
+            // the pixel's kH x kW positions, three reads in flight; a read past the last tap
+            // takes tap (0, 0) again, which leaves the maximum as it is
+            const uint32_t* mr = s_m1u + pr * a.sH * a.IW + pc * a.sW;
+            uint32_t mu = 0u;
+            int kh = 0, kw = 0;
+            for (int tp = 0; tp < khw; tp += 3) {
+                uint32_t v[3];
+#pragma unroll
+                for (int u = 0; u < 3; u++) {
+                    const int off = tp + u < khw ? kh * a.dH * a.IW + kw * a.dW : 0;
+                    v[u] = mr[off];
+                    if (++kw == a.kW) {
+                        kw = 0;
+                        kh++;
+                    }
+                }
+                mu = max(mu, max(v[0], max(v[1], v[2])));
+            }
+            const float m = __uint_as_float(mu);
+            const float scale = row_scale(m);
+            const float inv = 1.0f / scale;
+
+            const int8_t* pix = win + (pr * a.sH * a.IWr + cur.s0 + pc * a.sW) * a.Pp;
+            const int8_t* wrow = wl + l31 * a.KWp + 16 * hi;
+            v16i acc[NCB];
+#pragma unroll
+            for (int cb = 0; cb < NCB; cb++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[cb][e] = 0;
+            // one step ahead: the window taps and weight fragments of step ks + 1 and the
+            // chunk offset of step ks + 2 are read while step ks is quantized (the offset
+            // table is padded with zeros past the last step, so the reads stay in the window)
+            int off_n = koff[2 + hi];
+            uint4 h0 = *reinterpret_cast<const uint4*>(pix + koff[hi]);
+            uint4 h1 = *reinterpret_cast<const uint4*>(pix + koff[hi] + 16);
+            v4i wf[NCB];
+#pragma unroll
+            for (int cb = 0; cb < NCB; cb++) wf[cb] = *reinterpret_cast<const v4i*>(wrow + cb * 32 * a.KWp);
+            for (int ks = 0; ks < a.ksteps; ks++) {
+                const uint4 c0 = h0, c1 = h1;
+                v4i wc[NCB];
+#pragma unroll
+                for (int cb = 0; cb < NCB; cb++) wc[cb] = wf[cb];
+                h0 = *reinterpret_cast<const uint4*>(pix + off_n);
+                h1 = *reinterpret_cast<const uint4*>(pix + off_n + 16);
+                off_n = koff[2 * ks + 4 + hi];
+                const int kn = ks + 1 < a.ksteps ? 32 * (ks + 1) : 0;
+#pragma unroll
+                for (int cb = 0; cb < NCB; cb++) wf[cb] = *reinterpret_cast<const v4i*>(wrow + cb * 32 * a.KWp + kn);
+                // (an empty asm that may write memory: the compiler otherwise folds the
+                // loop-carried loads back into loads at the top of the step, waited on at once)
+                asm volatile("" ::: "memory");
+                const v4i fb = quant16_cl(c0, c1, inv);
+#pragma unroll
+                for (int cb = 0; cb < NCB; cb++) acc[cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wc[cb], fb, acc[cb], 0, 0, 0);
+            }
+
+            // the epilogue as dequant_gemm: half(fma((float)acc, as * ws, bias)), with -0 as
+            // the bias without one; 2-byte buffer stores at 32-bit offsets, where pixels
+            // outside the image and channels past C_out fall past the range and are dropped
+            const __amdgpu_buffer_rsrc_t ry =
+                buf_rsrc(a.y + static_cast<size_t>(cur.n) * a.Co * (plane2 >> 1), a.y_bytes);
+            const int ho = cur.ho0 + pr, wo = cur.wo0 + pc;
+            const bool pok = p0 < a.npix && ho < a.Ho && wo < a.Wo;
+            const uint32_t vo = pok ? 2u * static_cast<uint32_t>(ho * a.Wo + wo) : 0x80000000u;
+#pragma unroll
+            for (int cb = 0; cb < NCB; cb++) {
+                const int co0 = cb * 32 + 4 * hi;
+                const uint32_t vc = vo + static_cast<uint32_t>(co0) * plane2;
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const float4 ws4 = *reinterpret_cast<const float4*>(s_ws + co0 + 8 * g);
+                    const float4 b4 = *reinterpret_cast<const float4*>(s_b + co0 + 8 * g);
+                    const float wsv[4] = {ws4.x, ws4.y, ws4.z, ws4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const uint16_t yv =
+                            f2h(__builtin_fmaf(static_cast<float>(acc[cb][4 * g + e]), scale * wsv[e], bv[e]));
+                        __builtin_amdgcn_raw_buffer_store_b16(yv, ry, vc + static_cast<uint32_t>(8 * g + e) * plane2, 0,
+                                                              0);
+                    }
+                }
+            }
+        }
+        if (!has_next) break;
+        walk.next = nxt;
+        cur = ng;
+        __syncthreads();   // the window and s_m1 are free for the next tile
+    }
+}
+
+// Workgroups of conv_nchw_cl_kernel<NCB, PF, NW> with lds bytes resident per CU, or minus a
+// HIP error (sets the 160 KB dynamic-LDS limit on first use).
+template <int NCB, bool PF, int NW>
+static int conv_nchw_cl_residency(size_t lds)
+{
+    static std::once_flag once;
+    static hipError_t attr;
+    const void* fn = reinterpret_cast<const void*>(&conv_nchw_cl_kernel<NCB, PF, NW>);
+    std::call_once(once, [&] { attr = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024); });
+    if (attr != hipSuccess) return -static_cast<int>(attr);
+    int blocks = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 64 * NW, lds);
+    if (e != hipSuccess) return -static_cast<int>(e);
+    return blocks > 0 ? blocks : 1;
+}
+
+template <int NCB, bool PF, int NW>
+static int conv_nchw_cl_launch(const ConvClArgs& a, size_t lds, hipStream_t s)
+{
+    int st = FORGE_OK;
+    const DeviceInfo& dinfo = device_info(&st);
+    if (st != FORGE_OK) return st;
+    const int per_cu = conv_nchw_cl_residency<NCB, PF, NW>(lds);
+    if (per_cu < 0) return -per_cu;
+    const long long total = static_cast<long long>(a.tiles) * a.N;
+    const long long cap = static_cast<long long>(dinfo.cu_count) * per_cu;
+    const unsigned grid = static_cast<unsigned>(total < cap ? total : cap);
+    note_route(PF ? "conv-nchw-cl prefetch" : "conv-nchw-cl", 32 * NW);
+    conv_nchw_cl_kernel<NCB, PF, NW><<<grid, 64 * NW, lds, s>>>(a);
+    return launch_status();
+}
+
+// Geometry of the channel-last path, or false when it does not apply (16-byte window loads
+// need W % 8 == 0 and an aligned input; C_out <= 128; window, weights and tables within 80 KB
+// of LDS so that two workgroups share a CU). The tile is Wt = 64 or 32 columns (fewer when the
+// output is narrower) by R = 128 / Wt rows, whichever loads fewer window positions per pixel.
+static bool conv_nchw_cl_plan(ConvClArgs& a, size_t* lds_bytes, int nw)
+{
+    const int npix_max = 32 * nw;
+    if (a.W % 8 != 0 || !aligned(a.x, 16) || a.Co > 128) return false;
+    a.Cp = (a.C + 15) & ~15;
+    a.CQ = a.Cp / 16;
+    const long long nch = static_cast<long long>(a.kH) * a.kW * a.CQ;
+    if (nch > 512) return false;
+    a.nch = static_cast<int>(nch);
+    a.ksteps = (a.nch + 1) / 2;
+    a.Pp = 2 * a.Cp + 16;
+    a.KWp = 32 * a.ksteps + 16;
+    const int cop = 32 * ((a.Co + 31) / 32);
+    const long long xb = 2LL * a.C * a.H * a.W;
+    if (xb >= (1LL << 30) || 2LL * cop * a.Ho * a.Wo >= (1LL << 31)) return false;
+    auto up16 = [](long long b) { return (b + 15) & ~15LL; };
+    long long best_bytes = -1;
+    double best_cost = 0.0;
+    for (const int wt_c : {64, 32}) {
+        const int Wt = a.Wo < wt_c ? a.Wo : wt_c;
+        const int R = std::min(npix_max / Wt, a.Ho);
+        const long long IH = static_cast<long long>(R - 1) * a.sH + static_cast<long long>(a.kH - 1) * a.dH + 1;
+        const long long IW = static_cast<long long>(Wt - 1) * a.sW + static_cast<long long>(a.kW - 1) * a.dW + 1;
+        const long long G = (IW + 7 + 7) / 8;   // the first column read sits at position 0..7
+        if (G > kWave) continue;
+        const long long win = IH * (8 * G + 1) * a.Pp;
+        const long long w_off = win, m1_off = w_off + static_cast<long long>(cop) * a.KWp;
+        const long long koff_off = m1_off + up16(4 * IH * IW), ws_off = koff_off + up16(4LL * (2 * a.ksteps + 4));
+        const long long bytes = ws_off + 8LL * cop;
+        if (bytes > 80 * 1024) continue;
+        const double cost = static_cast<double>(IH * 8 * G) / (R * Wt);
+        if (best_bytes < 0 || cost < best_cost) {
+            best_bytes = bytes;
+            best_cost = cost;
+            a.Wt = Wt;
+            a.R = R;
+            a.IH = static_cast<int>(IH);
+            a.IW = static_cast<int>(IW);
+            a.G = static_cast<int>(G);
+            a.w_off = static_cast<int>(w_off);
+            a.m1_off = static_cast<int>(m1_off);
+            a.koff_off = static_cast<int>(koff_off);
+            a.ws_off = static_cast<int>(ws_off);
+        }
+    }
+    if (best_bytes < 0) return false;
+    a.nw = nw;
+    a.npix = a.R * a.Wt;
+    a.IWr = 8 * a.G + 1;   // odd: the 8 positions a lane writes per row fall on different banks per row
+    a.rpi = kWave / a.G;
+    a.nrows = (a.Cp / 8) * a.IH;
+    a.ninst = (a.nrows + a.rpi - 1) / a.rpi;
+    a.mg_wt = udiv_multiplier(a.Wt);
+    a.mg_rpi = udiv_multiplier(a.rpi);
+    a.mg_ih = udiv_multiplier(a.IH);
+    a.mg_iw = udiv_multiplier(a.IW);
+    a.x_bytes = static_cast<uint32_t>(xb);
+    a.y_bytes = static_cast<uint32_t>(2LL * a.Co * a.Ho * a.Wo);
+    a.tiles_h = divup(a.Ho, a.R);
+    a.tiles_w = divup(a.Wo, a.Wt);
+    const long long tiles = static_cast<long long>(a.tiles_h) * a.tiles_w;
+    if (tiles * a.N > 0x7FFFFFFFLL) return false;
+    a.tiles = static_cast<int>(tiles);
+    // udiv_magic ranges of the tile decode and the weight fill (larger calls take the
+    // NCHW-window kernel)
+    if (tiles * a.N * tiles >= (1LL << 32) || tiles * a.tiles_w >= (1LL << 32)) return false;
+    if (1LL * a.Co * a.C * a.C >= (1LL << 32)) return false;
+    a.mg_c = udiv_multiplier(a.C);
+    a.wpad = a.C != a.Cp || a.Co % 32 != 0 || a.nch % 2 != 0;
+
+    a.mg_tiles = udiv_multiplier(a.tiles);
+    a.mg_tw = udiv_multiplier(a.tiles_w);
+    *lds_bytes = static_cast<size_t>(best_bytes);
+    return true;
+}
+
+template <int NW>
+static int conv_nchw_cl_nw(const ConvClArgs& a, size_t lds, hipStream_t s)
+{
+    // each wave holds at most one load instruction's data (the 8-wave plan guarantees it)
+    const bool pf = NW == 8 || a.ninst <= NW;
+    switch ((a.Co + 31) / 32) {
+        case 1: return pf ? conv_nchw_cl_launch<1, true, NW>(a, lds, s) : conv_nchw_cl_launch<1, NW == 8, NW>(a, lds, s);
+        case 2: return pf ? conv_nchw_cl_launch<2, true, NW>(a, lds, s) : conv_nchw_cl_launch<2, NW == 8, NW>(a, lds, s);
+        case 3: return pf ? conv_nchw_cl_launch<3, true, NW>(a, lds, s) : conv_nchw_cl_launch<3, NW == 8, NW>(a, lds, s);
+        default: return pf ? conv_nchw_cl_launch<4, true, NW>(a, lds, s) : conv_nchw_cl_launch<4, NW == 8, NW>(a, lds, s);
+    }
+}
+static int conv_nchw_cl(const ConvClArgs& a, size_t lds, hipStream_t s)
+{
+    return a.nw == 8 ? conv_nchw_cl_nw<8>(a, lds, s) : conv_nchw_cl_nw<4>(a, lds, s);
+}
+
 }  // namespace forge_amd
 
 using namespace forge_amd;
@@ -643,6 +1167,32 @@ extern "C" int forge_int8_conv2d_forward(const uint16_t* input, const int8_t* we
         return FORGE_EINVAL;
     const int M = Ho * Wo, K = C_in * kH * kW;
     hipStream_t s = as_stream(stream);
+    {
+        ConvClArgs a{};
+        a.x = input;
+        a.w = weight;
+        a.w_scale = w_scale;
+        a.bias = bias;
+        a.y = output;
+        a.C = C_in;
+        a.H = H;
+        a.W = W;
+        a.Co = C_out;
+        a.kH = kH;
+        a.kW = kW;
+        a.padH = padH;
+        a.padW = padW;
+        a.sH = strideH;
+        a.sW = strideW;
+        a.dH = dilH;
+        a.dW = dilW;
+        a.Ho = Ho;
+        a.Wo = Wo;
+        a.K = K;
+        a.N = N;
+        size_t lds = 0;
+        if (conv_nchw_cl_plan(a, &lds, 8) || conv_nchw_cl_plan(a, &lds, 4)) return conv_nchw_cl(a, lds, s);
+    }
     {
         ConvNchwArgs a{input, weight, w_scale, bias, output, C_in, H, W, C_out, kH, kW, padH, padW, strideH, strideW,
                        dilH, dilW, Ho, Wo, K};

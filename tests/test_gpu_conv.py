@@ -143,27 +143,24 @@ def test_conv_nchw_api(dev, orc, C, H, W, Co, k, pad, stride, dil, bias):
         assert err.max() < 0.5 and err.mean() < 0.1
 
 
-# The one-launch NCHW path (K % 16 == 0): 64-pixel tiles of one output row (partial column
-# tiles at Wo = 70), several output rows per tile when Wo < 64 (stride 2: Wo = 10, 6 rows),
-# two and more 32-channel blocks (Co = 48: partial), a 5x5 dilated kernel (K = 800), K % 32 ==
-# 16 (C = 48, 3x3: the last 32-deep step half past K), pointwise 1x1, three images. Every output
-# against the reference pipeline's composition on the oracle.
-FUSED_CASES = [(32, 64, 64, 32, 3, 1, 1, 1, True), (32, 45, 70, 48, 3, 1, 1, 1, True),
-               (16, 20, 20, 24, 3, 1, 2, 1, False), (32, 24, 40, 16, 5, 4, 1, 2, True),
-               (48, 17, 33, 16, 3, 1, 1, 1, True), (64, 33, 33, 128, 1, 0, 1, 1, True)]
+def _nchw_check(orc, y, x, w, ws, b, k, pad, stride, dil):
+    """Every output of every image against the reference pipeline composed on the oracle."""
+    N, Co = y.shape[0], y.shape[1]
+    for n in range(N):
+        cols, Ho, Wo = _im2col_nchw(x[n], k, k, (pad, pad), (stride, stride), (dil, dil))
+        assert y.shape[2:] == (Ho, Wo)
+        q, s = orc.quantize_rows(cols)
+        ref = orc.gemm_dequant(q, w, s, ws, b)
+        got = y[n].reshape(Co, -1).T.copy().view(np.uint16)
+        bad = int((got != ref.view(np.uint16)).sum())
+        assert bad == 0, f"image {n}: {bad} of {got.size} outputs differ"
 
 
-@pytest.mark.parametrize("C,H,W,Co,k,pad,stride,dil,bias", FUSED_CASES)
-def test_conv_nchw_fused(dev, orc, C, H, W, Co, k, pad, stride, dil, bias):
+def _nchw_run(dev, x, w, ws, b, k, pad, stride, dil):
     import torch
     from forge_amd import ops
-    rng = np.random.default_rng(C * W + Co + k)
-    N = 3
-    x = rng.uniform(-1, 1, (N, C, H, W)).astype(np.float16)
-    w = int8_uniform(rng, (Co, C * k * k))
-    ws = rng.uniform(0.005, 0.05, Co).astype(np.float16)
-    b = rng.uniform(-0.5, 0.5, Co).astype(np.float16) if bias else None
-    say(f"conv nchw fused C={C} H={H} W={W} Co={Co} k={k} s={stride} d={dil}")
+    N, _, H, W = x.shape
+    Co = w.shape[0]
     Ho = (H + 2 * pad - dil * (k - 1) - 1) // stride + 1
     Wo = (W + 2 * pad - dil * (k - 1) - 1) // stride + 1
     out = torch.empty((N, Co, Ho, Wo), dtype=torch.float16, device=dev)
@@ -171,66 +168,85 @@ def test_conv_nchw_fused(dev, orc, C, H, W, Co, k, pad, stride, dil, bias):
     y = to_host(ops.int8_conv2d_forward(to_dev(x, dev), to_dev(w, dev), to_dev(ws, dev),
                                         None if b is None else to_dev(b, dev), k, k, (pad, pad), (stride, stride),
                                         (dil, dil), out=out))
-    assert ops.last_route().startswith("conv-nchw-fused")
-    for n in range(N):
-        cols, Ho2, Wo2 = _im2col_nchw(x[n], k, k, (pad, pad), (stride, stride), (dil, dil))
-        assert (Ho2, Wo2) == (Ho, Wo)
-        q, s = orc.quantize_rows(cols)
-        ref = orc.gemm_dequant(q, w, s, ws, b)
-        got = y[n].reshape(Co, -1).T.copy().view(np.uint16)
-        bad = int((got != ref.view(np.uint16)).sum())
-        assert bad == 0, f"image {n}: {bad} of {got.size} outputs differ"
+    return y, ops.last_route()
+
+
+# The one-launch NCHW paths. "conv-nchw-cl": channel-last window (W % 8 == 0, C_out <= 128,
+# LDS <= 80 KB), tiles of 32 output pixels per wave (8 waves: "tile256", else 4: "tile128"),
+# weights permuted to the (kh, kw, c) order in LDS; with the next tile's window loads in flight
+# ("prefetch") when each wave has at most one load instruction per tile. "conv-nchw-fused":
+# NCHW window, 64-pixel tiles (K % 16 == 0).
+# Cases: 64 x 4 tiles; C = 24 (channels padded to 32 with zeros) with C_out = 48 (two
+# 32-channel blocks, the second partial); C = 16 (odd chunk count: the last 32-deep step half
+# past the patch) at stride 2 with C_out = 64 and Wo = 24 (pixel blocks across output rows);
+# C = 8 with a dilated 5x5 and C_out = 96 (4 waves: the 8-wave window does not fit); RGB input
+# (C = 3); pointwise 1x1 with Wo = 24, a partial last pixel block and C_out = 128; C = 64 (4
+# waves, five load instructions: no prefetch); the NCHW-window kernel at W % 8 != 0 (several
+# rows per tile at Wo = 10, K % 32 == 16, 1x1) and at C_out > 128 (a dilated 5x5).
+FUSED_CASES = [(32, 64, 64, 32, 3, 1, 1, 1, True, "conv-nchw-cl prefetch tile256"),
+               (24, 20, 72, 48, 3, 1, 1, 1, True, "conv-nchw-cl prefetch tile256"),
+               (16, 30, 48, 64, 3, 1, 2, 1, False, "conv-nchw-cl prefetch tile256"),
+               (8, 33, 40, 96, 5, 4, 1, 2, True, "conv-nchw-cl prefetch tile128"),
+               (3, 32, 32, 16, 3, 1, 1, 1, True, "conv-nchw-cl prefetch tile256"),
+               (48, 17, 24, 128, 1, 0, 1, 1, True, "conv-nchw-cl prefetch tile256"),
+               (64, 40, 96, 32, 3, 1, 1, 1, True, "conv-nchw-cl tile128"),
+               (32, 45, 70, 48, 3, 1, 1, 1, True, "conv-nchw-fused"),
+               (16, 20, 20, 24, 3, 1, 2, 1, False, "conv-nchw-fused"),
+               (32, 24, 40, 160, 5, 4, 1, 2, True, "conv-nchw-fused"),
+               (48, 17, 33, 16, 3, 1, 1, 1, True, "conv-nchw-fused"),
+               (64, 33, 33, 128, 1, 0, 1, 1, True, "conv-nchw-fused")]
+
+
+@pytest.mark.parametrize("C,H,W,Co,k,pad,stride,dil,bias,route", FUSED_CASES)
+def test_conv_nchw_fused(dev, orc, C, H, W, Co, k, pad, stride, dil, bias, route):
+    rng = np.random.default_rng(C * W + Co + k)
+    N = 3
+    x = rng.uniform(-1, 1, (N, C, H, W)).astype(np.float16)
+    w = int8_uniform(rng, (Co, C * k * k))
+    ws = rng.uniform(0.005, 0.05, Co).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, Co).astype(np.float16) if bias else None
+    say(f"conv nchw one-launch C={C} H={H} W={W} Co={Co} k={k} s={stride} d={dil} ({route})")
+    y, got_route = _nchw_run(dev, x, w, ws, b, k, pad, stride, dil)
+    assert got_route == route if route.startswith("conv-nchw-cl") else got_route.startswith(route), got_route
+    _nchw_check(orc, y, x, w, ws, b, k, pad, stride, dil)
 
 
 # Shapes with more tiles than the persistent grid holds (each workgroup walks several tiles):
-# 16-byte window loads with the next tile's loads in flight, 16-byte loads without (a window of
-# more than 16 load rounds), and 2-byte loads (W % 8 != 0).
-PERSISTENT_CASES = [(4, 16, 256, 512, 16, "conv-nchw-fused prefetch"), (2, 128, 64, 256, 32, "conv-nchw-fused"),
+# the channel-last kernel with and without the next tile's loads in flight; the NCHW-window
+# kernel with 16-byte loads and prefetch (C_out > 128), 16-byte loads without (a window of
+# more than 16 load rounds at C = 128) and 2-byte loads (W % 8 != 0).
+PERSISTENT_CASES = [(4, 16, 256, 512, 16, "conv-nchw-cl prefetch tile256"), (2, 64, 256, 256, 32, "conv-nchw-cl tile128"),
+                    (2, 16, 256, 512, 160, "conv-nchw-fused prefetch"), (2, 128, 64, 256, 32, "conv-nchw-fused"),
                     (3, 16, 200, 250, 24, "conv-nchw-fused")]
 
 
 @pytest.mark.parametrize("N,C,H,W,Co,route", PERSISTENT_CASES)
 def test_conv_nchw_fused_persistent(dev, orc, N, C, H, W, Co, route):
-    import torch
-    from forge_amd import ops
     rng = np.random.default_rng(N * C + W)
     x = rng.uniform(-1, 1, (N, C, H, W)).astype(np.float16)
     w = int8_uniform(rng, (Co, C * 9))
     ws = rng.uniform(0.005, 0.05, Co).astype(np.float16)
     b = rng.uniform(-0.5, 0.5, Co).astype(np.float16)
-    say(f"conv nchw fused persistent N={N} C={C} H={H} W={W} Co={Co}")
-    out = torch.empty((N, Co, H, W), dtype=torch.float16, device=dev)
-    poison(out, 0x7B)
-    y = to_host(ops.int8_conv2d_forward(to_dev(x, dev), to_dev(w, dev), to_dev(ws, dev), to_dev(b, dev), 3, 3,
-                                        (1, 1), (1, 1), (1, 1), out=out))
-    assert ops.last_route() == route
-    for n in range(N):
-        cols, Ho, Wo = _im2col_nchw(x[n], 3, 3, (1, 1), (1, 1), (1, 1))
-        q, s = orc.quantize_rows(cols)
-        ref = orc.gemm_dequant(q, w, s, ws, b)
-        got = y[n].reshape(Co, -1).T.copy().view(np.uint16)
-        bad = int((got != ref.view(np.uint16)).sum())
-        assert bad == 0, f"image {n}: {bad} of {got.size} outputs differ"
+    say(f"conv nchw one-launch persistent N={N} C={C} H={H} W={W} Co={Co} ({route})")
+    y, got_route = _nchw_run(dev, x, w, ws, b, 3, 1, 1, 1)
+    assert got_route == route, got_route
+    _nchw_check(orc, y, x, w, ws, b, 3, 1, 1, 1)
 
 
-def test_conv_nchw_fused_special_values(dev, orc):
-    """Patches holding NaN, +-inf, subnormals and all-zero windows through the one-launch path:
+@pytest.mark.parametrize("W,Co,route", [(80, 32, "conv-nchw-cl prefetch tile256"), (84, 32, "conv-nchw-fused"),
+                                        (80, 160, "conv-nchw-fused prefetch")])
+def test_conv_nchw_fused_special_values(dev, orc, W, Co, route):
+    """Patches holding NaN, +-inf, subnormals and all-zero windows through the one-launch paths:
     the same bits as quantize_rows on the reference's im2col rows, then its GEMM epilogue."""
-    from forge_amd import ops
     from helpers import special_fp16_rows
     rng = np.random.default_rng(77)
-    N, C, H, W, Co = 2, 16, 12, 80, 32
+    N, C, H = 2, 16, 12
     x = special_fp16_rows(rng, N * C * H, W).reshape(N, C, H, W)
     x[1, :, 4:7, 10:20] = 0
     w = int8_uniform(rng, (Co, C * 9))
     ws = rng.uniform(0.005, 0.05, Co).astype(np.float16)
     b = rng.uniform(-0.5, 0.5, Co).astype(np.float16)
-    say("conv nchw fused special values")
-    y = to_host(ops.int8_conv2d_forward(to_dev(x, dev), to_dev(w, dev), to_dev(ws, dev), to_dev(b, dev), 3, 3,
-                                        (1, 1), (1, 1), (1, 1)))
-    assert ops.last_route().startswith("conv-nchw-fused")
-    for n in range(N):
-        cols, Ho, Wo = _im2col_nchw(x[n], 3, 3, (1, 1), (1, 1), (1, 1))
-        q, s = orc.quantize_rows(cols)
-        ref = orc.gemm_dequant(q, w, s, ws, b)
-        assert np.array_equal(y[n].reshape(Co, -1).T.copy().view(np.uint16), ref.view(np.uint16))
+    say(f"conv nchw one-launch special values W={W} Co={Co} ({route})")
+    y, got_route = _nchw_run(dev, x, w, ws, b, 3, 1, 1, 1)
+    assert got_route == route, got_route
+    _nchw_check(orc, y, x, w, ws, b, 3, 1, 1, 1)
