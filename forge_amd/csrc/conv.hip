@@ -629,8 +629,9 @@ static bool conv_nchw_fused_plan(ConvNchwArgs& a, int N, size_t* lds_bytes, bool
 //     v_mfma_i32_32x32x32_i8, which it feeds straight to the MFMA (no INT8 tile in LDS, no
 //     barrier between quantize and MFMA), for every 32-channel block of C_out.
 //   * The per-pixel scale is the max over the pixel's kH x kW window positions of each
-//     position's channel absmax (fp16 bit patterns, as the one-launch NCHW kernel takes them),
-//     computed once per position by the whole workgroup.
+//     position's channel absmax (fp16 magnitude bit patterns, as the one-launch NCHW kernel
+//     takes them), which the lanes that write the window take over their 8 channels in
+//     registers and merge per position with LDS atomic maxima (no pass of its own).
 // A tile is R output rows x Wt columns (R Wt <= 128); workgroups are persistent and walk their
 // XCD's contiguous range of tiles, with the next tile's window loads in flight during the
 // current tile (when a wave has at most one load instruction per tile).
@@ -705,7 +706,8 @@ __global__ __launch_bounds__(64 * NW, (NCB == 1 ? 16 : NCB == 2 ? 12 : 8) / NW) 
     extern __shared__ __align__(16) int8_t lds[];
     int8_t* win = lds;
     int8_t* wl = lds + a.w_off;
-    float* s_m1 = reinterpret_cast<float*>(lds + a.m1_off);
+    // the tile's channel maxima (tagged), IH x IW entries
+    uint32_t* s_m1u = reinterpret_cast<uint32_t*>(lds + a.m1_off);
     int* koff = reinterpret_cast<int*>(lds + a.koff_off);
     float* s_ws = reinterpret_cast<float*>(lds + a.ws_off);
     float* s_b = s_ws + 32 * NCB;
@@ -716,6 +718,7 @@ __global__ __launch_bounds__(64 * NW, (NCB == 1 ? 16 : NCB == 2 ? 12 : 8) / NW) 
     const int l31 = lane & 31, hi = lane >> 5;
     const int HW = a.H * a.W;
     const int khw = a.kH * a.kW;
+    const int m1n = a.IH * a.IW;
     const uint32_t plane2 = 2u * static_cast<uint32_t>(a.Ho * a.Wo);
     const bool has_bias = a.bias != nullptr;
 
@@ -763,8 +766,12 @@ __global__ __launch_bounds__(64 * NW, (NCB == 1 ? 16 : NCB == 2 ? 12 : 8) / NW) 
             v[u] = __builtin_amdgcn_raw_buffer_load_b128(
                 rx, (ok & (u < cleft)) ? base + static_cast<uint32_t>(2 * u * HW) : 0x80000000u, 0, 0);
     };
-    // the 8 x 8 block transposed by v_perm into 8 positions of 8 channels (16 bytes each)
-    auto write_rows = [&](int i, const v4i* v) {
+    // the 8 x 8 block transposed by v_perm into 8 positions of 8 channels (16 bytes each); and
+    // per position read by the tile (columns s0 .. s0 + IW - 1) the maximum of the 8 channels'
+    // fp16 magnitude bit patterns, merged into the tile's channel maxima by LDS atomic maxima
+    // of (tag << 15 | bits): a tile's tag exceeds every earlier tile's, so its first merge
+    // replaces an entry left by an earlier tile (no zeroing between tiles)
+    auto write_rows = [&](int i, const v4i* v, int s0, uint32_t tag) {
         const int r = i * a.rpi + slot;
         if (!lok || r >= a.nrows) return;
         const int cg = udiv_magic(r, a.mg_ih), ih = r - cg * a.IH;
@@ -779,6 +786,20 @@ __global__ __launch_bounds__(64 * NW, (NCB == 1 ? 16 : NCB == 2 ? 12 : 8) / NW) 
             o.z = __builtin_amdgcn_perm(static_cast<uint32_t>(v[5][d]), static_cast<uint32_t>(v[4][d]), sel);
             o.w = __builtin_amdgcn_perm(static_cast<uint32_t>(v[7][d]), static_cast<uint32_t>(v[6][d]), sel);
             *reinterpret_cast<uint4*>(dst + jj * a.Pp) = o;
+        }
+        if constexpr (!PF) return;   // without prefetch a pass of its own takes the maxima
+        const int iw0 = 8 * grp - s0;   // window column of this group's first position
+        uint32_t* mrow = s_m1u + ih * a.IW + iw0;
+        const uint32_t tg = tag << 15;
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            uint32_t cm = static_cast<uint32_t>(v[0][d]) & 0x7FFF7FFFu;
+#pragma unroll
+            for (int u = 1; u < 8; u++) cm = pk_max_u16(cm, static_cast<uint32_t>(v[u][d]) & 0x7FFF7FFFu);
+            if (static_cast<unsigned>(iw0 + 2 * d) < static_cast<unsigned>(a.IW))
+                __hip_atomic_fetch_max(mrow + 2 * d, tg | (cm & 0xFFFFu), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (static_cast<unsigned>(iw0 + 2 * d + 1) < static_cast<unsigned>(a.IW))
+                __hip_atomic_fetch_max(mrow + 2 * d + 1, tg | (cm >> 16), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     };
 
@@ -858,18 +879,28 @@ __global__ __launch_bounds__(64 * NW, (NCB == 1 ? 16 : NCB == 2 ? 12 : 8) / NW) 
             s_ws[c] = c < a.Co ? h2f(a.w_scale[c]) : 0.0f;
             s_b[c] = c < a.Co && has_bias ? h2f(a.bias[c]) : -0.0f;
         }
+        for (int i = t; i < m1n; i += kThr) s_m1u[i] = 0u;
+        __syncthreads();   // zeroed (tag 0) before the first tile's atomics
     }
 
+    constexpr uint32_t kTagMax = 0x1FFFFu;   // 17 tag bits above the 15 magnitude bits
+    uint32_t tag = 1;
     while (true) {
-        // the current tile's window into LDS (the previous tile's readers are past the
-        // barrier at the end of the loop)
+        // the current tile's window into LDS and its channel maxima (the previous tile's readers
+        // are past the barrier at the end of the loop); after kTagMax tiles the maxima start
+        // over from zero
+        if (tag > kTagMax) {
+            for (int i = t; i < m1n; i += kThr) s_m1u[i] = 0u;
+            __syncthreads();
+            tag = 1;
+        }
         if constexpr (PF) {
-            if (wave < a.ninst) write_rows(wave, pf);
+            if (wave < a.ninst) write_rows(wave, pf, cur.s0, tag);
         } else {
             for (int i = wave; i < a.ninst; i += NW) {
                 v4i v[8];
                 issue_rows(cur, i, v);
-                write_rows(i, v);
+                write_rows(i, v, cur.s0, tag);
             }
         }
         const int nxt = walk.next + walk.stride;
@@ -879,33 +910,22 @@ __global__ __launch_bounds__(64 * NW, (NCB == 1 ? 16 : NCB == 2 ? 12 : 8) / NW) 
         __syncthreads();
         if constexpr (PF) {
             if (has_next && wave < a.ninst) issue_rows(ng, wave, pf);   // in flight while this tile computes
-        }
-
-        // 2. per window position (IH rows x IW columns from s0) the channel absmax on fp16
-        //    magnitude bit patterns; a maximum above 0x7C00 is a NaN, and the position then
-        //    takes the fp32 maximum, which skips NaN as the reference quantizer's reduction does
-        //    The maxima are stored as fp32 bit patterns: never NaN and never negative, they
-        //    order as unsigned integers.
-        uint32_t* s_m1u = reinterpret_cast<uint32_t*>(s_m1);
-        for (int q = t; q < a.IH * a.IW; q += kThr) {
-            const int ih = udiv_magic(q, a.mg_iw), iw = q - ih * a.IW;
-            const int8_t* src = win + (ih * a.IWr + cur.s0 + iw) * a.Pp;
-            uint32_t mb = 0u;
-            for (int c8 = 0; c8 < a.Cp; c8 += 16) {   // Cp % 16 == 0: two 16-byte reads in flight
-                const uint4 v0 = *reinterpret_cast<const uint4*>(src + 2 * c8);
-                const uint4 v1 = *reinterpret_cast<const uint4*>(src + 2 * c8 + 16);
-                mb = absbits8(v1, absbits8(v0, mb));
+        } else {
+            // the channel maxima by a pass over the window positions, spread over all threads
+            // (the loading lanes hold more than one load instruction's data here)
+            for (int q = t; q < m1n; q += kThr) {
+                const int ih = udiv_magic(q, a.mg_iw), iw = q - ih * a.IW;
+                const int8_t* src = win + (ih * a.IWr + cur.s0 + iw) * a.Pp;
+                uint32_t mb = 0u;
+                for (int c8 = 0; c8 < a.Cp; c8 += 16) {   // Cp % 16 == 0: two 16-byte reads in flight
+                    const uint4 v0 = *reinterpret_cast<const uint4*>(src + 2 * c8);
+                    const uint4 v1 = *reinterpret_cast<const uint4*>(src + 2 * c8 + 16);
+                    mb = absbits8(v1, absbits8(v0, mb));
+                }
+                s_m1u[q] = (tag << 15) | max(mb & 0xFFFFu, mb >> 16);
             }
-            const uint32_t m16 = max(mb & 0xFFFFu, mb >> 16);
-            float m = h2f(static_cast<uint16_t>(m16));
-            if (m16 > kHalfInfBits) {
-                m = 0.0f;
-                for (int c = 0; c < a.Cp; c++)
-                    m = fmaxf(m, fabsf(h2f(*reinterpret_cast<const uint16_t*>(src + 2 * c))));
-            }
-            s_m1u[q] = __float_as_uint(m);
+            __syncthreads();
         }
-        __syncthreads();
 
         // 3./4./5. per wave: 32 pixels' scales, the quantized B fragments fed to the MFMAs,
         //    the dequant epilogue stored to NCHW (2-byte buffer stores; pixels outside the
@@ -914,8 +934,11 @@ __global__ __launch_bounds__(64 * NW, (NCB == 1 ? 16 : NCB == 2 ? 12 : 8) / NW) 
             const int p0 = 32 * wave + l31;
             const int p = p0 < a.npix ? p0 : a.npix - 1;
             const int pr = udiv_magic(p, a.mg_wt), pc = p - pr * a.Wt;
-            // the pixel's kH x kW positions, three reads in flight; a read past the last tap
-            // takes tap (0, 0) again, which leaves the maximum as it is
+            // the pixel's kH x kW window positions (tagged channel maxima, fp16 magnitude bit
+            // patterns), three reads in flight; a read past the last tap takes tap (0, 0) again,
+            // which leaves the maximum as it is. A maximum above 0x7C00 is a NaN: the pixel then
+            // takes the fp32 maximum over its taps, which skips NaN as the reference quantizer's
+            // reduction does.
             const uint32_t* mr = s_m1u + pr * a.sH * a.IW + pc * a.sW;
             uint32_t mu = 0u;
             int kh = 0, kw = 0;
@@ -932,7 +955,17 @@ __global__ __launch_bounds__(64 * NW, (NCB == 1 ? 16 : NCB == 2 ? 12 : 8) / NW) 
                 }
                 mu = max(mu, max(v[0], max(v[1], v[2])));
             }
-            const float m = __uint_as_float(mu);
+            mu &= 0x7FFFu;   // the tag (the same for all of this tile's entries) off
+            float m = h2f(static_cast<uint16_t>(mu));
+            if (mu > kHalfInfBits) {
+                m = 0.0f;
+                for (int kh2 = 0; kh2 < a.kH; kh2++)
+                    for (int kw2 = 0; kw2 < a.kW; kw2++) {
+                        const uint16_t* xp = reinterpret_cast<const uint16_t*>(
+                            win + ((pr * a.sH + kh2 * a.dH) * a.IWr + cur.s0 + pc * a.sW + kw2 * a.dW) * a.Pp);
+                        for (int c = 0; c < a.Cp; c++) m = fmaxf(m, fabsf(h2f(xp[c])));
+                    }
+            }
             const float scale = row_scale(m);
             const float inv = 1.0f / scale;
 
@@ -1001,7 +1034,8 @@ __global__ __launch_bounds__(64 * NW, (NCB == 1 ? 16 : NCB == 2 ? 12 : 8) / NW) 
         if (!has_next) break;
         walk.next = nxt;
         cur = ng;
-        __syncthreads();   // the window and s_m1 are free for the next tile
+        tag++;
+        __syncthreads();   // the window and the maxima are free for the next tile
     }
 }
 
