@@ -905,11 +905,9 @@ __global__ __launch_bounds__(64 * NW, (NCB == 1 ? 16 : NCB == 2 ? 12 : 8) / NW) 
         }
         const int nxt = walk.next + walk.stride;
         const bool has_next = nxt < walk.end;
-        Geo ng = cur;
-        if (has_next) ng = geo_of(nxt);
         __syncthreads();
         if constexpr (PF) {
-            if (has_next && wave < a.ninst) issue_rows(ng, wave, pf);   // in flight while this tile computes
+            if (has_next && wave < a.ninst) issue_rows(geo_of(nxt), wave, pf);   // in flight while this tile computes
         } else {
             // the channel maxima by a pass over the window positions, spread over all threads
             // (the loading lanes hold more than one load instruction's data here)
@@ -1033,7 +1031,7 @@ __global__ __launch_bounds__(64 * NW, (NCB == 1 ? 16 : NCB == 2 ? 12 : 8) / NW) 
         }
         if (!has_next) break;
         walk.next = nxt;
-        cur = ng;
+        cur = geo_of(nxt);   // (decoded again rather than kept live across the tile)
         tag++;
         __syncthreads();   // the window and the maxima are free for the next tile
     }
