@@ -333,6 +333,7 @@ PROBE_TITLES = {
     "c4_dense_M16": "configs[3] M=16 dense decode GEMM (`decode_dense_kernel`)",
     "c4_sparse_M16": "configs[3] M=16 2:4 decode GEMM (`decode_sparse_reg_kernel`)",
     "f1_fq": "fused quantize + 2:4 sparse linear 1280->320 at M=147,456 (`sparse_fq_kernel<5,48,true,3>`)",
+    "f2_conv_nchw": "`int8_conv2d_forward` NCHW FP16 (1,32,540,960) 3x3 -> 32 (`conv_nchw_cl_kernel<1,true,8>`: channel-last window, 256-pixel tiles)",
 }
 
 
