@@ -171,6 +171,67 @@ __device__ __forceinline__ uint2 quant8_row(uint4 v, float inv) {
     return make_uint2(pack_low_bytes(b[0], b[1], b[2], b[3]), pack_low_bytes(b[4], b[5], b[6], b[7]));
 }
 
+// fl(h * inv) for the fp16 in the low / high half of h, as one v_fma_mix_f32 (the widening
+// inside, fma(x, inv, +0) rounds the product once as the multiply does; only a zero's sign can
+// differ, which the rounding add below erases).
+__device__ __forceinline__ float fma_mix_lo(uint32_t h, float inv) {
+    float p;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(p) : "v"(h), "v"(inv));
+    return p;
+}
+__device__ __forceinline__ float fma_mix_hi(uint32_t h, float inv) {
+    float p;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(p) : "v"(h), "v"(inv));
+    return p;
+}
+// 16 rounded products -> 16 INT8 bytes (byte k of dword d from p[4 d + k]), the bytes of
+// qrow_bits: one SDWA add of 1.5 * 2^23 per value whose low result byte goes straight into its
+// byte of the dword (dst_sel:BYTE_k; a dword's first write zero-pads it, the others keep the
+// bytes already there), in place of an add and a quarter of a 3-instruction pack. The adds
+// cycle over the 4 dwords, so no add reads a dword the instruction just before it wrote (a
+// byte-select write read by the next VALU instruction needs a wait state on this
+// architecture), and the block ends with one for the instruction that reads the dwords.
+__device__ __forceinline__ uint4 pack16_rint_sdwa(const float (&p)[16]) {
+    const float magic = 12582912.0f;
+    uint32_t q0, q1, q2, q3;
+    asm("v_add_f32_sdwa %0, %4, %20 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %1, %8, %20 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %2, %12, %20 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %3, %16, %20 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %0, %5, %20 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %1, %9, %20 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %2, %13, %20 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %3, %17, %20 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %0, %6, %20 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %1, %10, %20 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %2, %14, %20 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %3, %18, %20 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %0, %7, %20 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %1, %11, %20 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %2, %15, %20 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "v_add_f32_sdwa %3, %19, %20 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
+        "s_nop 0"
+        : "=&v"(q0), "=&v"(q1), "=&v"(q2), "=&v"(q3)
+        : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5]), "v"(p[6]), "v"(p[7]), "v"(p[8]),
+          "v"(p[9]), "v"(p[10]), "v"(p[11]), "v"(p[12]), "v"(p[13]), "v"(p[14]), "v"(p[15]), "v"(magic));
+    return make_uint4(q0, q1, q2, q3);
+}
+// Two rows' 8 halves each -> their 8 INT8 values (qa from a with inv_a, qb from b with inv_b),
+// each equal to quant8_row of that row.
+__device__ __forceinline__ void quant8_rows2(uint4 a, float inv_a, uint4 b, float inv_b, uint2& qa, uint2& qb) {
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float p[16];
+#pragma unroll
+    for (int d = 0; d < 8; d++) {
+        const float inv = d < 4 ? inv_a : inv_b;
+        p[2 * d] = fma_mix_lo(w[d], inv);
+        p[2 * d + 1] = fma_mix_hi(w[d], inv);
+    }
+    const uint4 q = pack16_rint_sdwa(p);
+    qa = make_uint2(q.x, q.y);
+    qb = make_uint2(q.z, q.w);
+}
+
 // GEMM dequant epilogue: half(fma((float)acc, as*ws, bias)), or acc*(as*ws) without bias.
 __device__ __forceinline__ uint16_t dequant_gemm(int acc, float as, float ws, float b, bool has_bias) {
     const float s = as * ws;

@@ -659,43 +659,16 @@ struct ConvClArgs {
 
 
 // 16 fp16 taps (8 dwords, two per dword, lower address in the low half) -> 16 INT8 values:
-// per tap one v_fma_mix_f32 (the rounded product, as qrow_bits_mix) and one SDWA add of
-// 1.5 * 2^23 whose low result byte (the INT8 value) goes straight into its byte of the
-// fragment dword (dst_sel:BYTE_k; the first write of a dword zero-pads it, the others keep
-// the bytes already there). The 16 adds cycle over the 4 dwords, so no add reads a dword the
-// add just before it wrote (a byte-select write read by the next VALU instruction needs a
-// wait state on this architecture), and the block ends with one for the MFMA that reads them.
+// per tap one v_fma_mix_f32 (the rounded product) and one SDWA add (pack16_rint_sdwa).
 __device__ __forceinline__ v4i quant16_cl(uint4 h0, uint4 h1, float inv) {
     const uint32_t w[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
     float p[16];
 #pragma unroll
     for (int d = 0; d < 8; d++) {
-        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(p[2 * d]) : "v"(w[d]), "v"(inv));
-        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(p[2 * d + 1]) : "v"(w[d]), "v"(inv));
+        p[2 * d] = fma_mix_lo(w[d], inv);
+        p[2 * d + 1] = fma_mix_hi(w[d], inv);
     }
-    const float magic = 12582912.0f;
-    uint32_t q0, q1, q2, q3;
-    asm("v_add_f32_sdwa %0, %4, %20 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD\n\t"
-        "v_add_f32_sdwa %1, %8, %20 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD\n\t"
-        "v_add_f32_sdwa %2, %12, %20 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD\n\t"
-        "v_add_f32_sdwa %3, %16, %20 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:DWORD\n\t"
-        "v_add_f32_sdwa %0, %5, %20 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
-        "v_add_f32_sdwa %1, %9, %20 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
-        "v_add_f32_sdwa %2, %13, %20 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
-        "v_add_f32_sdwa %3, %17, %20 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
-        "v_add_f32_sdwa %0, %6, %20 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
-        "v_add_f32_sdwa %1, %10, %20 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
-        "v_add_f32_sdwa %2, %14, %20 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
-        "v_add_f32_sdwa %3, %18, %20 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
-        "v_add_f32_sdwa %0, %7, %20 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
-        "v_add_f32_sdwa %1, %11, %20 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
-        "v_add_f32_sdwa %2, %15, %20 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
-        "v_add_f32_sdwa %3, %19, %20 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD src1_sel:DWORD\n\t"
-        "s_nop 0"
-        : "=&v"(q0), "=&v"(q1), "=&v"(q2), "=&v"(q3)
-        : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5]), "v"(p[6]), "v"(p[7]), "v"(p[8]),
-          "v"(p[9]), "v"(p[10]), "v"(p[11]), "v"(p[12]), "v"(p[13]), "v"(p[14]), "v"(p[15]), "v"(magic));
-    return v4i{static_cast<int>(q0), static_cast<int>(q1), static_cast<int>(q2), static_cast<int>(q3)};
+    return __builtin_bit_cast(v4i, pack16_rint_sdwa(p));
 }
 
 template <int NCB, bool PF, int NW>

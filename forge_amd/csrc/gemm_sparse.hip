@@ -1417,7 +1417,7 @@ int sparse_gemm(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, con
 //     together, before the previous batch is quantized; the last batch of a tile fetches the
 //     first batch of the next, across the barrier. Row absmax on fp16 bit patterns (one
 //     packed u16 max per two values, DPP across the wave, two rows per reduction), values by
-//     quant8_row: the arithmetic of quantize_rows.
+//     quant8_rows2 (two rows at a time, SDWA byte inserts): the arithmetic of quantize_rows.
 //   - consumer waves 0..3 run tile t from the other buffer: each owns NBW consecutive 16-row
 //     weight blocks per pass, streams their compressed bytes and index words straight from
 //     L2 into registers (kFqAhead K steps ahead, in the SMFMAC lane layout), reads the
@@ -1510,6 +1510,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             abits[u] = r2 & 0xFFFFu;
             abits[u + 1] = r2 >> 16;
         }
+        float inv[kR];
 #pragma unroll
         for (int u = 0; u < kR; u++) {
             float amax;
@@ -1521,17 +1522,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             } else {
                 amax = h2f(static_cast<uint16_t>(abits[u]));
             }
-            const int r = r0 + u;
             const float scale = row_scale(amax);
-            const float inv = 1.0f / scale;
-            if (ln == 0) sc[r] = scale;
+            inv[u] = 1.0f / scale;
+            if (ln == 0) sc[r0 + u] = scale;
+        }
+        // two rows' vectors at a time: quant8_rows2's SDWA byte inserts need 4 dwords to cycle over
+#pragma unroll
+        for (int u = 0; u < kR; u += 2) {
 #pragma unroll
             for (int i = 0; i < NV; i++) {
                 const int idx = ln + kWave * i;
+                uint2 qa, qb;
+                quant8_rows2(v[u][i], inv[u], v[u + 1][i], inv[u + 1], qa, qb);
                 if (idx < nvec) {
                     const int k = 8 * idx;
-                    *reinterpret_cast<uint2*>(Xs + (k >> 7) * kSlab + sp_b_off(r, (k >> 4) & 7) + (k & 8)) =
-                        quant8_row(v[u][i], inv);
+                    int8_t* xk = Xs + (k >> 7) * kSlab + (k & 8);
+                    *reinterpret_cast<uint2*>(xk + sp_b_off(r0 + u, (k >> 4) & 7)) = qa;
+                    *reinterpret_cast<uint2*>(xk + sp_b_off(r0 + u + 1, (k >> 4) & 7)) = qb;
                 }
             }
         }
