@@ -138,15 +138,6 @@ struct ConvNchwArgs {
 
 constexpr int kCnPix = 64;     // output pixels per workgroup tile
 
-// One value of a quantized row as qrow_bits computes it, with the fp16 widening and the product
-// in one v_fma_mix_f32 (f16 source in the low half, fp32 inv, + 0): fma(a, b, 0) rounds a b once
-// as the multiply does (only a zero's sign can differ, and the + 1.5 2^23 erases it).
-__device__ __forceinline__ uint32_t qrow_bits_mix(uint32_t h, float inv) {
-    float p;
-    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(p) : "v"(h), "v"(inv));
-    return __float_as_uint(p + 12582912.0f);
-}
-
 // A persistent workgroup runs tiles start, start + stride, ... of its XCD's contiguous range
 // (xcd_contiguous's split of the tiles over the 8 XCDs), so the workgroups of one XCD work on
 // neighbouring tiles together and share their window halos in that XCD's L2.
@@ -466,13 +457,10 @@ __global__ __launch_bounds__(256, 4) void conv_nchw_fused_kernel(ConvNchwArgs a)
                     uint32_t h[16];
 #pragma unroll
                     for (int j = 0; j < 16; j++) h[j] = xin[base + o[j]];
-                    uint32_t b[16];
+                    float pr[16];
 #pragma unroll
-                    for (int j = 0; j < 16; j++) b[j] = qrow_bits_mix(h[j], inv);
-                    qv.x = pack_low_bytes(b[0], b[1], b[2], b[3]);
-                    qv.y = pack_low_bytes(b[4], b[5], b[6], b[7]);
-                    qv.z = pack_low_bytes(b[8], b[9], b[10], b[11]);
-                    qv.w = pack_low_bytes(b[12], b[13], b[14], b[15]);
+                    for (int j = 0; j < 16; j++) pr[j] = fma_mix_lo(h[j], inv);
+                    qv = pack16_rint_sdwa(pr);
                 }
                 *reinterpret_cast<uint4*>(At + lane * a.pitch + 16 * ch) = qv;
             }
