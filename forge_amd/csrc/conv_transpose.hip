@@ -210,11 +210,12 @@ __global__ __launch_bounds__(128, convt_min_waves<KC>()) void convt_fused_kernel
         v4i fb[KC];
 #pragma unroll
         for (int ks = 0; ks < KC; ks++) fb[ks] = cur.fb[ks];
-        float wsv[4], bv[4];
+        float wsv[4];
+        uint32_t bbits[4];
 #pragma unroll
         for (int g = 0; g < 4; g++) {
             wsv[g] = h2f(cur.ws[g]);
-            bv[g] = h2f(cur.b[g]);
+            bbits[g] = cur.b[g];
         }
         if (it + kNW < items) load_item(it + kNW, cur);
         v16i acc;
@@ -235,16 +236,26 @@ __global__ __launch_bounds__(128, convt_min_waves<KC>()) void convt_fused_kernel
             for (int g = 0; g < 4; g++) {
                 const int co = 8 * j + 2 * g + hi;     // columns 4co .. 4co + 3
                 if (co >= C_out) continue;
-                uint32_t hv[4];
+                // dequant_gemm without a bias, (kw 0, 1) pairs rounded to fp16 by one
+                // v_cvt_pk_f16_f32 (round to nearest even, kw 0 in the low half), then the bias by
+                // one v_pk_add_f16: an fp16 sum rounded once equals the sum taken in fp32 and
+                // rounded to fp16 (when fp32 cannot hold the exact sum, the smaller term is below
+                // a quarter of the larger's fp16 ulp, and both round to the larger)
+                const float sc = as * wsv[g];
+                float pq[4];
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    uint16_t r = dequant_gemm(acc[4 * g + q], as, wsv[g], 0.0f, false);
-                    if (has_bias) r = f2h(h2f(r) + bv[g]);
-                    hv[q] = r;
+                for (int q = 0; q < 4; q++) pq[q] = static_cast<float>(acc[4 * g + q]) * sc;
+                uint32_t h01, h23;
+                asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(h01) : "v"(pq[0]), "v"(pq[1]));
+                asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(h23) : "v"(pq[2]), "v"(pq[3]));
+                if (has_bias) {
+                    const uint32_t b2 = bbits[g] | (bbits[g] << 16);
+                    asm("v_pk_add_f16 %0, %1, %2" : "=v"(h01) : "v"(h01), "v"(b2));
+                    asm("v_pk_add_f16 %0, %1, %2" : "=v"(h23) : "v"(h23), "v"(b2));
                 }
                 const uint32_t off = pix_b + static_cast<uint32_t>(co) * plane_b;
-                __builtin_amdgcn_raw_buffer_store_b32(hv[0] | (hv[1] << 16), yr, off, 0, 0);          // kh = 0
-                __builtin_amdgcn_raw_buffer_store_b32(hv[2] | (hv[3] << 16), yr, off + row_b, 0, 0);  // kh = 1
+                __builtin_amdgcn_raw_buffer_store_b32(h01, yr, off, 0, 0);          // kh = 0
+                __builtin_amdgcn_raw_buffer_store_b32(h23, yr, off + row_b, 0, 0);  // kh = 1
             }
         }
     }
