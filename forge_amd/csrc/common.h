@@ -239,6 +239,22 @@ __device__ __forceinline__ uint16_t dequant_gemm(int acc, float as, float ws, fl
     return f2h(has_bias ? __builtin_fmaf(a, s, b) : a * s);
 }
 
+// dequant_gemm of 4 consecutive columns of one row as their 8 bytes of fp16:
+// fma((float)acc, as * ws, b), where the caller passes b = -0 without a bias (fma(a, s, -0) is
+// a * s rounded once, zeros' signs included, so one form serves both), rounded in column pairs
+// by v_cvt_pk_f16_f32 (round to nearest even, the first column in the low half).
+__device__ __forceinline__ uint2 dequant4_pk(int a0, int a1, int a2, int a3, float as, const float (&ws)[4],
+                                             const float (&b)[4]) {
+    const float p0 = __builtin_fmaf(static_cast<float>(a0), as * ws[0], b[0]);
+    const float p1 = __builtin_fmaf(static_cast<float>(a1), as * ws[1], b[1]);
+    const float p2 = __builtin_fmaf(static_cast<float>(a2), as * ws[2], b[2]);
+    const float p3 = __builtin_fmaf(static_cast<float>(a3), as * ws[3], b[3]);
+    uint32_t h01, h23;
+    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(h01) : "v"(p0), "v"(p1));
+    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(h23) : "v"(p2), "v"(p3));
+    return make_uint2(h01, h23);
+}
+
 // n / d for 0 <= n with n * d < 2^32, with m = ceil(2^32 / d) (m = 0 stands for d = 1): n m / 2^32
 // exceeds n / d by n (m d - 2^32) / (d 2^32) < 1 / d, which cannot carry it past the next integer.
 __device__ __forceinline__ int udiv_magic(int n, uint32_t m) {

@@ -915,17 +915,14 @@ __device__ __forceinline__ void sp_store_tile(const v4i (&acc)[BNW / 32][BMT / 3
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 ws[t] = h2f(static_cast<uint16_t>(wr[t]));
-                b[t] = h2f(static_cast<uint16_t>(br[t]));
+                b[t] = has_bias ? h2f(static_cast<uint16_t>(br[t])) : -0.0f;   // dequant4_pk: -0 without a bias
             }
             const int u = 2 * i + (q >> 1), half = q & 1;
 #pragma unroll
             for (int j = 0; j < kTM; j++) {
                 const int r = 16 * j + r16;
-                uint16_t h[4];
-#pragma unroll
-                for (int t = 0; t < 4; t++) h[t] = dequant_gemm(acc[i][j][t], as[j], ws[t], b[t], has_bias);
                 *reinterpret_cast<uint2*>(stage + r * kRowBytes + ((u ^ (r & (kU - 1))) << 4) + 8 * half) =
-                    make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+                    dequant4_pk(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3], as[j], ws, b);
             }
         }
         flush_rows<kU, 2, true, false, BMT / 2>(stage, ep, wm, wn);
@@ -1476,7 +1473,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int nvec = K / 8;
     for (int n = t; n < N; n += 512) {
         sws[n] = w_scale[n];
-        sbias[n] = has_bias ? bias[n] : static_cast<uint16_t>(0);
+        sbias[n] = has_bias ? bias[n] : static_cast<uint16_t>(0x8000);   // -0: dequant4_pk without a bias
     }
 
     // Producer: rows pw*BT/4 .. +BT/4 of `tile` into buffer `buf`, kFqRowsInFlight rows per
@@ -1657,12 +1654,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
                     for (int j = 0; j < kTB; j++) {
                         const float as = sc[16 * j + r16];
-                        uint16_t h[4];
-#pragma unroll
-                        for (int e = 0; e < 4; e++) h[e] = dequant_gemm(acc[i][j][e], as, ws[e], bv[e], has_bias);
                         *reinterpret_cast<uint2*>(sw + (16 * j + r16) * kStgPitch + 16 * i + 4 * g) =
-                            make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16),
-                                       h[2] | (static_cast<uint32_t>(h[3]) << 16));
+                            dequant4_pk(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3], as, ws, bv);
                     }
                 }
                 // The strip is this wave's own and a wave's LDS accesses complete in order, so
@@ -1692,11 +1685,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     const int m = m0 + 16 * j + r16;
                     if (m >= M) continue;
                     const float as = sc[16 * j + r16];
-                    uint16_t h[4];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) h[e] = dequant_gemm(acc[i][j][e], as, ws[e], bv[e], has_bias);
                     *reinterpret_cast<uint2*>(out + static_cast<size_t>(m) * N + n) =
-                        make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+                        dequant4_pk(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3], as, ws, bv);
                 }
             }
         }

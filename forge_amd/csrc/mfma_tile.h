@@ -773,23 +773,20 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[BN / 64][BM / 64], 
                 const uint2 b2 = *reinterpret_cast<const uint2*>(bl + nl);
                 const uint32_t wr[4] = {w2.x & 0xFFFFu, w2.x >> 16, w2.y & 0xFFFFu, w2.y >> 16};
                 const uint32_t br[4] = {b2.x & 0xFFFFu, b2.x >> 16, b2.y & 0xFFFFu, b2.y >> 16};
+                // dequant4_pk: b = -0 without a bias
                 float ws[4], b[4];
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
                     ws[t] = h2f(static_cast<uint16_t>(wr[t]));
-                    b[t] = h2f(static_cast<uint16_t>(br[t]));
+                    b[t] = has_bias ? h2f(static_cast<uint16_t>(br[t])) : -0.0f;
                 }
                 const int u = nl / kPer;                   // unit of 8 columns; half = hi
 #pragma unroll
                 for (int i = 0; i < kTM; i++) {
                     const int r = 32 * i + l31;
-                    uint16_t h[4];
-#pragma unroll
-                    for (int t = 0; t < 4; t++)
-                        h[t] = dequant_gemm(acc[j][i][4 * g + t], as[i], ws[t], b[t], has_bias);
                     *reinterpret_cast<uint2*>(stage + r * kRowBytes + ((u ^ (r & (kU - 1))) << 4) + 8 * hi) =
-                        make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16),
-                                   h[2] | (static_cast<uint32_t>(h[3]) << 16));
+                        dequant4_pk(acc[j][i][4 * g], acc[j][i][4 * g + 1], acc[j][i][4 * g + 2], acc[j][i][4 * g + 3],
+                                    as[i], ws, b);
                 }
             }
         }
