@@ -211,14 +211,14 @@ __global__ __launch_bounds__(WN * WM * kWave) void sparse_gemm_kernel(SparseArgs
 #pragma unroll
                 for (int e = 0; e < 4; e++) atomicAdd(p.out32 + o + e, acc[i][j][e]);
             } else if (p.out16) {
-                uint16_t h[4];
+                float ws4[4], b4[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const float b = p.bias ? h2f(p.bias[n + e]) : 0.0f;
-                    h[e] = dequant_gemm(acc[i][j][e], as, h2f(p.w_scale[n + e]), b, p.bias != nullptr);
+                    ws4[e] = h2f(p.w_scale[n + e]);
+                    b4[e] = p.bias ? h2f(p.bias[n + e]) : -0.0f;   // dequant4_pk: -0 without a bias
                 }
                 *reinterpret_cast<uint2*>(p.out16 + o) =
-                    make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+                    dequant4_pk(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3], as, ws4, b4);
             } else {
                 *reinterpret_cast<int4*>(p.out32 + o) = make_int4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
             }
@@ -1129,14 +1129,14 @@ __global__ __launch_bounds__(256) void sparse_ring_kernel(const int8_t* __restri
             if (n >= N) continue;
             const size_t o = static_cast<size_t>(m) * N + n;
             if constexpr (DEQUANT) {
-                uint16_t h[4];
+                float ws4[4], b4[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const float bv = ep.bias ? h2f(ep.bias[n + e]) : 0.0f;
-                    h[e] = dequant_gemm(t.acc[i][j][e], as, h2f(ep.w_scale[n + e]), bv, ep.bias != nullptr);
+                    ws4[e] = h2f(ep.w_scale[n + e]);
+                    b4[e] = ep.bias ? h2f(ep.bias[n + e]) : -0.0f;   // dequant4_pk: -0 without a bias
                 }
                 *reinterpret_cast<uint2*>(ep.c16 + o) =
-                    make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+                    dequant4_pk(t.acc[i][j][0], t.acc[i][j][1], t.acc[i][j][2], t.acc[i][j][3], as, ws4, b4);
             } else {
                 *reinterpret_cast<int4*>(ep.c32 + o) =
                     make_int4(t.acc[i][j][0], t.acc[i][j][1], t.acc[i][j][2], t.acc[i][j][3]);
