@@ -44,6 +44,7 @@ SOURCES = [
     "gemm_sparse.hip",
     "gemm_sparse_wide.hip",
     "conv.hip",
+    "conv_window.hip",
     "conv_transpose.hip",
     "conv_depthwise.hip",
     "noalloc.hip",

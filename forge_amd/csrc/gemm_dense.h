@@ -89,6 +89,10 @@ bool sparse_wide_plan(int M, int N, int K, int cu, SpWidePlan* out);
 int launch_sparse_wide_s32(const int8_t* W_comp, const int8_t* x, const uint32_t* meta, int32_t* C, int M, int K,
                            int N, const SpWidePlan& p, hipStream_t s);
 
+// NHWC conv, stride 1, C % 128 == 0, Co % 256 == 0, on the window-fed tile (conv_window.hip):
+// returns -1 when the shape is not one it takes.
+int launch_conv_window(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep, int Co, hipStream_t s);
+
 // Implicit-GEMM NHWC conv through the dense tile engine (conv.hip supplies the geometry).
 int launch_conv_gemm(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep, int Co, bool vec,
                      hipStream_t s);

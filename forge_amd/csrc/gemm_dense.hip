@@ -311,6 +311,10 @@ int launch_conv_gemm(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep,
                      hipStream_t s)
 {
     const int M = g.rows, K = g.K;
+    if (vec) {
+        const int r = launch_conv_window(g, w, ep, Co, s);
+        if (r != -1) return r;
+    }
     // DMA engine when every 128-deep stage of a patch row is one pixel's contiguous channels
     // (and the image fits one buffer resource, the taps one 32-bit mask).
     const long long img_bytes = static_cast<long long>(g.rows / (g.Ho * g.Wo)) * g.H * g.W * g.C;

@@ -65,6 +65,52 @@ def test_conv_dma_gather(dev, orc, N, H, W, C, Co, k, pad, stride, dil, check):
         assert np.array_equal(out[n:n + 1], ref)
 
 
+# Stride-1 convs with C % 128 == 0 whose tiles are whole output rows: the window-fed tile (input
+# window in LDS once per 128-channel chunk, every tap's fragment read at its shift), 448 / 512
+# pixels x 128 channels or 224 / 256 x 256. Padding on every side, no padding, 5x5, dilation
+# along W, 1-3 channel chunks, several column tiles; INT32 and FP16 (with and without bias)
+# against the oracle.
+@pytest.mark.parametrize("N,H,W,C,Co,k,pad,dil,route", [
+    (2, 56, 56, 128, 256, 3, 1, (1, 1), "conv-window448x128"),
+    (2, 32, 14, 256, 256, 3, 1, (1, 1), "conv-window448x128"),
+    (1, 16, 28, 128, 512, 5, 2, (1, 1), "conv-window448x128"),
+    (2, 34, 30, 384, 256, 3, 0, (1, 1), "conv-window448x128"),
+    (1, 16, 34, 128, 256, 3, 1, (1, 2), "conv-window256x256"),    # 512-pixel window too large
+    (2, 16, 32, 256, 256, 3, 1, (1, 1), "conv-window512x128"),
+    (2, 17, 33, 128, 256, 2, 0, (1, 1), "conv-window512x128"),   # odd tap reach: padded window rows
+    (1, 4, 56, 128, 256, 3, 1, (1, 1), "conv-window224x256"),     # Ho = 4: one 224-pixel row group
+])
+def test_conv_window(dev, orc, N, H, W, C, Co, k, pad, dil, route):
+    import torch
+    from forge_amd import ops
+    rng = np.random.default_rng(H * W + C + Co + k)
+    x = int8_uniform(rng, (N, H, W, C))
+    w = int8_uniform(rng, (Co, k, k, C))
+    ref = orc.conv2d_nhwc_s32(x, w, (pad, pad), (1, 1), dil, threads=orc.cpu_threads())
+    say(f"conv window N={N} H={H} W={W} C={C} Co={Co} k={k} p={pad} d={dil}")
+    xd, wd = to_dev(x, dev), to_dev(w, dev)
+    o32 = torch.empty(ref.shape, dtype=torch.int32, device=dev)
+    poison(o32, 0x7B)
+    out = to_host(ops.int8_conv2d_nhwc_s32(xd, wd, (pad, pad), (1, 1), dil, out=o32))
+    assert ops.last_route() == route, ops.last_route()
+    bad = int((out != ref).sum())
+    assert bad == 0, f"{bad} of {out.size} INT32 outputs differ"
+    M = ref.size // Co
+    act = rng.uniform(0.01, 0.03, M).astype(np.float32)
+    ws = rng.uniform(1e-3, 1e-2, Co).astype(np.float16)
+    b = (rng.standard_normal(Co) * 0.1).astype(np.float16)
+    for bias in (b, None):
+        o16 = torch.empty(ref.shape, dtype=torch.float16, device=dev)
+        poison(o16, 0x7B)
+        y = to_host(ops.int8_conv2d_nhwc_dequant(xd, wd, to_dev(act, dev), to_dev(ws, dev),
+                                                 None if bias is None else to_dev(bias, dev), (pad, pad), (1, 1),
+                                                 dil, out=o16))
+        assert ops.last_route() == route, ops.last_route()
+        refy = orc.dequant_epilogue(ref.reshape(-1, Co), act, ws, bias)
+        bad = int((y.reshape(-1, Co).view(np.uint16) != refy.view(np.uint16)).sum())
+        assert bad == 0, f"{bad} of {y.size} FP16 outputs differ (bias={bias is not None})"
+
+
 def test_config5_full_size(dev, orc):
     """NHWC (32,56,56,256) x (256,3,3,256), stride 1, pad 1; every INT32 output of
     all 32 images bit-exact against the oracle's direct convolution (threaded), and every FP16
@@ -80,6 +126,7 @@ def test_config5_full_size(dev, orc):
     o32 = torch.empty((32, 56, 56, 256), dtype=torch.int32, device=dev)
     poison(o32, 0x7B)
     out = to_host(ops.int8_conv2d_nhwc_s32(xd, wd, (1, 1), out=o32))
+    assert ops.last_route() == "conv-window448x128", ops.last_route()
     bad = int((out != ref).sum())
     assert bad == 0, f"{bad} of {out.size} INT32 outputs differ"
     M = 32 * 56 * 56
