@@ -7,8 +7,9 @@
 // channels: the input window those rows touch (R + (kH-1) dilH rows x Wo + (kW-1) dilW columns,
 // zeros where it leaves the image) is loaded into LDS once per 128-channel chunk, and every tap's
 // A fragment is read from it at the tap's pixel shift. Only the weights stream per tap
-// (256 rows x 128 bytes a stage, the dense engine's 2-slot ring). For configs[4] (56 x 56 x 256
-// -> 256, 3x3): 224-pixel tiles move 89 KB of window + 576 KB of weights instead of 2 x 590 KB.
+// (256 rows x 128 bytes a stage: the dense engine's 2-slot ring with a double-buffered window,
+// or, where two windows do not fit, a 3-slot ring with one). For configs[4] (56 x 56 x 256 ->
+// 256, 3x3): 224-pixel tiles move 89 KB of window + 576 KB of weights instead of 2 x 590 KB.
 //
 // Integer sums do not depend on the order of K, so the INT32 result equals the reference's
 // im2col GEMM (src/nn/int8_conv2d.cu:151-223) on the same integers, and the FP16 epilogue is
@@ -21,8 +22,7 @@ namespace forge_amd {
 
 namespace {
 
-constexpr int kWinMaxQ = 20;          // window DMA instructions per wave (<= 640 pixels)
-constexpr int kWinSlots = 3;          // weight ring: 3 slots of BN rows x 128 bytes
+constexpr int kWinMaxQ = 16;          // window DMA instructions per wave (<= 512 pixels)
 constexpr int kWinLds = 160 * 1024;   // LDS per workgroup
 
 struct ConvWinArgs {
@@ -32,9 +32,14 @@ struct ConvWinArgs {
     uint32_t x_bytes;
     int H, W, C, K, kW, T;    // T = kH kW taps
     int padH, padW, dilH, dilW;
-    int Wo, R, WC, nwin;      // R output rows per tile, window columns WC, window pixels nwin
+    int Ho, Wo, WC, nwin;     // window columns WC (row stride), window pixels nwin
     int nc, nqw, win_bytes;   // 128-channel chunks, window DMA instructions per wave, bytes per window
-    int tiles_h, tiles_m, tiles_n;
+    // Row groups: each image's Ho rows are gpi groups of RG rows; a group is one tile of R rows
+    // (32 NI1 pixels), or, paired, a tile of R rows and one of R2 rows (at most 32 NI2 pixels,
+    // the rest of its row blocks masked). Workgroups [0, n1) run the first tiles of the groups,
+    // [n1, 2 n1) the second ones.
+    int R, R2, RG, gpi, n1;
+    int tiles_m, tiles_n;     // groups, 256-channel column tiles
 };
 
 // s_waitcnt vmcnt(N) lgkmcnt(0) (expcnt unconstrained; gfx9 splits the 6-bit vmcnt over bits
@@ -63,34 +68,33 @@ struct StagePos {
 
 }  // namespace
 
-// One tile per workgroup (4 waves) of WM x 32 NI pixels (R whole output rows) x BN = 256 / WM
-// output channels: wave w owns pixels [32 NI wm, +32 NI) and channels [64 wn, +64) of the tile
-// (wm = w / WN, wn = w % WN, WN = 4 / WM), 2 x NI accumulator blocks of
-// v_mfma_i32_32x32x32_i8. WM = 2 halves the weight bytes per pixel (the weights stream once per
-// tile) for a window twice as tall.
-template <int NI, int WM, bool DEQUANT>
-__global__ __launch_bounds__(kGemmThreads) void conv_window_kernel(ConvWinArgs a)
+// One tile (4 waves) of `rows` output rows from row ho0 of image img (32 NI pixels, those past
+// rows * Wo masked) x 256 output channels from n0: wave w owns channels [64 w, +64) of all the
+// tile's pixels, 2 x NI accumulator blocks of v_mfma_i32_32x32x32_i8.
+template <int NI, int SLOTS, bool DEQUANT>
+__device__ __forceinline__ void conv_window_tile(const ConvWinArgs& a, int8_t* lds, int img, int ho0, int n0,
+                                                 int rows)
 {
-    extern __shared__ __align__(16) int8_t lds[];
-    constexpr int WN = 4 / WM;
-    constexpr int kBN = 64 * WN;               // tile channels
-    constexpr int kWP = 32 * NI;               // pixels per wave
-    constexpr int kTW = kWP * WM;              // tile pixels
+    constexpr int kBN = 256;                   // tile channels
     constexpr int kSlot = kBN * kBK;           // weight ring slot bytes
     constexpr int kBI = kBN / 32;              // weight DMA instructions per wave per stage
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    const int wm = wave / WN, wn = wave % WN;
     const int l31 = lane & 31, hi = lane >> 5;
-    int tm, tn;
-    tile_coords(blockIdx.x, a.tiles_m, a.tiles_n, tm, tn);
-    const int img = tm / a.tiles_h, th = tm - img * a.tiles_h;
-    const int m0 = tm * kTW;                  // tiles are whole rows: pixel index of the tile
-    const int n0 = tn * kBN;
-    const int h0 = th * a.R - a.padH;          // input row of window row 0
+    const int m0 = (img * a.Ho + ho0) * a.Wo;  // pixel index of the tile's first pixel
+    const int h0 = ho0 - a.padH;               // input row of window row 0
+    const int mlast = min(a.ep.M, m0 + rows * a.Wo) - 1;   // the tile's last stored pixel
+
+    // FP16 out: the rows' activation scales are loaded first, so that no load waits behind the
+    // epilogue's stores (vector-memory operations complete in issue order).
+    [[maybe_unused]] float asv[NI];
+    if constexpr (DEQUANT) {
+#pragma unroll
+        for (int i = 0; i < NI; i++) asv[i] = a.ep.act_scale[min(m0 + 32 * i + l31, mlast)];
+    }
 
     int8_t* ring = lds;
-    int8_t* win = lds + kWinSlots * kSlot;
+    int8_t* win = lds + SLOTS * kSlot;
 
     // Weight DMA lanes: instruction q of this wave fills ring chunks s = (kBI wave + q) 64 + lane,
     // row s / 8, physical chunk s % 8 = logical chunk (s % 8) ^ swz(row).
@@ -119,11 +123,11 @@ __global__ __launch_bounds__(kGemmThreads) void conv_window_kernel(ConvWinArgs a
         const bool ok = q < a.nqw && wp < a.nwin && hin >= 0 && hin < a.H && win_c >= 0 && win_c < a.W;
         vo[q] = ok ? static_cast<uint32_t>(((img * a.H + hin) * a.W + win_c) * a.C + 16 * cj) : 0x80000000u;
     }
-    // Window pixel of tile pixel p = 32 NI wm + 32 i + l31 at tap (0, 0).
+    // Window pixel of tile pixel p = 32 i + l31 at tap (0, 0).
     int wp0[NI];
 #pragma unroll
     for (int i = 0; i < NI; i++) {
-        const int p = kWP * wm + 32 * i + l31;
+        const int p = 32 * i + l31;
         const int r = p / a.Wo;
         wp0[i] = r * a.WC + (p - r * a.Wo);
     }
@@ -133,15 +137,18 @@ __global__ __launch_bounds__(kGemmThreads) void conv_window_kernel(ConvWinArgs a
     const int nst = a.nc * a.T;
 
     auto issue_w = [&](int st, const StagePos& P) {
-        int8_t* slot = ring + (st % kWinSlots) * kSlot;
+        int8_t* slot = ring + (st % SLOTS) * kSlot;
         const uint32_t soff = static_cast<uint32_t>(P.tap * a.C + P.ch * kBK);
 #pragma unroll
         for (int q = 0; q < kBI; q++) dma16_buf(wres, lb[q], soff, slot + (wave * kBI + q) * 1024);
     };
+    // With 2 ring slots the window is double-buffered by chunk parity; with 3, single.
+    auto win_buf = [&](int ch) { return win + (SLOTS == 2 ? (ch & 1) * a.win_bytes : 0); };
     auto issue_win = [&](int ch) {
+        int8_t* buf = win_buf(ch);
 #pragma unroll
         for (int q = 0; q < kWinMaxQ; q++)
-            if (q < a.nqw) dma16_buf(xres, vo[q] + static_cast<uint32_t>(ch * kBK), 0, win + (wave * a.nqw + q) * 1024);
+            if (q < a.nqw) dma16_buf(xres, vo[q] + static_cast<uint32_t>(ch * kBK), 0, buf + (wave * a.nqw + q) * 1024);
     };
 
     struct Frags {
@@ -157,19 +164,19 @@ __global__ __launch_bounds__(kGemmThreads) void conv_window_kernel(ConvWinArgs a
             for (int e = 0; e < 16; e++) acc[j][i][e] = 0;
 
     auto load_frags = [&](int st, const StagePos& P, int ks, Frags& F) {
-        const int8_t* wb = win;
-        const int8_t* bs = ring + (st % kWinSlots) * kSlot;
+        const int8_t* wb = win_buf(P.ch);
+        const int8_t* bs = ring + (st % SLOTS) * kSlot;
         const int tp = P.kh * a.dilH * a.WC + P.kw * a.dilW;       // window pixel shift
         const int tv = P.kh * a.dilH * a.Wo + P.kw * a.dilW;       // its v shift
         const int c = 2 * ks + hi;
 #pragma unroll
         for (int i = 0; i < NI; i++) {
-            const int sw = ((kWP * wm + 32 * i + l31 + tv) >> 1) & 7;
+            const int sw = ((32 * i + l31 + tv) >> 1) & 7;
             F.a[i] = *reinterpret_cast<const v4i*>(wb + ((wp0[i] + tp) << 7) + ((c ^ sw) << 4));
         }
 #pragma unroll
         for (int j = 0; j < 2; j++)
-            F.b[j] = *reinterpret_cast<const v4i*>(bs + lds_off128(64 * wn + 32 * j + l31, c));
+            F.b[j] = *reinterpret_cast<const v4i*>(bs + lds_off128(64 * wave + 32 * j + l31, c));
     };
     auto mfmas = [&](const Frags& F) {
 #pragma unroll
@@ -179,13 +186,16 @@ __global__ __launch_bounds__(kGemmThreads) void conv_window_kernel(ConvWinArgs a
                 acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(F.b[j], F.a[i], acc[j][i], 0, 0, 0);
     };
 
-    // Fragments are read two sub-steps ahead of their MFMAs, as in the dense engine, but the
-    // weight ring has 3 slots: the DMA of stage kt+3 goes out after the barrier of stage kt
-    // (into stage kt's slot), so each stage's weights have two stages of lead and the wait
-    // before a barrier leaves the kBI DMAs of the next stage in flight (vector-memory loads
-    // return in issue order). The window has one buffer: at a chunk's first stage the next
-    // chunk's window is loaded after the barrier that ends the last reads of the current one,
-    // and the workgroup waits for it.
+    // Fragments are read two sub-steps ahead of their MFMAs, as in the dense engine.
+    // SLOTS = 2: the dense engine's ring (the weight DMA of stage kt+2 after the barrier of stage
+    // kt, into its slot), and the window of chunk ch+1 is issued at the first stage of chunk ch
+    // into the other window buffer (which last served chunk ch-1, whose reads ended before this
+    // barrier); it has landed by the barrier that publishes chunk ch+1's first stage (T >= 2).
+    // SLOTS = 3: the DMA of stage kt+3 goes out after the barrier of stage kt (into stage kt's
+    // slot), so each stage's weights have two stages of lead, and the wait before a barrier
+    // leaves the kBI DMAs of the next stage in flight (vector-memory loads return in issue
+    // order); the one window buffer is reloaded after the barrier that ends the last reads of a
+    // chunk, and the workgroup waits for it.
     constexpr int kMf = 2 * NI, kRd = NI + 2, kVm = kBI / 2;
     Frags F0, F1, F2, F3;
     StagePos P0{0, 0, 0, 0};                   // stage kt
@@ -198,8 +208,12 @@ __global__ __launch_bounds__(kGemmThreads) void conv_window_kernel(ConvWinArgs a
     issue_win(0);
     issue_w(0, P0);
     issue_w(1, P1);
-    issue_w(2, P2);
-    wait_vm_lgkm<2 * kBI>();                   // window and stage 0
+    if constexpr (SLOTS == 3) {
+        issue_w(2, P2);
+        wait_vm_lgkm<2 * kBI>();               // window and stage 0
+    } else {
+        wait_vm_lgkm<kBI>();
+    }
     lds_barrier();
     load_frags(0, P0, 0, F0);
     load_frags(0, P0, 1, F1);
@@ -210,14 +224,21 @@ __global__ __launch_bounds__(kGemmThreads) void conv_window_kernel(ConvWinArgs a
         load_frags(kt, P0, 3, F3);
         mfmas(F1);
         sched_interleave<kMf, kRd, 0>();
-        wait_vm_lgkm<kBI>();                   // stage kt+1 landed; stage kt+2 may be in flight
-        lds_barrier();
-        if (P1.tap == 0) {                     // stage kt+1 opens chunk P1.ch
-            issue_win(P1.ch);
-            wait_vm_lgkm<0>();
+        if constexpr (SLOTS == 3) {
+            wait_vm_lgkm<kBI>();               // stage kt+1 landed; stage kt+2 may be in flight
             lds_barrier();
+            if (P1.tap == 0) {                 // stage kt+1 opens chunk P1.ch
+                issue_win(P1.ch);
+                wait_vm_lgkm<0>();
+                lds_barrier();
+            }
+            issue_w(kt + 3, P3);               // into stage kt's slot; past the end: unused re-reads
+        } else {
+            wait_vm_lgkm<0>();                 // stage kt+1 (and a window issued one stage ago)
+            lds_barrier();
+            if (P0.tap == 0 && P0.ch + 1 < a.nc) issue_win(P0.ch + 1);
+            issue_w(kt + 2, P2);               // into stage kt's slot; past the end: unused re-reads
         }
-        issue_w(kt + 3, P3);                   // into stage kt's slot; past the end: unused re-reads
         load_frags(kt + 1, P1, 0, F0);
         mfmas(F2);
         load_frags(kt + 1, P1, 1, F1);
@@ -240,9 +261,10 @@ __global__ __launch_bounds__(kGemmThreads) void conv_window_kernel(ConvWinArgs a
 
     // Epilogue: per 32-pixel block, the wave's 32 x 64 outputs go through a wave-private LDS
     // strip (16-byte units XOR-swizzled by row) and out as coalesced 16-byte row stores.
-    const GemmEpilogue& ep = a.ep;
-    const int rm = m0 + kWP * wm;              // the wave's first pixel
-    const int cn = n0 + 64 * wn;               // the wave's first channel
+    GemmEpilogue ep = a.ep;
+    ep.M = mlast + 1;                          // masked pixels are not stored
+    const int rm = m0;                         // the wave's first pixel
+    const int cn = n0 + 64 * wave;             // the wave's first channel
     if constexpr (DEQUANT) {
         constexpr int kU = 8;                  // 64 FP16 columns = 8 units of 16 bytes
         int8_t* strip = lds + wave * (32 * kU * 16);
@@ -253,7 +275,7 @@ __global__ __launch_bounds__(kGemmThreads) void conv_window_kernel(ConvWinArgs a
         bl[lane] = has_bias ? ep.bias[cn + lane] : static_cast<uint16_t>(0);
 #pragma unroll
         for (int i = 0; i < NI; i++) {
-            const float as = ep.act_scale[rm + 32 * i + l31];
+            const float as = asv[i];
 #pragma unroll
             for (int j = 0; j < 2; j++)
 #pragma unroll
@@ -294,88 +316,139 @@ __global__ __launch_bounds__(kGemmThreads) void conv_window_kernel(ConvWinArgs a
     }
 }
 
+// Workgroups [0, n1) take the first tile of group tm (XCD-aware order), [n1, 2 n1) the paired
+// second tile (NI2 > 0): tile t of both halves is the same group, on the same XCD.
+template <int NI1, int NI2, int SLOTS, bool DEQUANT>
+__global__ __launch_bounds__(kGemmThreads) void conv_window_kernel(ConvWinArgs a)
+{
+    extern __shared__ __align__(16) int8_t lds[];
+    const int bid = static_cast<int>(blockIdx.x);
+    const bool second = NI2 > 0 && bid >= a.n1;
+    int tm, tn;
+    tile_coords(second ? bid - a.n1 : bid, a.tiles_m, a.tiles_n, tm, tn);
+    const int img = tm / a.gpi, g = tm - img * a.gpi;
+    if constexpr (NI2 > 0) {
+        if (second) {
+            conv_window_tile<NI2, SLOTS, DEQUANT>(a, lds, img, g * a.RG + a.R, tn * 256, a.R2);
+            return;
+        }
+    }
+    conv_window_tile<NI1, SLOTS, DEQUANT>(a, lds, img, g * a.RG, tn * 256, a.R);
+}
+
 // The kernel's dynamic-LDS limit is raised once to the largest window (host-side attribute).
-template <int NI, int WM, bool DEQUANT>
+template <int NI1, int NI2, int SLOTS, bool DEQUANT>
 static int launch_win(const ConvWinArgs& a, unsigned grid, int lds, hipStream_t s)
 {
     static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(conv_window_kernel<NI, WM, DEQUANT>), hipFuncAttributeMaxDynamicSharedMemorySize,
-        kWinLds);
+        reinterpret_cast<const void*>(conv_window_kernel<NI1, NI2, SLOTS, DEQUANT>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, kWinLds);
     if (attr != hipSuccess) return static_cast<int>(attr);
-    conv_window_kernel<NI, WM, DEQUANT><<<grid, kGemmThreads, lds, s>>>(a);
+    conv_window_kernel<NI1, NI2, SLOTS, DEQUANT><<<grid, kGemmThreads, lds, s>>>(a);
     return launch_status();
 }
 
 // Returns -1 when the shape is not one the window kernel takes.
-int launch_conv_window(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep, int Co, hipStream_t s)
+int launch_conv_window(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep, int Co, int cu, hipStream_t s)
 {
     const int N = g.rows / (g.Ho * g.Wo);
     const int kH = g.K / (g.C * g.kW), T = kH * g.kW;
-    if (g.strideH != 1 || g.strideW != 1 || g.C % kBK != 0 || Co % 128 != 0 || T < 2 || g.r0 != 0 ||
-        !ep.vec_out || ep.up_w != 0 || !aligned(g.x, 16) || !aligned(w, 16))
+    if (g.strideH != 1 || g.strideW != 1 || g.C % kBK != 0 || Co % 256 != 0 || T < 2 || g.r0 != 0 ||
+        !ep.vec_out || ep.up_w != 0 || !aligned(g.x, 16) || !aligned(w, 16) || cu <= 0)
         return -1;
     const long long x_bytes = static_cast<long long>(N) * g.H * g.W * g.C;
     if (x_bytes >= (1LL << 31) || static_cast<long long>(Co) * g.K >= (1LL << 31)) return -1;
-    // Window row stride: the columns the taps reach, padded to keep WC - Wo even (the swizzle).
-    long long WC = g.Wo + static_cast<long long>(g.kW - 1) * g.dilW;
-    WC += (WC - g.Wo) & 1;
-    // A wave's pixels are Rw whole output rows with Rw Wo = 224 or 256 (7 or 8 row blocks); a
-    // tile is WM of them. WM = 2 (448 / 512 pixels x 128 channels) where its window fits, else
-    // WM = 1 (224 / 256 pixels x 256 channels).
-    for (int wm : {2, 1}) {
-        if (Co % (256 / wm) != 0) continue;
-        for (int ni : {8, 7}) {
-            if ((32 * ni) % g.Wo != 0) continue;
-            const int R = wm * (32 * ni / g.Wo);
-            if (g.Ho % R != 0) continue;
-            const long long WR = R + static_cast<long long>(kH - 1) * g.dilH;
-            const long long nwin = WR * WC;
-            const long long nqw = (nwin * 8 + 4 * kWave - 1) / (4 * kWave);
-            const long long lds = static_cast<long long>(kWinSlots) * (256 / wm) * kBK + nqw * 4 * 1024;
-            if (nqw > kWinMaxQ || lds > kWinLds) continue;
-            const long long tiles_m = static_cast<long long>(N) * (g.Ho / R);
-            const long long tiles = tiles_m * (Co / (256 / wm));
-            if (tiles > 0x7FFFFFFFLL) continue;
-
-            ConvWinArgs a;
-            a.x = g.x;
-            a.w = w;
-            a.ep = ep;
-            a.x_bytes = static_cast<uint32_t>(x_bytes);
-            a.H = g.H;
-            a.W = g.W;
-            a.C = g.C;
-            a.K = g.K;
-            a.kW = g.kW;
-            a.T = T;
-            a.padH = g.padH;
-            a.padW = g.padW;
-            a.dilH = g.dilH;
-            a.dilW = g.dilW;
-            a.Wo = g.Wo;
-            a.R = R;
-            a.WC = static_cast<int>(WC);
-            a.nwin = static_cast<int>(nwin);
-            a.nc = g.C / kBK;
-            a.nqw = static_cast<int>(nqw);
-            a.win_bytes = static_cast<int>(nqw) * 4 * 1024;
-            a.tiles_h = g.Ho / R;
-            a.tiles_m = static_cast<int>(tiles_m);
-            a.tiles_n = Co / (256 / wm);
-            const unsigned grid = static_cast<unsigned>(tiles);
-            const int l = static_cast<int>(lds);
-            const bool o16 = ep.c16 != nullptr;
-            if (wm == 2) {
-                note_route(ni == 8 ? "conv-window512x128" : "conv-window448x128");
-                if (ni == 8) return o16 ? launch_win<8, 2, true>(a, grid, l, s) : launch_win<8, 2, false>(a, grid, l, s);
-                return o16 ? launch_win<7, 2, true>(a, grid, l, s) : launch_win<7, 2, false>(a, grid, l, s);
-            }
-            note_route(ni == 8 ? "conv-window256x256" : "conv-window224x256");
-            if (ni == 8) return o16 ? launch_win<8, 1, true>(a, grid, l, s) : launch_win<8, 1, false>(a, grid, l, s);
-            return o16 ? launch_win<7, 1, true>(a, grid, l, s) : launch_win<7, 1, false>(a, grid, l, s);
+    // Tile height: R whole output rows with R Wo = 256 or 224 pixels (8 or 7 row blocks).
+    int NI = 0, R = 0;
+    for (int ni : {8, 7}) {
+        if ((32 * ni) % g.Wo == 0 && g.Ho % ((32 * ni) / g.Wo) == 0) {
+            NI = ni;
+            R = 32 * ni / g.Wo;
+            break;
         }
     }
-    return -1;
+    if (NI == 0) return -1;
+    const int tn = Co / 256;
+    // Pairing: when the R-row tiles take more than one wave of CUs, groups of R + R2 rows (a tile
+    // of R rows and one of R2 rows in NI - 1 row blocks) spread the rows more evenly: configs[4]
+    // (1792 rows of 56 pixels, 256 CUs) takes 7 + 6 row blocks per CU instead of 7 + 7 on the
+    // busiest CUs of 448 four-row tiles.
+    int R2 = 0;
+    {
+        const long long t1 = static_cast<long long>(N) * (g.Ho / R) * tn;
+        const long long plain = (t1 + cu - 1) / cu * NI;
+        for (int r2 = R - 1; r2 >= 1; r2--) {
+            if (g.Ho % (R + r2) != 0 || (32 * (NI - 1)) < r2 * g.Wo) continue;
+            const long long groups = static_cast<long long>(N) * (g.Ho / (R + r2)) * tn;
+            if (groups <= cu && 2 * NI - 1 < plain) {
+                R2 = r2;
+                break;
+            }
+        }
+    }
+    const int RG = R + R2;
+    // Window row stride: the columns the taps reach, padded to keep WC - Wo even (the swizzle).
+    // Rows: the R rows of a first tile (a second tile's masked pixels read rows within them).
+    long long WC = g.Wo + static_cast<long long>(g.kW - 1) * g.dilW;
+    WC += (WC - g.Wo) & 1;
+    const long long WR = R + static_cast<long long>(kH - 1) * g.dilH;
+    const long long nwin = WR * WC;
+    const long long nqw = (nwin * 8 + 4 * kWave - 1) / (4 * kWave);
+    // 2 ring slots + two window buffers where they fit (measured faster on configs[4]), else
+    // 3 slots + one window buffer.
+    const int slots = 2 * 256 * kBK + 2 * nqw * 4 * 1024 <= kWinLds ? 2 : 3;
+    const long long lds = static_cast<long long>(slots) * 256 * kBK + (4 - slots) * nqw * 4 * 1024;
+    if (nqw > kWinMaxQ || lds > kWinLds) return -1;
+    const long long tiles_m = static_cast<long long>(N) * (g.Ho / RG);
+    const long long n1 = tiles_m * tn;
+    if (2 * n1 > 0x7FFFFFFFLL) return -1;
+    if (R2 > 0 && slots != 2) R2 = 0;          // pairs are instantiated with the 2-slot ring only
+
+    ConvWinArgs a;
+    a.x = g.x;
+    a.w = w;
+    a.ep = ep;
+    a.x_bytes = static_cast<uint32_t>(x_bytes);
+    a.H = g.H;
+    a.W = g.W;
+    a.C = g.C;
+    a.K = g.K;
+    a.kW = g.kW;
+    a.T = T;
+    a.padH = g.padH;
+    a.padW = g.padW;
+    a.dilH = g.dilH;
+    a.dilW = g.dilW;
+    a.Ho = g.Ho;
+    a.Wo = g.Wo;
+    a.WC = static_cast<int>(WC);
+    a.nwin = static_cast<int>(nwin);
+    a.nc = g.C / kBK;
+    a.nqw = static_cast<int>(nqw);
+    a.win_bytes = static_cast<int>(nqw) * 4 * 1024;
+    a.R = R;
+    a.R2 = R2;
+    a.RG = R + R2;
+    a.gpi = g.Ho / (R + R2);
+    a.n1 = static_cast<int>(N * static_cast<long long>(g.Ho / (R + R2)) * tn);
+    a.tiles_m = N * (g.Ho / (R + R2));
+    a.tiles_n = tn;
+    const unsigned grid = static_cast<unsigned>(R2 > 0 ? 2 * a.n1 : a.n1);
+    const int l = static_cast<int>(lds);
+    const bool o16 = ep.c16 != nullptr;
+    if (R2 > 0) {
+        note_route(NI == 8 ? "conv-window256+224" : "conv-window224+192");
+        if (NI == 8) return o16 ? launch_win<8, 7, 2, true>(a, grid, l, s) : launch_win<8, 7, 2, false>(a, grid, l, s);
+        return o16 ? launch_win<7, 6, 2, true>(a, grid, l, s) : launch_win<7, 6, 2, false>(a, grid, l, s);
+    }
+    note_route(NI == 8 ? (slots == 2 ? "conv-window256" : "conv-window256 ring3")
+                       : (slots == 2 ? "conv-window224" : "conv-window224 ring3"));
+    if (slots == 2) {
+        if (NI == 8) return o16 ? launch_win<8, 0, 2, true>(a, grid, l, s) : launch_win<8, 0, 2, false>(a, grid, l, s);
+        return o16 ? launch_win<7, 0, 2, true>(a, grid, l, s) : launch_win<7, 0, 2, false>(a, grid, l, s);
+    }
+    if (NI == 8) return o16 ? launch_win<8, 0, 3, true>(a, grid, l, s) : launch_win<8, 0, 3, false>(a, grid, l, s);
+    return o16 ? launch_win<7, 0, 3, true>(a, grid, l, s) : launch_win<7, 0, 3, false>(a, grid, l, s);
 }
 
 }  // namespace forge_amd
