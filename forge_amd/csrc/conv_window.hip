@@ -34,12 +34,8 @@ struct ConvWinArgs {
     int padH, padW, dilH, dilW;
     int Ho, Wo, WC, nwin;     // window columns WC (row stride), window pixels nwin
     int nc, nqw, win_bytes;   // 128-channel chunks, window DMA instructions per wave, bytes per window
-    // Row groups: each image's Ho rows are gpi groups of RG rows; a group is one tile of R rows
-    // (32 NI1 pixels), or, paired, a tile of R rows and one of R2 rows (at most 32 NI2 pixels,
-    // the rest of its row blocks masked). Workgroups [0, n1) run the first tiles of the groups,
-    // [n1, 2 n1) the second ones.
-    int R, R2, RG, gpi, n1;
-    int tiles_m, tiles_n;     // groups, 256-channel column tiles
+    int R, tiles_h;           // output rows per tile (32 NI pixels), tiles per image
+    int tiles_m, tiles_n;     // row tiles, 256-channel column tiles
 };
 
 // s_waitcnt vmcnt(N) lgkmcnt(0) (expcnt unconstrained; gfx9 splits the 6-bit vmcnt over bits
@@ -68,13 +64,18 @@ struct StagePos {
 
 }  // namespace
 
-// One tile (4 waves) of `rows` output rows from row ho0 of image img (32 NI pixels, those past
-// rows * Wo masked) x 256 output channels from n0: wave w owns channels [64 w, +64) of all the
-// tile's pixels, 2 x NI accumulator blocks of v_mfma_i32_32x32x32_i8.
+// One tile per workgroup (4 waves) of R output rows from row ho0 of image img (32 NI pixels) x
+// 256 output channels from n0: wave w owns channels [64 w, +64) of all the tile's pixels,
+// 2 x NI accumulator blocks of v_mfma_i32_32x32x32_i8. Tiles map to workgroups XCD-aware.
 template <int NI, int SLOTS, bool DEQUANT>
-__device__ __forceinline__ void conv_window_tile(const ConvWinArgs& a, int8_t* lds, int img, int ho0, int n0,
-                                                 int rows)
+__global__ __launch_bounds__(kGemmThreads) void conv_window_kernel(ConvWinArgs a)
 {
+    extern __shared__ __align__(16) int8_t lds[];
+    int tm, tn;
+    tile_coords(static_cast<int>(blockIdx.x), a.tiles_m, a.tiles_n, tm, tn);
+    const int img = tm / a.tiles_h;
+    const int ho0 = (tm - img * a.tiles_h) * a.R;
+    const int n0 = tn * 256;
     constexpr int kBN = 256;                   // tile channels
     constexpr int kSlot = kBN * kBK;           // weight ring slot bytes
     constexpr int kBI = kBN / 32;              // weight DMA instructions per wave per stage
@@ -83,14 +84,13 @@ __device__ __forceinline__ void conv_window_tile(const ConvWinArgs& a, int8_t* l
     const int l31 = lane & 31, hi = lane >> 5;
     const int m0 = (img * a.Ho + ho0) * a.Wo;  // pixel index of the tile's first pixel
     const int h0 = ho0 - a.padH;               // input row of window row 0
-    const int mlast = min(a.ep.M, m0 + rows * a.Wo) - 1;   // the tile's last stored pixel
 
     // FP16 out: the rows' activation scales are loaded first, so that no load waits behind the
     // epilogue's stores (vector-memory operations complete in issue order).
     [[maybe_unused]] float asv[NI];
     if constexpr (DEQUANT) {
 #pragma unroll
-        for (int i = 0; i < NI; i++) asv[i] = a.ep.act_scale[min(m0 + 32 * i + l31, mlast)];
+        for (int i = 0; i < NI; i++) asv[i] = a.ep.act_scale[m0 + 32 * i + l31];
     }
 
     int8_t* ring = lds;
@@ -261,8 +261,7 @@ __device__ __forceinline__ void conv_window_tile(const ConvWinArgs& a, int8_t* l
 
     // Epilogue: per 32-pixel block, the wave's 32 x 64 outputs go through a wave-private LDS
     // strip (16-byte units XOR-swizzled by row) and out as coalesced 16-byte row stores.
-    GemmEpilogue ep = a.ep;
-    ep.M = mlast + 1;                          // masked pixels are not stored
+    const GemmEpilogue& ep = a.ep;
     const int rm = m0;                         // the wave's first pixel
     const int cn = n0 + 64 * wave;             // the wave's first channel
     if constexpr (DEQUANT) {
@@ -316,45 +315,25 @@ __device__ __forceinline__ void conv_window_tile(const ConvWinArgs& a, int8_t* l
     }
 }
 
-// Workgroups [0, n1) take the first tile of group tm (XCD-aware order), [n1, 2 n1) the paired
-// second tile (NI2 > 0): tile t of both halves is the same group, on the same XCD.
-template <int NI1, int NI2, int SLOTS, bool DEQUANT>
-__global__ __launch_bounds__(kGemmThreads) void conv_window_kernel(ConvWinArgs a)
-{
-    extern __shared__ __align__(16) int8_t lds[];
-    const int bid = static_cast<int>(blockIdx.x);
-    const bool second = NI2 > 0 && bid >= a.n1;
-    int tm, tn;
-    tile_coords(second ? bid - a.n1 : bid, a.tiles_m, a.tiles_n, tm, tn);
-    const int img = tm / a.gpi, g = tm - img * a.gpi;
-    if constexpr (NI2 > 0) {
-        if (second) {
-            conv_window_tile<NI2, SLOTS, DEQUANT>(a, lds, img, g * a.RG + a.R, tn * 256, a.R2);
-            return;
-        }
-    }
-    conv_window_tile<NI1, SLOTS, DEQUANT>(a, lds, img, g * a.RG, tn * 256, a.R);
-}
-
 // The kernel's dynamic-LDS limit is raised once to the largest window (host-side attribute).
-template <int NI1, int NI2, int SLOTS, bool DEQUANT>
+template <int NI, int SLOTS, bool DEQUANT>
 static int launch_win(const ConvWinArgs& a, unsigned grid, int lds, hipStream_t s)
 {
     static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(conv_window_kernel<NI1, NI2, SLOTS, DEQUANT>),
+        reinterpret_cast<const void*>(conv_window_kernel<NI, SLOTS, DEQUANT>),
         hipFuncAttributeMaxDynamicSharedMemorySize, kWinLds);
     if (attr != hipSuccess) return static_cast<int>(attr);
-    conv_window_kernel<NI1, NI2, SLOTS, DEQUANT><<<grid, kGemmThreads, lds, s>>>(a);
+    conv_window_kernel<NI, SLOTS, DEQUANT><<<grid, kGemmThreads, lds, s>>>(a);
     return launch_status();
 }
 
 // Returns -1 when the shape is not one the window kernel takes.
-int launch_conv_window(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep, int Co, int cu, hipStream_t s)
+int launch_conv_window(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep, int Co, hipStream_t s)
 {
     const int N = g.rows / (g.Ho * g.Wo);
     const int kH = g.K / (g.C * g.kW), T = kH * g.kW;
     if (g.strideH != 1 || g.strideW != 1 || g.C % kBK != 0 || Co % 256 != 0 || T < 2 || g.r0 != 0 ||
-        !ep.vec_out || ep.up_w != 0 || !aligned(g.x, 16) || !aligned(w, 16) || cu <= 0)
+        !ep.vec_out || ep.up_w != 0 || !aligned(g.x, 16) || !aligned(w, 16))
         return -1;
     const long long x_bytes = static_cast<long long>(N) * g.H * g.W * g.C;
     if (x_bytes >= (1LL << 31) || static_cast<long long>(Co) * g.K >= (1LL << 31)) return -1;
@@ -369,26 +348,7 @@ int launch_conv_window(const ConvGeom& g, const int8_t* w, const GemmEpilogue& e
     }
     if (NI == 0) return -1;
     const int tn = Co / 256;
-    // Pairing: when the R-row tiles take more than one wave of CUs, groups of R + R2 rows (a tile
-    // of R rows and one of R2 rows in NI - 1 row blocks) spread the rows more evenly: configs[4]
-    // (1792 rows of 56 pixels, 256 CUs) takes 7 + 6 row blocks per CU instead of 7 + 7 on the
-    // busiest CUs of 448 four-row tiles.
-    int R2 = 0;
-    {
-        const long long t1 = static_cast<long long>(N) * (g.Ho / R) * tn;
-        const long long plain = (t1 + cu - 1) / cu * NI;
-        for (int r2 = R - 1; r2 >= 1; r2--) {
-            if (g.Ho % (R + r2) != 0 || (32 * (NI - 1)) < r2 * g.Wo) continue;
-            const long long groups = static_cast<long long>(N) * (g.Ho / (R + r2)) * tn;
-            if (groups <= cu && 2 * NI - 1 < plain) {
-                R2 = r2;
-                break;
-            }
-        }
-    }
-    const int RG = R + R2;
     // Window row stride: the columns the taps reach, padded to keep WC - Wo even (the swizzle).
-    // Rows: the R rows of a first tile (a second tile's masked pixels read rows within them).
     long long WC = g.Wo + static_cast<long long>(g.kW - 1) * g.dilW;
     WC += (WC - g.Wo) & 1;
     const long long WR = R + static_cast<long long>(kH - 1) * g.dilH;
@@ -399,10 +359,8 @@ int launch_conv_window(const ConvGeom& g, const int8_t* w, const GemmEpilogue& e
     const int slots = 2 * 256 * kBK + 2 * nqw * 4 * 1024 <= kWinLds ? 2 : 3;
     const long long lds = static_cast<long long>(slots) * 256 * kBK + (4 - slots) * nqw * 4 * 1024;
     if (nqw > kWinMaxQ || lds > kWinLds) return -1;
-    const long long tiles_m = static_cast<long long>(N) * (g.Ho / RG);
-    const long long n1 = tiles_m * tn;
-    if (2 * n1 > 0x7FFFFFFFLL) return -1;
-    if (R2 > 0 && slots != 2) R2 = 0;          // pairs are instantiated with the 2-slot ring only
+    const long long tiles_m = static_cast<long long>(N) * (g.Ho / R);
+    if (tiles_m * tn > 0x7FFFFFFFLL) return -1;
 
     ConvWinArgs a;
     a.x = g.x;
@@ -427,28 +385,20 @@ int launch_conv_window(const ConvGeom& g, const int8_t* w, const GemmEpilogue& e
     a.nqw = static_cast<int>(nqw);
     a.win_bytes = static_cast<int>(nqw) * 4 * 1024;
     a.R = R;
-    a.R2 = R2;
-    a.RG = R + R2;
-    a.gpi = g.Ho / (R + R2);
-    a.n1 = static_cast<int>(N * static_cast<long long>(g.Ho / (R + R2)) * tn);
-    a.tiles_m = N * (g.Ho / (R + R2));
+    a.tiles_h = g.Ho / R;
+    a.tiles_m = static_cast<int>(tiles_m);
     a.tiles_n = tn;
-    const unsigned grid = static_cast<unsigned>(R2 > 0 ? 2 * a.n1 : a.n1);
+    const unsigned grid = static_cast<unsigned>(tiles_m * tn);
     const int l = static_cast<int>(lds);
     const bool o16 = ep.c16 != nullptr;
-    if (R2 > 0) {
-        note_route(NI == 8 ? "conv-window256+224" : "conv-window224+192");
-        if (NI == 8) return o16 ? launch_win<8, 7, 2, true>(a, grid, l, s) : launch_win<8, 7, 2, false>(a, grid, l, s);
-        return o16 ? launch_win<7, 6, 2, true>(a, grid, l, s) : launch_win<7, 6, 2, false>(a, grid, l, s);
-    }
     note_route(NI == 8 ? (slots == 2 ? "conv-window256" : "conv-window256 ring3")
                        : (slots == 2 ? "conv-window224" : "conv-window224 ring3"));
     if (slots == 2) {
-        if (NI == 8) return o16 ? launch_win<8, 0, 2, true>(a, grid, l, s) : launch_win<8, 0, 2, false>(a, grid, l, s);
-        return o16 ? launch_win<7, 0, 2, true>(a, grid, l, s) : launch_win<7, 0, 2, false>(a, grid, l, s);
+        if (NI == 8) return o16 ? launch_win<8, 2, true>(a, grid, l, s) : launch_win<8, 2, false>(a, grid, l, s);
+        return o16 ? launch_win<7, 2, true>(a, grid, l, s) : launch_win<7, 2, false>(a, grid, l, s);
     }
-    if (NI == 8) return o16 ? launch_win<8, 0, 3, true>(a, grid, l, s) : launch_win<8, 0, 3, false>(a, grid, l, s);
-    return o16 ? launch_win<7, 0, 3, true>(a, grid, l, s) : launch_win<7, 0, 3, false>(a, grid, l, s);
+    if (NI == 8) return o16 ? launch_win<8, 3, true>(a, grid, l, s) : launch_win<8, 3, false>(a, grid, l, s);
+    return o16 ? launch_win<7, 3, true>(a, grid, l, s) : launch_win<7, 3, false>(a, grid, l, s);
 }
 
 }  // namespace forge_amd

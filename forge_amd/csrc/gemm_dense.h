@@ -91,7 +91,7 @@ int launch_sparse_wide_s32(const int8_t* W_comp, const int8_t* x, const uint32_t
 
 // NHWC conv, stride 1, C % 128 == 0, Co % 256 == 0, on the window-fed tile (conv_window.hip):
 // returns -1 when the shape is not one it takes.
-int launch_conv_window(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep, int Co, int cu, hipStream_t s);
+int launch_conv_window(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep, int Co, hipStream_t s);
 
 // Implicit-GEMM NHWC conv through the dense tile engine (conv.hip supplies the geometry).
 int launch_conv_gemm(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep, int Co, bool vec,

@@ -312,10 +312,7 @@ int launch_conv_gemm(const ConvGeom& g, const int8_t* w, const GemmEpilogue& ep,
 {
     const int M = g.rows, K = g.K;
     if (vec) {
-        int st = FORGE_OK;
-        const int cu = cu_count(&st);
-        if (st != FORGE_OK) return st;
-        const int r = launch_conv_window(g, w, ep, Co, cu, s);
+        const int r = launch_conv_window(g, w, ep, Co, s);
         if (r != -1) return r;
     }
     // DMA engine when every 128-deep stage of a patch row is one pixel's contiguous channels
