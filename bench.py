@@ -197,7 +197,7 @@ PROBE_KERNELS = {
     "c2_gemm": ("gemm_dma_kernel<256, 256, true, forge_amd::DmaRowMajor>",),
     "c3_sparse": ("sparse_wide_s32_kernel", "sparse_dma32_tail_kernel<false,", "sparse_dma32_kernel<false,"),
     "c3_dense": ("gemm_dma_coltail_kernel<false>", "gemm_dma_kernel<256, 256, false, forge_amd::DmaRowMajor>"),
-    "c5_conv": ("gemm_dma_tail_kernel<false, forge_amd::DmaConv>",),
+    "c5_conv": ("conv_window_kernel<7, 2, false>",),
     "c4_dense_M16": ("decode_dense_kernel<true",),
     "c4_sparse_M16": ("decode_sparse_reg_kernel<true",),
     "f1_fq": ("sparse_fq_kernel<5, 48, true",),
@@ -329,7 +329,7 @@ PROBE_TITLES = {
     "c2_gemm": "configs[1] GEMM 4096^3, FP16 out (`gemm_dma_kernel<256,256,true>`)",
     "c3_sparse": "configs[2] 2:4 sparse 4096x11008x4096, INT32 out (`sparse_wide_s32_kernel`: 256 tokens x 320-352 weight rows per tile, 2 tiles per CU)",
     "c3_dense": "configs[2] shape dense, INT32 out (`gemm_dma_coltail_kernel<false>`: 256- and 192-row tiles, one launch)",
-    "c5_conv": "configs[4] NHWC conv, INT32 out (`gemm_dma_tail_kernel<false,DmaConv>`: 256- and 192-row tiles, one launch)",
+    "c5_conv": "configs[4] NHWC conv, INT32 out (`conv_window_kernel<7,2,false>`: 224-pixel x 256-channel tiles, input window in LDS once per channel chunk)",
     "c4_dense_M16": "configs[3] M=16 dense decode GEMM (`decode_dense_kernel`)",
     "c4_sparse_M16": "configs[3] M=16 2:4 decode GEMM (`decode_sparse_reg_kernel`)",
     "f1_fq": "fused quantize + 2:4 sparse linear 1280->320 at M=147,456 (`sparse_fq_kernel<5,48,true,3>`)",
