@@ -80,6 +80,7 @@ def test_conv_dma_gather(dev, orc, N, H, W, C, Co, k, pad, stride, dil, check):
     (2, 17, 33, 128, 256, 2, 0, (1, 1), "conv-window256"),       # odd tap reach: padded window rows
     (1, 4, 56, 128, 256, 3, 1, (1, 1), "conv-window224"),
     (2, 64, 64, 256, 256, 3, 1, (1, 1), "conv-window256 ring3"),  # two windows do not fit
+    (1, 8, 56, 512, 768, 3, 1, (1, 1), "conv-window224"),         # 4 channel chunks, 3 column tiles
 ])
 def test_conv_window(dev, orc, N, H, W, C, Co, k, pad, dil, route):
     import torch
