@@ -81,6 +81,7 @@ def test_conv_dma_gather(dev, orc, N, H, W, C, Co, k, pad, stride, dil, check):
     (1, 4, 56, 128, 256, 3, 1, (1, 1), "conv-window224"),
     (2, 64, 64, 256, 256, 3, 1, (1, 1), "conv-window256 ring3"),  # two windows do not fit
     (1, 8, 56, 512, 768, 3, 1, (1, 1), "conv-window224"),         # 4 channel chunks, 3 column tiles
+    (1, 16, 28, 128, 256, 3, 2, (2, 2), "conv-window224"),        # dilation 2 on both axes
 ])
 def test_conv_window(dev, orc, N, H, W, C, Co, k, pad, dil, route):
     import torch
