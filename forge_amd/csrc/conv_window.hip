@@ -85,8 +85,8 @@ __global__ __launch_bounds__(kGemmThreads) void conv_window_kernel(ConvWinArgs a
     const int m0 = (img * a.Ho + ho0) * a.Wo;  // pixel index of the tile's first pixel
     const int h0 = ho0 - a.padH;               // input row of window row 0
 
-    // FP16 out: the rows' activation scales are loaded first, so that no load waits behind the
-    // epilogue's stores (vector-memory operations complete in issue order).
+    // FP16 out: the rows' activation scales are loaded first: a load issued after the epilogue's
+    // stores would be waited for together with them (one counter covers both).
     [[maybe_unused]] float asv[NI];
     if constexpr (DEQUANT) {
 #pragma unroll
